@@ -1,0 +1,88 @@
+// Library-wide C ABI pieces: version, thread-local error text, device queries,
+// and key derivation for the executor's sampled route.
+#include <mutex>
+#include <string.h>
+
+#include "nvjsel_device.h"
+#include "nvjsel_host.h"
+
+namespace nvjsel {
+
+static thread_local char g_last_error[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_last_error[0] = '\0'; }
+
+int device_cu_count() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+size_t device_max_lds_per_block() {
+  static std::mutex mu;
+  static size_t cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || n <= 0)
+      n = 64 * 1024;
+    cached[dev] = (size_t)n;
+  }
+  return cached[dev];
+}
+
+// keys[b] = fold_in(fold_in((0,0), slot), counter); fold_in(k, d) = threefry2x32(k, (0, d)).
+__global__ void derive_keys_kernel(const int32_t* __restrict__ slots,
+                                   const int32_t* __restrict__ counters, int batch,
+                                   uint32_t* __restrict__ keys, int32_t* __restrict__ counters_out) {
+  int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  int32_t slot = slots[b];
+  if (slot < 0) slot = 0;
+  uint32_t a0, a1, c0, c1;
+  threefry2x32(tf_key(0u, 0u), 0u, (uint32_t)slot, a0, a1);
+  int32_t ctr = counters[b];
+  threefry2x32(tf_key(a0, a1), 0u, (uint32_t)ctr, c0, c1);
+  keys[2 * b] = c0;
+  keys[2 * b + 1] = c1;
+  if (counters_out) counters_out[b] = ctr + 1;
+}
+
+}  // namespace nvjsel
+
+using namespace nvjsel;
+
+extern "C" int nvjsel_abi_version(void) { return NVJSEL_ABI_VERSION; }
+
+extern "C" const char* nvjsel_last_error(void) { return g_last_error; }
+
+extern "C" int nvjsel_derive_keys(const int32_t* slots, const int32_t* counters, int batch,
+                                  uint32_t* keys, int32_t* counters_out, void* stream) {
+  clear_error();
+  if (batch <= 0) return fail(NVJSEL_EINVAL, "derive_keys: batch must be positive");
+  if (!slots || !counters || !keys) return fail(NVJSEL_EINVAL, "derive_keys: null pointer");
+  int threads = 256;
+  int blocks = (batch + threads - 1) / threads;
+  hipLaunchKernelGGL(derive_keys_kernel, dim3(blocks), dim3(threads), 0, (hipStream_t)stream,
+                     slots, counters, batch, keys, counters_out);
+  NVJSEL_CHECK_LAUNCH("derive_keys_kernel");
+  return NVJSEL_OK;
+}

@@ -1,0 +1,476 @@
+// LM-head projection fused with greedy top-1 or Gumbel-max sampling (gfx950).
+//
+// Replaces nanovllm_jax/kernels/lm_head_triton.py:22-186 (two-stage Triton
+// top-1) and the dense dot + argmax / categorical of nanovllm_jax/model.py:
+// 806-830, 894, 901-938.  Logits are never written to memory.
+//
+// Hot path (weight [V,H] bf16, hidden bf16 or f32): one pass over W.
+//   * Matrix cores: v_mfma_f32_16x16x32_bf16 with M = 16 vocabulary rows,
+//     N = 16 batch rows, K = 32.  Lane l loads 16 contiguous bytes of vocab row
+//     (l % 16) straight from HBM into its A operand (group g = l / 16 takes
+//     k = 8g..8g+7 of each 32-wide step), so W is read once with 128-bit loads
+//     and never staged.  B operands (hidden) are staged once per block in LDS
+//     in fragment order, so each lane's ds_read_b128 is contiguous across the
+//     16 lanes that share a k group.
+//   * An f32 hidden is split exactly into three bf16 terms (hi + mid + lo =
+//     h); bf16 x bf16 products are exact in fp32, so the three MFMAs give an
+//     fp32-accurate dot while W stays bf16 and is still read once.
+//   * Epilogue per 16x16 tile: optional bf16/f16 rounding of the logit
+//     (REDUCE_CAST), optional temperature division + Threefry Gumbel noise at
+//     the vocabulary index, then a running max of 64-bit (value, ~index) keys.
+//   * Cross-block reduce: one 64-bit atomicMax per (block, row) into the
+//     workspace, then the last block to finish (ticket counter) writes the ids
+//     and re-zeroes the workspace -- a single launch per call.
+// Any other dtype/layout/shape goes through a generic VALU kernel with the same
+// reduction and epilogue.
+#include "nvjsel_device.h"
+#include "nvjsel_host.h"
+
+namespace nvjsel {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+enum { MODE_GREEDY = 0, MODE_SAMPLE = 1 };
+
+struct LmArgs {
+  const void* W;
+  const void* hidden;
+  int hidden_dtype;
+  int weight_dtype;
+  int layout;
+  int B;  // rows handled by this launch
+  int H;
+  int V;
+  int reduce_cast;
+  const float* temperature;  // MODE_SAMPLE, offset to this launch's first row
+  const uint32_t* keys;      // MODE_SAMPLE, [B,2]
+  unsigned long long* row_keys;
+  unsigned int* counter;
+  int32_t* out_ids;
+  float* out_best;
+};
+
+template <int WT>
+__device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  if constexpr (WT == DT_BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ float apply_cast(float v, int rc) {
+  if (rc == 1) return round_bf16(v);
+  if (rc == 2) return round_f16(v);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t bf16_bits_rne(float v) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ uint32_t f16_bits(float v) {
+  _Float16 h = (_Float16)v;
+  uint16_t b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
+
+// Last block to arrive converts the per-row keys into ids and re-zeroes the
+// accumulators and the ticket counter for the next call.
+__device__ __forceinline__ void finish_rows(unsigned long long* row_keys, unsigned int* counter,
+                                            int B, int32_t* out_ids, float* out_best) {
+  __shared__ int s_last;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned int t = atomicAdd(counter, 1u);
+    s_last = (t == gridDim.x - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    unsigned long long k =
+        __hip_atomic_load(&row_keys[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    out_ids[b] = (int32_t)(~(uint32_t)k);
+    if (out_best) out_best[b] = unord_f32((uint32_t)(k >> 32));
+    __hip_atomic_store(&row_keys[b], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Block-wide max of per-(wave, row) keys held in LDS, then one atomic per row.
+template <int WAVES, int BP>
+__device__ __forceinline__ void block_commit(unsigned long long* red, int B,
+                                             unsigned long long* row_keys) {
+  __syncthreads();
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    unsigned long long m = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) m = max_u64(m, red[w * BP + b]);
+    if (m) atomicMax(&row_keys[b], m);
+  }
+}
+
+// ------------------------------------------------------------------ MFMA kernel
+// WT: weight element type (DT_BF16 / DT_F16).  NSPLIT: hidden terms (1, or 3
+// for an exact f32 hidden on bf16 weights).  NB: 16-row batch tiles.  MT:
+// 16-row vocab tiles per wave.  KU: k-steps (32 each) per prefetch chunk.
+template <int WT, int NSPLIT, int NB, int MT, int WAVES, int MODE>
+__global__ void __launch_bounds__(WAVES * 64)
+lm_head_mfma_kernel(LmArgs a) {
+  constexpr int BP = NB * 16;
+  constexpr int KU = 4;
+  extern __shared__ u32x4_t lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 4;
+  const int r = lane & 15;
+  const int H = a.H, V = a.V, B = a.B;
+  const int KQ = H >> 3;  // 8-element groups per row
+
+  // ---- stage hidden [B, H] into LDS fragments: lds[(kq * NSPLIT + s) * BP + n]
+  for (int f = tid; f < KQ * BP; f += WAVES * 64) {
+    const int n = f % BP;
+    const int kq = f / BP;
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      v[j] = (n < B) ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)n * H + kq * 8 + j) : 0.0f;
+#pragma unroll
+    for (int s = 0; s < NSPLIT; ++s) {
+      uint32_t bits[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if constexpr (WT == DT_BF16) {
+          bits[j] = bf16_bits_rne(v[j]);
+          v[j] = v[j] - __uint_as_float(bits[j] << 16);
+        } else {
+          bits[j] = f16_bits(v[j]);
+        }
+      }
+      u32x4_t p;
+      p.x = bits[0] | (bits[1] << 16);
+      p.y = bits[2] | (bits[3] << 16);
+      p.z = bits[4] | (bits[5] << 16);
+      p.w = bits[6] | (bits[7] << 16);
+      lds[(kq * NSPLIT + s) * BP + n] = p;
+    }
+  }
+  __syncthreads();
+
+  float tp[NB];
+  bool greedy_row[NB];
+  TfKey key[NB];
+  if constexpr (MODE == MODE_SAMPLE) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int b = nb * 16 + r;
+      float t = (b < B) ? a.temperature[b] : 0.0f;
+      greedy_row[nb] = (t <= 0.0f);
+      tp[nb] = temp_floor(t);
+      key[nb] = (b < B) ? tf_key(a.keys[2 * b], a.keys[2 * b + 1]) : tf_key(0u, 0u);
+    }
+  }
+
+  unsigned long long best[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) best[nb] = 0;
+
+  const int ksteps = H >> 5;
+  const int nch = ksteps / KU;
+  constexpr int ROWS = 16 * MT;
+  const int ntiles = (V + ROWS - 1) / ROWS;
+  const uint16_t* W = (const uint16_t*)a.W;
+
+  for (int tile = blockIdx.x * WAVES + wave; tile < ntiles; tile += gridDim.x * WAVES) {
+    const int v0 = tile * ROWS;
+    const u32x4_t* wp[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      int row = v0 + t * 16 + r;
+      row = row < V ? row : V - 1;
+      wp[t] = (const u32x4_t*)(W + (size_t)row * H) + g;
+    }
+    f32x4_t acc[MT][NB];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[t][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    u32x4_t A0[KU][MT], A1[KU][MT];
+    auto load_chunk = [&](u32x4_t(&A)[KU][MT], int c) {
+#pragma unroll
+      for (int u = 0; u < KU; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) A[u][t] = __builtin_nontemporal_load(wp[t] + (c * KU + u) * 4);
+    };
+    auto step = [&](const u32x4_t(&At)[MT], int kb) {
+#pragma unroll
+      for (int s = 0; s < NSPLIT; ++s)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const u32x4_t bfr = lds[((kb * 4 + g) * NSPLIT + s) * BP + nb * 16 + r];
+#pragma unroll
+          for (int t = 0; t < MT; ++t) acc[t][nb] = mfma16x16x32<WT>(At[t], bfr, acc[t][nb]);
+        }
+    };
+    auto comp_chunk = [&](u32x4_t(&A)[KU][MT], int c) {
+#pragma unroll
+      for (int u = 0; u < KU; ++u) step(A[u], c * KU + u);
+    };
+
+    if (nch > 0) load_chunk(A0, 0);
+    for (int c = 0; c < nch; c += 2) {
+      if (c + 1 < nch) load_chunk(A1, c + 1);
+      comp_chunk(A0, c);
+      if (c + 1 < nch) {
+        if (c + 2 < nch) load_chunk(A0, c + 2);
+        comp_chunk(A1, c + 1);
+      }
+    }
+    for (int kb = nch * KU; kb < ksteps; ++kb) {
+      u32x4_t At[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) At[t] = __builtin_nontemporal_load(wp[t] + kb * 4);
+      step(At, kb);
+    }
+
+    // ---- epilogue: D[row = 4g + i][col = r] of each 16x16 tile
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int b = nb * 16 + r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int v = v0 + t * 16 + g * 4 + i;
+          if (v < V && b < B) {
+            float val = apply_cast(acc[t][nb][i], a.reduce_cast);
+            if constexpr (MODE == MODE_SAMPLE) {
+              if (!greedy_row[nb]) val = val / tp[nb] + gumbel_at(key[nb], (uint32_t)v);
+            }
+            best[nb] = max_u64(best[nb], argmax_key(val, (uint32_t)v));
+          }
+        }
+      }
+  }
+
+  // ---- reduce the four k-groups, then the waves, then across blocks
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    best[nb] = max_u64(best[nb], shfl_xor_u64(best[nb], 16));
+    best[nb] = max_u64(best[nb], shfl_xor_u64(best[nb], 32));
+  }
+  __syncthreads();  // hidden fragments are dead from here on
+  unsigned long long* red = (unsigned long long*)lds;
+  if (g == 0) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) red[wave * BP + nb * 16 + r] = best[nb];
+  }
+  block_commit<WAVES, BP>(red, B, a.row_keys);
+  finish_rows(a.row_keys, a.counter, B, a.out_ids, a.out_best);
+}
+
+// ------------------------------------------------------------------ generic kernel
+// One vocabulary entry per thread, every batch row, any dtype/layout.
+template <int MODE>
+__global__ void __launch_bounds__(256) lm_head_generic_kernel(LmArgs a) {
+  __shared__ unsigned long long red[4 * 64];
+  const int v = blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int b0 = 0; b0 < a.B; b0 += 64) {
+    const int nb = min(64, a.B - b0);
+    for (int bb = 0; bb < nb; ++bb) {
+      const int b = b0 + bb;
+      unsigned long long k = 0;
+      if (v < a.V) {
+        float acc = 0.0f;
+        for (int kk = 0; kk < a.H; ++kk) {
+          size_t wi = (a.layout == NVJSEL_W_VH) ? (size_t)v * a.H + kk : (size_t)kk * a.V + v;
+          acc = fmaf(load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * a.H + kk),
+                     load_as_f32(a.W, a.weight_dtype, wi), acc);
+        }
+        float val = apply_cast(acc, a.reduce_cast);
+        if constexpr (MODE == MODE_SAMPLE) {
+          float t = a.temperature[b];
+          if (!(t <= 0.0f))
+            val = val / temp_floor(t) + gumbel_at(tf_key(a.keys[2 * b], a.keys[2 * b + 1]), (uint32_t)v);
+        }
+        k = argmax_key(val, (uint32_t)v);
+      }
+      k = wave_max_u64(k);
+      if (lane == 0) red[wave * 64 + bb] = k;
+    }
+    __syncthreads();
+    for (int bb = threadIdx.x; bb < nb; bb += blockDim.x) {
+      unsigned long long m = 0;
+      for (int w = 0; w < 4; ++w) m = max_u64(m, red[w * 64 + bb]);
+      if (m) atomicMax(&a.row_keys[b0 + bb], m);
+    }
+    __syncthreads();
+  }
+  finish_rows(a.row_keys, a.counter, a.B, a.out_ids, a.out_best);
+}
+
+// ------------------------------------------------------------------ host side
+static constexpr int kWaves = 8;
+// LDS reserved for the kernel's static shared variables (finish_rows flag).
+static constexpr size_t kStaticLdsSlack = 256;
+
+template <int WT, int NSPLIT, int NB, int MODE>
+static int launch_mfma(const LmArgs& a, hipStream_t stream) {
+  constexpr int MT = (NB == 1) ? 4 : 2;
+  auto kern = lm_head_mfma_kernel<WT, NSPLIT, NB, MT, kWaves, MODE>;
+  size_t lds = (size_t)a.H * NSPLIT * NB * 16 * 2;
+  size_t red = (size_t)kWaves * NB * 16 * 8;
+  if (lds < red) lds = red;
+  if (lds > 64 * 1024) {
+    NVJSEL_CHECK_HIP(hipFuncSetAttribute((const void*)kern,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  }
+  int per_cu = 0;
+  NVJSEL_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kWaves * 64, lds));
+  if (per_cu < 1) per_cu = 1;
+  const int rows = 16 * MT * kWaves;
+  const int need = (a.V + rows - 1) / rows;
+  int grid = per_cu * device_cu_count();
+  if (grid > need) grid = need;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kWaves * 64), lds, stream, a);
+  NVJSEL_CHECK_LAUNCH("lm_head_mfma_kernel");
+  return NVJSEL_OK;
+}
+
+template <int WT, int NSPLIT, int MODE>
+static int dispatch_nb(const LmArgs& a, hipStream_t s) {
+  const int nb = (a.B + 15) / 16;
+  switch (nb) {
+    case 1: return launch_mfma<WT, NSPLIT, 1, MODE>(a, s);
+    case 2: return launch_mfma<WT, NSPLIT, 2, MODE>(a, s);
+    case 3: return launch_mfma<WT, NSPLIT, 3, MODE>(a, s);
+    default: return launch_mfma<WT, NSPLIT, 4, MODE>(a, s);
+  }
+}
+
+static size_t lm_ws_keys_bytes(int batch) { return align_up((size_t)batch * 8, 256); }
+
+static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const void* weight,
+                         int weight_dtype, int layout, int batch, int H, int V, int reduce_cast,
+                         const float* temperature, const uint32_t* keys, int32_t* out_ids,
+                         float* out_best, void* workspace, size_t ws_bytes, void* stream) {
+  clear_error();
+  const char* who = mode == MODE_GREEDY ? "lm_head_top1" : "lm_head_sample";
+  if (!hidden || !weight || !out_ids) { set_error("%s: null hidden/weight/out_ids", who); return NVJSEL_EINVAL; }
+  if (batch <= 0 || H <= 0 || V <= 0) {
+    set_error("%s requires non-empty dimensions (batch=%d hidden=%d vocab=%d)", who, batch, H, V);
+    return NVJSEL_EINVAL;
+  }
+  if (V >= 0x7FFFFFFF) { set_error("%s: vocab too large", who); return NVJSEL_EINVAL; }
+  if (!valid_dtype(hidden_dtype) || !valid_dtype(weight_dtype)) {
+    set_error("%s: unsupported dtype (hidden=%d weight=%d)", who, hidden_dtype, weight_dtype);
+    return NVJSEL_EINVAL;
+  }
+  if (layout != NVJSEL_W_VH && layout != NVJSEL_W_HV) { set_error("%s: bad weight layout %d", who, layout); return NVJSEL_EINVAL; }
+  if (reduce_cast < 0 || reduce_cast > 2) { set_error("%s: reduce_cast must be 0, 1 or 2", who); return NVJSEL_EINVAL; }
+  if (mode == MODE_SAMPLE && (!temperature || !keys)) { set_error("%s: null temperature/keys", who); return NVJSEL_EINVAL; }
+  if (!workspace || ws_bytes < nvjsel_lm_head_workspace_size(batch)) {
+    set_error("%s: workspace %zu bytes < required %zu", who, ws_bytes, nvjsel_lm_head_workspace_size(batch));
+    return NVJSEL_EWORKSPACE;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  unsigned long long* row_keys = (unsigned long long*)workspace;
+  unsigned int* counter = (unsigned int*)((char*)workspace + lm_ws_keys_bytes(batch));
+
+  const bool aligned = (((uintptr_t)weight) & 15) == 0;
+  const bool bf16_mfma = layout == NVJSEL_W_VH && weight_dtype == NVJSEL_BF16 && (H % 32) == 0 && aligned;
+  const bool f16_mfma = layout == NVJSEL_W_VH && weight_dtype == NVJSEL_F16 &&
+                        hidden_dtype == NVJSEL_F16 && (H % 32) == 0 && aligned;
+  const int nsplit = (bf16_mfma && hidden_dtype != NVJSEL_BF16) ? 3 : 1;
+  // rows per launch: LDS holds H * nsplit * rows bf16 values
+  int chunk = 0;
+  if ((bf16_mfma || f16_mfma) && (size_t)H * nsplit * 16 * 2 + kStaticLdsSlack <= device_max_lds_per_block()) {
+    size_t per16 = (size_t)H * nsplit * 16 * 2;
+    size_t max_lds = device_max_lds_per_block();
+    max_lds = max_lds > kStaticLdsSlack ? max_lds - kStaticLdsSlack : 0;
+    int tiles = (int)(max_lds / per16);
+    if (tiles > 4) tiles = 4;
+    if (nsplit == 3 && tiles > 1) tiles = 1;
+    chunk = tiles * 16;
+  }
+  for (int b0 = 0; b0 < batch; b0 += (chunk > 0 ? chunk : batch)) {
+    LmArgs a;
+    const int nb = chunk > 0 ? (batch - b0 < chunk ? batch - b0 : chunk) : batch;
+    a.W = weight;
+    a.hidden = (const char*)hidden + (size_t)b0 * H * dtype_size(hidden_dtype);
+    a.hidden_dtype = hidden_dtype;
+    a.weight_dtype = weight_dtype;
+    a.layout = layout;
+    a.B = nb;
+    a.H = H;
+    a.V = V;
+    a.reduce_cast = reduce_cast;
+    a.temperature = temperature ? temperature + b0 : nullptr;
+    a.keys = keys ? keys + 2 * (size_t)b0 : nullptr;
+    a.row_keys = row_keys + b0;
+    a.counter = counter;
+    a.out_ids = out_ids + b0;
+    a.out_best = out_best ? out_best + b0 : nullptr;
+    int rc;
+    if (chunk > 0) {
+      if (f16_mfma)
+        rc = mode == MODE_GREEDY ? dispatch_nb<DT_F16, 1, MODE_GREEDY>(a, s) : dispatch_nb<DT_F16, 1, MODE_SAMPLE>(a, s);
+      else if (nsplit == 1)
+        rc = mode == MODE_GREEDY ? dispatch_nb<DT_BF16, 1, MODE_GREEDY>(a, s) : dispatch_nb<DT_BF16, 1, MODE_SAMPLE>(a, s);
+      else
+        rc = mode == MODE_GREEDY ? launch_mfma<DT_BF16, 3, 1, MODE_GREEDY>(a, s)
+                                 : launch_mfma<DT_BF16, 3, 1, MODE_SAMPLE>(a, s);
+    } else {
+      const int grid = (V + 255) / 256;
+      if (mode == MODE_GREEDY)
+        hipLaunchKernelGGL(lm_head_generic_kernel<MODE_GREEDY>, dim3(grid), dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL(lm_head_generic_kernel<MODE_SAMPLE>, dim3(grid), dim3(256), 0, s, a);
+      NVJSEL_CHECK_LAUNCH("lm_head_generic_kernel");
+      rc = NVJSEL_OK;
+    }
+    if (rc != NVJSEL_OK) return rc;
+  }
+  return NVJSEL_OK;
+}
+
+}  // namespace nvjsel
+
+using namespace nvjsel;
+
+extern "C" size_t nvjsel_lm_head_workspace_size(int batch) {
+  if (batch <= 0) return 0;
+  return lm_ws_keys_bytes(batch) + 256;
+}
+
+extern "C" int nvjsel_lm_head_top1(const void* hidden, int hidden_dtype, const void* weight,
+                                   int weight_dtype, int weight_layout, int batch, int hidden_dim,
+                                   int vocab, int reduce_cast, int32_t* out_ids, float* out_best,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  return lm_head_entry(MODE_GREEDY, hidden, hidden_dtype, weight, weight_dtype, weight_layout, batch,
+                       hidden_dim, vocab, reduce_cast, nullptr, nullptr, out_ids, out_best, workspace,
+                       workspace_bytes, stream);
+}
+
+extern "C" int nvjsel_lm_head_sample(const void* hidden, int hidden_dtype, const void* weight,
+                                     int weight_dtype, int weight_layout, int batch, int hidden_dim,
+                                     int vocab, int reduce_cast, const float* temperature,
+                                     const uint32_t* keys, int32_t* out_ids, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  return lm_head_entry(MODE_SAMPLE, hidden, hidden_dtype, weight, weight_dtype, weight_layout, batch,
+                       hidden_dim, vocab, reduce_cast, temperature, keys, out_ids, nullptr, workspace,
+                       workspace_bytes, stream);
+}

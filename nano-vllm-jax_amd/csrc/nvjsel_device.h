@@ -1,0 +1,157 @@
+// Device-side building blocks shared by the LM-head and sampler kernels (gfx950).
+//
+//  * Threefry-2x32-20 and the JAX float/Gumbel construction on top of it, so a
+//    kernel can draw the exact noise `jax.random.categorical` would add at any
+//    vocabulary index without materialising it
+//    (reference use: nanovllm_jax/model.py:929-936; key derivation
+//    nanovllm_jax/engine/model_executor.py:2131, 2214-2219).
+//  * The 64-bit argmax key: (orderable float << 32) | ~index.  A plain unsigned
+//    max over keys gives the maximum value and, among equal values, the lowest
+//    index -- the tie rule of nanovllm_jax/kernels/lm_head_triton.py:66-75 and
+//    99-102 and of jnp.argmax (model.py:819, 894).  NaN is canonicalised to the
+//    largest key (first NaN wins, as jnp.argmax) and -0.0 to +0.0 (they compare
+//    equal, so the lower index must win).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nvjsel {
+
+// ---------------------------------------------------------------- Threefry-2x32-20
+__device__ __forceinline__ uint32_t rotl32(uint32_t v, int r) {
+  return __builtin_rotateleft32(v, (uint32_t)r);
+}
+
+struct TfKey {
+  uint32_t k0, k1, k2;
+};
+
+__device__ __forceinline__ TfKey tf_key(uint32_t k0, uint32_t k1) {
+  return TfKey{k0, k1, k0 ^ k1 ^ 0x1BD11BDAu};
+}
+
+#define NVJSEL_TF_ROUND(r) \
+  do { x0 += x1; x1 = rotl32(x1, r); x1 ^= x0; } while (0)
+
+__device__ __forceinline__ void threefry2x32(const TfKey& k, uint32_t c0, uint32_t c1,
+                                             uint32_t& o0, uint32_t& o1) {
+  uint32_t x0 = c0 + k.k0, x1 = c1 + k.k1;
+  NVJSEL_TF_ROUND(13); NVJSEL_TF_ROUND(15); NVJSEL_TF_ROUND(26); NVJSEL_TF_ROUND(6);
+  x0 += k.k1; x1 += k.k2 + 1u;
+  NVJSEL_TF_ROUND(17); NVJSEL_TF_ROUND(29); NVJSEL_TF_ROUND(16); NVJSEL_TF_ROUND(24);
+  x0 += k.k2; x1 += k.k0 + 2u;
+  NVJSEL_TF_ROUND(13); NVJSEL_TF_ROUND(15); NVJSEL_TF_ROUND(26); NVJSEL_TF_ROUND(6);
+  x0 += k.k0; x1 += k.k1 + 3u;
+  NVJSEL_TF_ROUND(17); NVJSEL_TF_ROUND(29); NVJSEL_TF_ROUND(16); NVJSEL_TF_ROUND(24);
+  x0 += k.k1; x1 += k.k2 + 4u;
+  NVJSEL_TF_ROUND(13); NVJSEL_TF_ROUND(15); NVJSEL_TF_ROUND(26); NVJSEL_TF_ROUND(6);
+  x0 += k.k2; x1 += k.k0 + 5u;
+  o0 = x0; o1 = x1;
+}
+#undef NVJSEL_TF_ROUND
+
+// random_bits(key, 32, shape)[i] in JAX's partitionable layout: counter (hi, lo) of i.
+__device__ __forceinline__ uint32_t random_bits32(const TfKey& k, uint32_t i) {
+  uint32_t o0, o1;
+  threefry2x32(k, 0u, i, o0, o1);
+  return o0 ^ o1;
+}
+
+// gumbel(key)[i], mode "low": -log(-log(max(tiny, f*(1-tiny)+tiny))), f in [0,1)
+// from the top 23 bits.  (1-tiny) rounds to 1 in fp32, so u = f, or tiny when
+// f == 0.  Each log is evaluated in fp64 and rounded once: a correctly rounded
+// fp32 log.
+__device__ __forceinline__ float gumbel_from_bits(uint32_t bits) {
+  float f = __uint_as_float((bits >> 9) | 0x3F800000u) - 1.0f;
+  float u = fmaxf(f + 1.17549435e-38f, 1.17549435e-38f);
+  float l1 = (float)log((double)u);
+  float l2 = (float)log((double)(-l1));
+  return -l2;
+}
+
+__device__ __forceinline__ float gumbel_at(const TfKey& k, uint32_t i) {
+  return gumbel_from_bits(random_bits32(k, i));
+}
+
+// ---------------------------------------------------------------- argmax keys
+__device__ __forceinline__ uint32_t ord_f32(float v) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) u = 0x7FFFFFFFu;  // any NaN -> +NaN (largest)
+  if (u == 0x80000000u) u = 0u;                           // -0.0 -> +0.0
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float unord_f32(uint32_t o) {
+  uint32_t u = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+  return __uint_as_float(u);
+}
+
+// Orderable key of a value without NaN/-0 canonicalisation, for radix selection
+// over finite values (monotone non-decreasing in the value).
+__device__ __forceinline__ uint32_t radix_key(float v) {
+  uint32_t u = __float_as_uint(v);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+  return ((uint64_t)ord_f32(v) << 32) | (uint64_t)(~idx);
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  lo = __shfl_xor(lo, m, 64);
+  hi = __shfl_xor(hi, m, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = max_u64(v, shfl_xor_u64(v, m));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) { uint32_t o = __shfl_xor(v, m, 64); v = v > o ? v : o; }
+  return v;
+}
+
+// ---------------------------------------------------------------- number formats
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// fp32 -> bf16 -> fp32 with round-to-nearest-even (NaN kept NaN).
+__device__ __forceinline__ float round_bf16(float v) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return v;
+  u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+  return __uint_as_float(u);
+}
+
+__device__ __forceinline__ float round_f16(float v) { return (float)(_Float16)v; }
+
+__device__ __forceinline__ float f16_to_f32(uint16_t b) {
+  _Float16 h;
+  __builtin_memcpy(&h, &b, 2);
+  return (float)h;
+}
+
+// Element types, as the C ABI numbers them.
+enum { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
+
+__host__ __device__ __forceinline__ size_t dtype_size_dev(int dtype) { return dtype == DT_F32 ? 4 : 2; }
+
+__device__ __forceinline__ float load_as_f32(const void* p, int dtype, size_t i) {
+  if (dtype == DT_F32) return ((const float*)p)[i];
+  if (dtype == DT_BF16) return bf16_to_f32(((const uint16_t*)p)[i]);
+  return f16_to_f32(((const uint16_t*)p)[i]);
+}
+
+// JAX's jnp.maximum(T, 1e-6) propagates NaN (fmaxf would not).
+__device__ __forceinline__ float temp_floor(float t) {
+  return (t != t) ? t : fmaxf(t, 1e-6f);
+}
+
+}  // namespace nvjsel

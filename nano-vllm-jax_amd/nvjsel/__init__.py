@@ -1,0 +1,35 @@
+"""nvjsel -- MI355X-native decode-step token selection (LM-head top-1 + sampler).
+
+Import with ``nano-vllm-jax_amd`` on ``sys.path`` (the repo-root entry points
+and tests do this).  The compute lives in ``libnvjsel.so`` (HIP, gfx950); see
+``include/nvjsel.h`` for the C ABI.
+"""
+from ._lib import NativeLibraryMissing, NvjselError, load
+from .registry import (
+    KernelBackendUnavailable,
+    available_backends,
+    lm_head_greedy_top1_impl,
+    select_token_selection_backend,
+)
+from .selection import (
+    derive_rng_keys,
+    lm_head_greedy_top1_hip,
+    lm_head_sample_token_ids,
+    reference_reduce_cast,
+    sample_token_ids,
+)
+
+__all__ = [
+    "NativeLibraryMissing",
+    "NvjselError",
+    "KernelBackendUnavailable",
+    "available_backends",
+    "derive_rng_keys",
+    "load",
+    "lm_head_greedy_top1_hip",
+    "lm_head_greedy_top1_impl",
+    "lm_head_sample_token_ids",
+    "reference_reduce_cast",
+    "sample_token_ids",
+    "select_token_selection_backend",
+]

@@ -1,0 +1,111 @@
+"""Backend selection for token selection.
+
+Mirrors the reference's declarative backend table and its strict-fail
+convention (nanovllm_jax/kernels/registry.py:15-110, 182-209) and the
+``lm_head_greedy_top1_impl`` value set (nanovllm_jax/model.py:369-380), with a
+``"hip"`` entry that is this package.  There is no pure-JAX path in this build,
+so an unavailable HIP library always raises ``KernelBackendUnavailable`` --
+never a silent fallback.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+from . import _lib
+
+
+class KernelBackendUnavailable(RuntimeError):
+    """Raised when the requested token-selection backend cannot run."""
+
+
+@dataclass(frozen=True)
+class KernelBackendSpec:
+    name: str
+    aliases: tuple[str, ...]
+    provided_kernels: tuple[str, ...]
+    description: str
+
+
+@dataclass(frozen=True)
+class KernelBackendStatus:
+    requested: str
+    selected: str
+    available: bool
+    provided_kernels: tuple[str, ...] = ()
+    reason: str = ""
+
+    def as_dict(self) -> dict[str, object]:
+        return {
+            "requested": self.requested,
+            "selected": self.selected,
+            "available": self.available,
+            "provided_kernels": list(self.provided_kernels),
+            "reason": self.reason,
+        }
+
+
+_SPECS = {
+    "hip": KernelBackendSpec(
+        name="hip",
+        aliases=("hip", "rocm", "nvjsel", "mi355x", "gfx950", "auto"),
+        provided_kernels=(
+            "lm_head_greedy_top1",
+            "lm_head_sample",
+            "sample_topk_topp",
+            "derive_rng_keys",
+        ),
+        description="Hand-written HIP kernels for gfx950 behind the libnvjsel C ABI.",
+    ),
+}
+_ALIASES = {a: n for n, s in _SPECS.items() for a in s.aliases}
+
+
+def lm_head_greedy_top1_impl(value: str | None) -> str:
+    """Normalise an ``lm_head_greedy_top1_impl`` setting (model.py:369-380 plus "hip")."""
+    v = str(value or "jax").strip().lower()
+    if v in {"", "0", "false", "no", "off", "none", "jax", "reference"}:
+        return "jax"
+    if v in {"triton", "triton_tensorcore", "triton_epilogue"}:
+        return "triton"
+    if v in {"cutlass", "cutlass_top1", "cutlass_fused_gemm", "fused_gemm"}:
+        return "cutlass"
+    if v in {"hip", "hip_mfma", "rocm", "nvjsel"}:
+        return "hip"
+    raise ValueError(
+        "lm_head_greedy_top1_impl must be jax, triton, cutlass, or hip, "
+        f"got {value!r}")
+
+
+def _normalize(name: str | None) -> str:
+    v = (name or "hip").strip().lower()
+    try:
+        return _ALIASES[v]
+    except KeyError:
+        valid = ", ".join(sorted(_ALIASES))
+        raise ValueError(f"Unknown token-selection backend {name!r}; expected one of: {valid}") from None
+
+
+def backend_status(name: str | None = None) -> KernelBackendStatus:
+    n = _normalize(name)
+    spec = _SPECS[n]
+    try:
+        _lib.load()
+        return KernelBackendStatus(requested=name or n, selected=n, available=True,
+                                   provided_kernels=spec.provided_kernels,
+                                   reason=f"{n} backend selected")
+    except Exception as exc:  # library missing or ABI mismatch
+        return KernelBackendStatus(requested=name or n, selected=n, available=False,
+                                   provided_kernels=spec.provided_kernels, reason=str(exc))
+
+
+def select_token_selection_backend(name: str | None = None, *, strict: bool = True) -> KernelBackendStatus:
+    """Resolve the backend; raises ``KernelBackendUnavailable`` when it cannot run
+    (``strict=False`` returns the unavailable status instead)."""
+    st = backend_status(name)
+    if strict and not st.available:
+        raise KernelBackendUnavailable(st.reason)
+    return st
+
+
+def available_backends() -> dict[str, KernelBackendStatus]:
+    return {n: backend_status(n) for n in _SPECS}

@@ -1,0 +1,268 @@
+"""Host-side mirror of the reference's token-selection interface, on torch-ROCm.
+
+Device memory and streams come from torch; every computation runs in
+libnvjsel.so (HIP, gfx950) through the C ABI of include/nvjsel.h.
+
+Mirrors:
+* ``lm_head_greedy_top1_hip``  <- ``lm_head_greedy_top1_triton``
+  (nanovllm_jax/kernels/lm_head_triton.py:114-186): same argument meaning,
+  same ``ValueError`` checks, returns int32 ``[B, 1]``.
+* ``lm_head_sample_token_ids`` <- ``lm_head_sample_token_ids``
+  (nanovllm_jax/model.py:901-938): ``T <= 0`` rows greedy, others
+  ``categorical(key, logits / max(T, 1e-6))``; extended with optional per-row
+  ``top_k`` / ``top_p`` (docs/kernel_roadmap.md:436-439).
+* ``sample_token_ids``         <- the roadmap ABI
+  ``sample_topk_topp(logits, temperature, top_k, top_p, rng_state) -> token_ids``.
+* ``derive_rng_keys``          <- the executor's key derivation
+  (nanovllm_jax/engine/model_executor.py:2131, 2214-2219, 2231).
+"""
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+
+_TORCH_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+
+
+def _dtype_code(t: torch.Tensor, what: str) -> int:
+    try:
+        return _TORCH_DTYPES[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported {what} dtype: {t.dtype}") from None
+
+
+def _require_cuda(*ts: torch.Tensor) -> torch.device:
+    dev = ts[0].device
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError("nvjsel kernels take device tensors (got a CPU tensor)")
+        if t.device != dev:
+            raise ValueError("all tensors must live on one device")
+    return dev
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class _WorkspacePool:
+    """Zero-filled scratch buffers per (device, stream, kind).
+
+    Each entry point leaves its workspace zero-filled when it returns, so a
+    buffer is zeroed once at allocation and reused in stream order."""
+
+    def __init__(self):
+        self._bufs: dict = {}
+        self._lock = threading.Lock()
+
+    def get(self, device: torch.device, stream: int, kind: str, nbytes: int) -> torch.Tensor:
+        key = (device.index, stream, kind)
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                buf = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
+                self._bufs[key] = buf
+            return buf
+
+
+_WS = _WorkspacePool()
+
+
+def _keys_as_i32(rng_keys: torch.Tensor, batch: int) -> torch.Tensor:
+    if rng_keys.ndim != 2 or rng_keys.shape[0] != batch or rng_keys.shape[1] != 2:
+        raise ValueError(f"rng_keys must be [B, 2] (got {tuple(rng_keys.shape)})")
+    if rng_keys.dtype == torch.int32:
+        return rng_keys.contiguous()
+    if rng_keys.dtype == torch.uint32:
+        return rng_keys.contiguous().view(torch.int32)
+    if rng_keys.dtype == torch.int64:
+        k = rng_keys & 0xFFFFFFFF
+        return torch.where(k >= 2**31, k - 2**32, k).to(torch.int32).contiguous()
+    raise ValueError(f"rng_keys dtype must be int32/uint32/int64 (got {rng_keys.dtype})")
+
+
+def _weight_operand(output_weight: torch.Tensor, weight_layout: str | None, hidden_dim: int):
+    """Return (tensor, layout code, vocab) for the weight.
+
+    ``weight_layout`` None follows the reference operand ``[H, V]``
+    (model.py:759): a transposed view of a contiguous ``[V, H]`` table --
+    ``embed_tokens.T`` -- is used in place, zero-copy, on the matrix-core path;
+    a contiguous ``[H, V]`` tensor uses the [H, V] layout."""
+    if output_weight.ndim != 2:
+        raise ValueError("LM-head top1 requires output weight shape [H, V]")
+    if weight_layout is None:
+        if output_weight.shape[0] != hidden_dim:
+            raise ValueError("hidden dimension must match output weight rows")
+        vocab = int(output_weight.shape[1])
+        if output_weight.stride() == (1, hidden_dim):
+            return output_weight.T, _lib.W_VH, vocab
+        return output_weight.contiguous(), _lib.W_HV, vocab
+    if weight_layout == "vh":
+        if output_weight.shape[1] != hidden_dim:
+            raise ValueError("hidden dimension must match output weight columns ([V, H] layout)")
+        return output_weight.contiguous(), _lib.W_VH, int(output_weight.shape[0])
+    if weight_layout == "hv":
+        if output_weight.shape[0] != hidden_dim:
+            raise ValueError("hidden dimension must match output weight rows")
+        return output_weight.contiguous(), _lib.W_HV, int(output_weight.shape[1])
+    raise ValueError(f"weight_layout must be None, 'hv' or 'vh' (got {weight_layout!r})")
+
+
+def reference_reduce_cast(hidden_dtype: torch.dtype, weight_dtype: torch.dtype) -> int:
+    """REDUCE_CAST rule of lm_head_triton.py:146-150 (and the bf16 output of jnp.dot)."""
+    if hidden_dtype == torch.bfloat16 and weight_dtype == torch.bfloat16:
+        return 1
+    if hidden_dtype == torch.float16 and weight_dtype == torch.float16:
+        return 2
+    return 0
+
+
+def _flatten_hidden(hidden_norm: torch.Tensor, require_3d: bool) -> torch.Tensor:
+    if hidden_norm.ndim == 3:
+        if int(hidden_norm.shape[1]) != 1:
+            raise ValueError("LM-head top1 requires hidden shape [B, 1, H]")
+        return hidden_norm.reshape(hidden_norm.shape[0], hidden_norm.shape[2])
+    if hidden_norm.ndim == 2 and not require_3d:
+        return hidden_norm
+    raise ValueError("LM-head top1 requires hidden shape [B, 1, H]")
+
+
+def lm_head_greedy_top1_hip(hidden_norm: torch.Tensor, output_weight: torch.Tensor, *,
+                            weight_layout: str | None = None, reduce_cast: int | None = None,
+                            return_best: bool = False):
+    """Greedy token ids for ``[B, 1, H] x [H, V]`` without materialising logits.
+
+    Returns int32 ``[B, 1]`` (and the winning logits ``f32[B]`` with
+    ``return_best``)."""
+    x = _flatten_hidden(hidden_norm, require_3d=False)
+    batch, hidden_dim = int(x.shape[0]), int(x.shape[1])
+    if batch <= 0 or hidden_dim <= 0 or output_weight.numel() == 0:
+        raise ValueError("LM-head top1 requires non-empty dimensions")
+    hd = _dtype_code(x, "hidden")
+    wd = _dtype_code(output_weight, "weight")
+    w, layout, vocab = _weight_operand(output_weight, weight_layout, hidden_dim)
+    dev = _require_cuda(x, w)
+    x = x.contiguous()
+    rc = reference_reduce_cast(x.dtype, w.dtype) if reduce_cast is None else int(reduce_cast)
+    out = torch.empty((batch,), dtype=torch.int32, device=dev)
+    best = torch.empty((batch,), dtype=torch.float32, device=dev) if return_best else None
+    stream = _stream_handle(dev)
+    lib = _lib.load()
+    nbytes = lib.nvjsel_lm_head_workspace_size(batch)
+    ws = _WS.get(dev, stream, "lm_head", nbytes)
+    _lib.call("nvjsel_lm_head_top1", x.data_ptr(), hd, w.data_ptr(), wd, layout, batch, hidden_dim,
+              vocab, rc, out.data_ptr(), best.data_ptr() if best is not None else None,
+              ws.data_ptr(), ws.numel(), stream)
+    ids = out[:, None]
+    return (ids, best) if return_best else ids
+
+
+def sample_token_ids(logits: torch.Tensor, temperatures: torch.Tensor, rng_keys: torch.Tensor, *,
+                     top_k: torch.Tensor | None = None, top_p: torch.Tensor | None = None,
+                     noise: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-row temperature / top-k / top-p sampling over ``logits [B, V]``
+    (or ``[B, 1, V]``).  Returns int32 ``[B]``."""
+    if logits.ndim == 3:
+        if int(logits.shape[1]) != 1:
+            raise ValueError("sampler takes logits [B, V] or [B, 1, V]")
+        logits = logits[:, 0, :]
+    if logits.ndim != 2:
+        raise ValueError("sampler takes logits [B, V] or [B, 1, V]")
+    batch, vocab = int(logits.shape[0]), int(logits.shape[1])
+    if batch <= 0 or vocab <= 0:
+        raise ValueError("sampler requires non-empty dimensions")
+    dt = _dtype_code(logits, "logits")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    dev = _require_cuda(logits, temperatures, rng_keys)
+    temps = temperatures.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+    if temps.numel() != batch:
+        raise ValueError("temperatures must have one value per row")
+    keys = _keys_as_i32(rng_keys.to(dev), batch)
+    tk = None
+    if top_k is not None:
+        tk = top_k.to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
+        if tk.numel() != batch:
+            raise ValueError("top_k must have one value per row")
+    tp = None
+    if top_p is not None:
+        tp = top_p.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+        if tp.numel() != batch:
+            raise ValueError("top_p must have one value per row")
+    nz = None
+    if noise is not None:
+        nz = noise.to(device=dev, dtype=torch.float32).contiguous()
+        if tuple(nz.shape) != (batch, vocab):
+            raise ValueError("noise must be [B, V]")
+    out = torch.empty((batch,), dtype=torch.int32, device=dev)
+    stream = _stream_handle(dev)
+    lib = _lib.load()
+    ws = _WS.get(dev, stream, "sample", lib.nvjsel_sample_workspace_size(batch, vocab))
+    _lib.call("nvjsel_sample", logits.data_ptr(), dt, batch, vocab, int(logits.stride(0)),
+              temps.data_ptr(), tk.data_ptr() if tk is not None else None,
+              tp.data_ptr() if tp is not None else None, keys.data_ptr(),
+              nz.data_ptr() if nz is not None else None, out.data_ptr(), ws.data_ptr(), ws.numel(),
+              stream)
+    return out
+
+
+def lm_head_sample_token_ids(hidden_norm: torch.Tensor, output_weight: torch.Tensor, *,
+                             temperatures: torch.Tensor, rng_keys: torch.Tensor,
+                             top_k: torch.Tensor | None = None, top_p: torch.Tensor | None = None,
+                             weight_layout: str | None = None,
+                             reduce_cast: int | None = None) -> torch.Tensor:
+    """Sample token ids from the LM head (model.py:901-938).
+
+    Without top-k/top-p the projection and the Gumbel-max are fused and no
+    logits are written.  With them, the logits are formed once (a library
+    GEMM, rounded as the reference's dot) and handed to the sampler."""
+    x = _flatten_hidden(hidden_norm, require_3d=False)
+    batch, hidden_dim = int(x.shape[0]), int(x.shape[1])
+    if batch <= 0 or hidden_dim <= 0:
+        raise ValueError("LM-head sampling requires non-empty dimensions")
+    hd = _dtype_code(x, "hidden")
+    wd = _dtype_code(output_weight, "weight")
+    w, layout, vocab = _weight_operand(output_weight, weight_layout, hidden_dim)
+    dev = _require_cuda(x, w)
+    x = x.contiguous()
+    rc = reference_reduce_cast(x.dtype, w.dtype) if reduce_cast is None else int(reduce_cast)
+    if top_k is not None or top_p is not None:
+        wt = w.T if layout == _lib.W_VH else w
+        if rc:
+            logits = torch.matmul(x, wt).float()
+        else:
+            logits = torch.matmul(x.float(), wt.float())
+        return sample_token_ids(logits, temperatures, rng_keys, top_k=top_k, top_p=top_p)
+    temps = temperatures.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+    if temps.numel() != batch:
+        raise ValueError("temperatures must have one value per row")
+    keys = _keys_as_i32(rng_keys.to(dev), batch)
+    out = torch.empty((batch,), dtype=torch.int32, device=dev)
+    stream = _stream_handle(dev)
+    lib = _lib.load()
+    ws = _WS.get(dev, stream, "lm_head", lib.nvjsel_lm_head_workspace_size(batch))
+    _lib.call("nvjsel_lm_head_sample", x.data_ptr(), hd, w.data_ptr(), wd, layout, batch, hidden_dim,
+              vocab, rc, temps.data_ptr(), keys.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
+              stream)
+    return out
+
+
+def derive_rng_keys(slots: torch.Tensor, counters: torch.Tensor):
+    """keys[b] = fold_in(fold_in(PRNGKey(0), slot_b), counter_b) on device.
+
+    Returns (keys int32[B, 2] holding the uint32 bit patterns, counters + 1)."""
+    dev = _require_cuda(slots, counters)
+    s = slots.to(dtype=torch.int32).reshape(-1).contiguous()
+    c = counters.to(dtype=torch.int32).reshape(-1).contiguous()
+    if s.numel() != c.numel() or s.numel() == 0:
+        raise ValueError("slots and counters must be non-empty and of equal length")
+    keys = torch.empty((s.numel(), 2), dtype=torch.int32, device=dev)
+    nxt = torch.empty_like(c)
+    _lib.call("nvjsel_derive_keys", s.data_ptr(), c.data_ptr(), s.numel(), keys.data_ptr(),
+              nxt.data_ptr(), _stream_handle(dev))
+    return keys, nxt

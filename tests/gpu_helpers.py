@@ -1,0 +1,72 @@
+"""Shared input builders and parity checks for the GPU tests.
+
+Inputs are seeded numpy arrays; the checker is the CPU oracle.  Nothing here
+reads the reference tree at run time."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import jax_random as jr
+from oracle import selection as sel
+
+
+def bf16_tensor(a: np.ndarray, device="cuda") -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device).to(torch.bfloat16)
+
+
+def as_f32(t: torch.Tensor) -> np.ndarray:
+    return t.float().cpu().numpy()
+
+
+def check_greedy(ids: np.ndarray, z64: np.ndarray, reduce_cast: int, ctx: str = "") -> int:
+    """ids must equal the oracle's, except on ambiguous rows (top-2 gap below
+    1e-3 relative, or a rounding boundary within fp32 accumulation error),
+    where they must be one of the admissible ids.  Returns the ambiguous count."""
+    exp, amb, adm = sel.greedy_top1(z64, reduce_cast)
+    ids = np.asarray(ids).reshape(-1)
+    for b in range(len(exp)):
+        if ids[b] != exp[b]:
+            assert amb[b] and int(ids[b]) in adm[b], (
+                f"{ctx} row {b}: got {ids[b]}, oracle {exp[b]}, admissible {sorted(adm[b])[:8]}")
+    return int(amb.sum())
+
+
+def engine_keys(batch: int, seed0: int = 0) -> np.ndarray:
+    """Per-row keys as the executor derives them, slot = row, counter = seed0."""
+    return np.array([[int(v) for v in jr.engine_key(b, seed0)] for b in range(batch)], dtype=np.uint32)
+
+
+def keys_tensor(keys: np.ndarray, device="cuda") -> torch.Tensor:
+    return torch.from_numpy(keys.view(np.int32).copy()).to(device)
+
+
+def check_sampled(ids, logits_f32, temps, top_k, top_p, keys, noise=None, ctx=""):
+    """Exact id match against the oracle except on rows the oracle reports as
+    mass-ambiguous (within 1e-5 of top_p at the threshold), where the id must be
+    admissible.  Returns the number of ambiguous rows."""
+    exp, info = sel.sample_rows(logits_f32, temps, top_k, top_p, keys, noise)
+    ids = np.asarray(ids).reshape(-1)
+    namb = 0
+    for b in range(len(exp)):
+        if info[b]["ambiguous"]:
+            namb += 1
+            assert int(ids[b]) in info[b]["ids"], f"{ctx} row {b}: {ids[b]} not in {info[b]['ids']}"
+        else:
+            assert int(ids[b]) == int(exp[b]), (
+                f"{ctx} row {b}: got {ids[b]}, oracle {exp[b]} (T={temps[b]}, k={top_k[b]}, "
+                f"p={top_p[b]}, kept={info[b]['kept']})")
+    return namb
+
+
+def zipf_logits(rng, batch: int, vocab: int, s_lo: float, s_hi: float, noise_sd: float) -> np.ndarray:
+    """log Zipf(s) profile, permuted per row, plus N(0, noise_sd) noise."""
+    ranks = np.arange(1, vocab + 1, dtype=np.float64)
+    out = np.empty((batch, vocab), dtype=np.float32)
+    for b in range(batch):
+        s = rng.uniform(s_lo, s_hi) if s_hi > s_lo else s_lo
+        lp = -s * np.log(ranks)
+        lp -= np.log(np.exp(lp).sum())
+        row = lp[rng.permutation(vocab)] + rng.normal(0.0, noise_sd, vocab)
+        out[b] = row.astype(np.float32)
+    return out

@@ -1,0 +1,115 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+include/nvjsel.h declares, and rejects bad arguments before any launch."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from nvjsel import _lib
+from nvjsel import registry
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "nvjsel.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nvjsel_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == sorted(_lib.exported_symbols())
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in declared_functions():
+        getattr(raw, name)  # raises AttributeError if not exported
+    assert lib.nvjsel_abi_version() == _lib.ABI_VERSION
+
+
+def test_workspace_sizes():
+    lib = _lib.load()
+    assert lib.nvjsel_lm_head_workspace_size(0) == 0
+    assert lib.nvjsel_lm_head_workspace_size(1) >= 8
+    assert lib.nvjsel_lm_head_workspace_size(256) >= 256 * 8
+    assert lib.nvjsel_sample_workspace_size(256, 248320) >= 256 * 16
+
+
+DUMMY = 0x1000  # never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("args,code", [
+    # batch 0
+    ((DUMMY, 1, DUMMY, 1, 0, 0, 32, 257, 1, DUMMY, None, DUMMY, 4096, None), -1),
+    # bad dtype
+    ((DUMMY, 7, DUMMY, 1, 0, 1, 32, 257, 1, DUMMY, None, DUMMY, 4096, None), -1),
+    # bad layout
+    ((DUMMY, 1, DUMMY, 1, 5, 1, 32, 257, 1, DUMMY, None, DUMMY, 4096, None), -1),
+    # bad reduce_cast
+    ((DUMMY, 1, DUMMY, 1, 0, 1, 32, 257, 9, DUMMY, None, DUMMY, 4096, None), -1),
+    # null hidden
+    ((None, 1, DUMMY, 1, 0, 1, 32, 257, 1, DUMMY, None, DUMMY, 4096, None), -1),
+    # workspace too small
+    ((DUMMY, 1, DUMMY, 1, 0, 64, 32, 257, 1, DUMMY, None, DUMMY, 8, None), -3),
+])
+def test_lm_head_top1_validation(args, code):
+    lib = _lib.load()
+    assert lib.nvjsel_lm_head_top1(*args) == code
+    assert lib.nvjsel_last_error()
+
+
+def test_sample_validation():
+    lib = _lib.load()
+    assert lib.nvjsel_sample(None, 0, 4, 100, 100, DUMMY, None, None, DUMMY, None, DUMMY, DUMMY, 4096, None) == -1
+    assert lib.nvjsel_sample(DUMMY, 0, 4, 100, 50, DUMMY, None, None, DUMMY, None, DUMMY, DUMMY, 4096, None) == -1
+    assert lib.nvjsel_sample(DUMMY, 3, 4, 100, 100, DUMMY, None, None, DUMMY, None, DUMMY, DUMMY, 4096, None) == -1
+    assert lib.nvjsel_sample(DUMMY, 0, 4, 100, 100, DUMMY, None, None, DUMMY, None, DUMMY, DUMMY, 1, None) == -3
+    assert lib.nvjsel_lm_head_sample(DUMMY, 1, DUMMY, 1, 0, 2, 32, 10, 1, None, DUMMY, DUMMY, DUMMY, 4096, None) == -1
+    assert lib.nvjsel_derive_keys(DUMMY, DUMMY, 0, DUMMY, None, None) == -1
+    with pytest.raises(_lib.NvjselError) as ei:
+        _lib.call("nvjsel_derive_keys", None, None, 3, None, None, None)
+    assert "null" in str(ei.value)
+
+
+def test_registry_semantics():
+    assert registry.lm_head_greedy_top1_impl(None) == "jax"
+    assert registry.lm_head_greedy_top1_impl("Triton") == "triton"
+    assert registry.lm_head_greedy_top1_impl("fused_gemm") == "cutlass"
+    assert registry.lm_head_greedy_top1_impl("hip") == "hip"
+    with pytest.raises(ValueError):
+        registry.lm_head_greedy_top1_impl("bogus")
+    st = registry.select_token_selection_backend("auto")
+    assert st.selected == "hip" and st.available
+    with pytest.raises(ValueError):
+        registry.select_token_selection_backend("nope")
+
+
+def test_registry_strict_raises_when_library_missing(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "missing.so")
+    with pytest.raises(registry.KernelBackendUnavailable):
+        registry.select_token_selection_backend("hip")
+    assert not registry.select_token_selection_backend("hip", strict=False).available
+
+
+def test_host_api_rejects_bad_shapes_before_launch():
+    torch = pytest.importorskip("torch")
+    import nvjsel
+
+    h = torch.zeros(3, 2, 32, dtype=torch.bfloat16)
+    w = torch.zeros(32, 257, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match=r"\[B, 1, H\]"):
+        nvjsel.lm_head_greedy_top1_hip(h, w)
+    with pytest.raises(ValueError, match="must match"):
+        nvjsel.lm_head_greedy_top1_hip(torch.zeros(3, 1, 16, dtype=torch.bfloat16), w)
+    with pytest.raises(ValueError, match="dtype"):
+        nvjsel.lm_head_greedy_top1_hip(torch.zeros(3, 1, 32, dtype=torch.int8), w)
+    with pytest.raises(ValueError, match="device"):
+        nvjsel.lm_head_greedy_top1_hip(torch.zeros(3, 1, 32, dtype=torch.bfloat16), w)
+    with pytest.raises(ValueError, match="non-empty"):
+        nvjsel.lm_head_greedy_top1_hip(torch.zeros(0, 1, 32, dtype=torch.bfloat16), w)

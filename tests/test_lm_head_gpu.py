@@ -1,0 +1,126 @@
+"""GPU parity: fused LM-head greedy top-1 (libnvjsel) against the CPU oracle.
+
+Mirrors the reference's checks (tests/test_lm_head_helpers.py:159-206: bf16
+hidden [3,1,32] x E[257,32], V not a multiple of the tile) and extends them to
+the BASELINE shapes (V=248320, H=1024) and every dispatch path."""
+import numpy as np
+import pytest
+import torch
+
+import nvjsel
+from oracle import selection as sel
+from tests.gpu_helpers import as_f32, bf16_tensor, check_greedy
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(h, w, **kw):
+    ids = nvjsel.lm_head_greedy_top1_hip(h, w, **kw)
+    torch.cuda.synchronize()
+    assert ids.dtype == torch.int32
+    return ids.cpu().numpy().reshape(-1)
+
+
+def test_reference_shape_tied_embedding_bf16():
+    rng = np.random.default_rng(19)
+    h = bf16_tensor(rng.standard_normal((3, 1, 32)))
+    E = bf16_tensor(rng.standard_normal((257, 32)))
+    ids = _run(h, E.T)  # the reference passes embed_tokens.T; used in place
+    z = sel.lm_head_logits(as_f32(h)[:, 0], as_f32(E), weight_layout="vh")
+    check_greedy(ids, z, 1, "ref-shape")
+    assert ids.shape == (3,)
+
+
+@pytest.mark.parametrize("batch", [1, 2, 5, 16, 17, 33, 64, 70])
+def test_bf16_batches_odd_vocab(batch):
+    rng = np.random.default_rng(100 + batch)
+    H, V = 1024, 4099
+    h = bf16_tensor(rng.standard_normal((batch, H)))
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.02)
+    ids = _run(h, W, weight_layout="vh")
+    z = sel.lm_head_logits(as_f32(h), as_f32(W))
+    check_greedy(ids, z, 1, f"B={batch}")
+
+
+def test_full_vocab_batch1_with_best_value():
+    """hidden [1,1024] ~N(0,1), W [248320,1024] ~N(0,0.02), bf16."""
+    g = torch.Generator().manual_seed(0)
+    H, V = 1024, 248320
+    h = torch.randn(1, H, generator=g).to(torch.bfloat16)
+    W = (torch.randn(V, H, generator=g) * 0.02).to(torch.bfloat16)
+    ids, best = nvjsel.lm_head_greedy_top1_hip(h.cuda(), W.cuda(), weight_layout="vh", return_best=True)
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(h.float().numpy(), W.float().numpy())
+    check_greedy(ids.cpu().numpy(), z, 1, "C1")
+    i = int(ids[0, 0])
+    assert abs(float(best[0]) - sel.round_bf16(np.float32(z[0, i]))) <= 2 ** -7 * abs(z[0, i])
+
+
+@pytest.mark.parametrize("batch", [1, 20])
+def test_f32_hidden_exact_split(batch):
+    """f32 activations x bf16 weight: fp32 dot (no logit rounding), as jnp.dot promotes."""
+    rng = np.random.default_rng(7 + batch)
+    H, V = 512, 3001
+    h = torch.from_numpy(rng.standard_normal((batch, H)).astype(np.float32)).cuda()
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    ids, best = nvjsel.lm_head_greedy_top1_hip(h, W, weight_layout="vh", return_best=True)
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(h.cpu().numpy(), as_f32(W))
+    check_greedy(ids.cpu().numpy(), z, 0, "f32-hidden")
+    zb = z[np.arange(batch), ids.cpu().numpy().reshape(-1)]
+    assert np.allclose(best.cpu().numpy(), zb, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("layout", ["hv", "vh"])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_generic_paths(layout, dt):
+    rng = np.random.default_rng(3)
+    B, H, V = 4, 96, 777
+    h = torch.from_numpy(rng.standard_normal((B, H)).astype(np.float32)).to(dt).cuda()
+    Wvh = torch.from_numpy((rng.standard_normal((V, H)) * 0.1).astype(np.float32)).to(dt).cuda()
+    W = Wvh if layout == "vh" else Wvh.T.contiguous()
+    ids = _run(h, W, weight_layout=layout)
+    z = sel.lm_head_logits(h.float().cpu().numpy(), Wvh.float().cpu().numpy())
+    check_greedy(ids, z, 2 if dt == torch.float16 else 0, f"{layout}/{dt}")
+
+
+def test_hidden_dim_not_multiple_of_32_uses_generic():
+    rng = np.random.default_rng(5)
+    h = bf16_tensor(rng.standard_normal((2, 1, 40)))
+    E = bf16_tensor(rng.standard_normal((300, 40)))
+    ids = _run(h, E.T)
+    check_greedy(ids, sel.lm_head_logits(as_f32(h)[:, 0], as_f32(E)), 1, "H=40")
+
+
+def test_ties_resolve_to_lowest_index_across_blocks():
+    """Identical rows far apart in the vocabulary (different blocks/waves)."""
+    rng = np.random.default_rng(11)
+    H, V = 256, 70000
+    Wn = (rng.standard_normal((V, H)) * 0.01).astype(np.float32)
+    h = np.abs(rng.standard_normal((2, H))).astype(np.float32)
+    hot = np.full(H, 0.5, np.float32)
+    for v in (65000, 40000, 12345, 69999):
+        Wn[v] = hot
+    ids = _run(bf16_tensor(h), bf16_tensor(Wn), weight_layout="vh")
+    assert list(ids) == [12345, 12345]
+
+
+def test_nan_logit_wins_first():
+    rng = np.random.default_rng(12)
+    H, V = 128, 5000
+    Wn = (rng.standard_normal((V, H)) * 0.01).astype(np.float32)
+    Wn[4000, 3] = np.nan
+    Wn[2500, 7] = np.nan
+    ids = _run(bf16_tensor(rng.standard_normal((3, H))), bf16_tensor(Wn), weight_layout="vh")
+    assert list(ids) == [2500, 2500, 2500]
+
+
+def test_repeated_calls_reuse_workspace():
+    rng = np.random.default_rng(13)
+    H, V = 256, 9000
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    for trial in range(4):
+        B = [3, 40, 1, 16][trial]
+        h = bf16_tensor(rng.standard_normal((B, H)))
+        ids = _run(h, W, weight_layout="vh")
+        check_greedy(ids, sel.lm_head_logits(as_f32(h), as_f32(W)), 1, f"trial{trial}")

@@ -1,0 +1,174 @@
+"""GPU parity: the logits sampler and key derivation (libnvjsel) against the oracle.
+
+The temperature route mirrors the reference's only sampler test
+(tests/test_lm_head_helpers.py:218-262: T=[0, 0.7], ids equal
+[argmax(l0), categorical(k1, l1/0.7)]); top-k / top-p follow the build's spec
+(the reference has no serving top-k/top-p sampler)."""
+import numpy as np
+import pytest
+import torch
+
+import nvjsel
+from oracle import jax_random as jr
+from oracle import selection as sel
+from tests.gpu_helpers import check_sampled, engine_keys, keys_tensor, zipf_logits
+
+pytestmark = pytest.mark.gpu
+
+
+def _sample(logits_np, temps, top_k=None, top_p=None, keys=None, dtype=torch.float32, noise=None):
+    B, V = logits_np.shape
+    keys = engine_keys(B) if keys is None else keys
+    lt = torch.from_numpy(logits_np).to(dtype).cuda()
+    out = nvjsel.sample_token_ids(
+        lt, torch.tensor(temps, dtype=torch.float32).cuda(), keys_tensor(keys),
+        top_k=None if top_k is None else torch.tensor(top_k, dtype=torch.int32).cuda(),
+        top_p=None if top_p is None else torch.tensor(top_p, dtype=torch.float32).cuda(),
+        noise=None if noise is None else torch.from_numpy(noise).cuda())
+    torch.cuda.synchronize()
+    used = lt.float().cpu().numpy()  # the values the kernel saw (bf16-rounded if bf16)
+    return out.cpu().numpy(), used, keys
+
+
+def test_reference_sampler_case_greedy_and_temperature():
+    rng = np.random.default_rng(7)
+    l = rng.standard_normal((2, 7)).astype(np.float32)
+    keys = jr.split(jr.prng_key(7), 2)
+    ids, used, _ = _sample(l, [0.0, 0.7], keys=keys)
+    assert ids[0] == np.argmax(l[0])
+    assert ids[1] == jr.categorical((keys[1, 0], keys[1, 1]), (l[1] / np.float32(0.7)).astype(np.float32))
+
+
+def test_temperature_full_vocab_c2():
+    """f32 [8, 248320] ~N(0,3) + 5 spikes/row at +12, T=0.7, seed=row."""
+    rng = np.random.default_rng(1)
+    B, V = 8, 248320
+    l = (rng.standard_normal((B, V)) * 3).astype(np.float32)
+    for b in range(B):
+        l[b, rng.choice(V, 5, replace=False)] += 12.0
+    keys = np.stack([np.array([int(x) for x in jr.prng_key(b)], np.uint32) for b in range(B)])
+    ids, used, _ = _sample(l, [0.7] * B, keys=keys)
+    check_sampled(ids, used, [0.7] * B, [0] * B, [1.0] * B, keys, ctx="C2")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_greedy_rows_all_dtypes(dtype):
+    rng = np.random.default_rng(2)
+    l = rng.standard_normal((5, 30011)).astype(np.float32)
+    l[3, 100] = l[3, 29000] = 50.0  # tie: lowest index
+    ids, used, _ = _sample(l, [0.0, -1.0, 0.0, 0.0, 0.0], top_k=[5] * 5, top_p=[0.5] * 5, dtype=dtype)
+    assert np.array_equal(ids, np.argmax(used, axis=1))
+    assert ids[3] == 100
+
+
+def test_topk_topp_c3_shape():
+    """BASELINE config 2 (at B=8): log Zipf(1.1) permuted + N(0,0.5), k=50, p=0.9, T=0.8."""
+    rng = np.random.default_rng(3)
+    B, V = 8, 248320
+    l = zipf_logits(rng, B, V, 1.1, 1.1, 0.5)
+    ids, used, keys = _sample(l, [0.8] * B, top_k=[50] * B, top_p=[0.9] * B)
+    check_sampled(ids, used, [0.8] * B, [50] * B, [0.9] * B, keys, ctx="C3")
+
+
+def test_mixed_rows_c5_shape_bf16():
+    """BASELINE config 4 (at B=24): bf16 Zipf(1.05..1.3) + N(0,1), mixed T/k/p per row."""
+    rng = np.random.default_rng(4)
+    B, V = 24, 248320
+    l = zipf_logits(rng, B, V, 1.05, 1.3, 1.0)
+    T = [float(x) for x in rng.choice([0.0, 0.6, 1.0], B)]
+    K = [int(x) for x in rng.choice([0, 20, 100], B)]
+    P = [float(x) for x in rng.choice([1.0, 0.95, 0.8], B)]
+    ids, used, keys = _sample(l, T, top_k=K, top_p=P, dtype=torch.bfloat16)
+    check_sampled(ids, used, T, K, P, keys, ctx="C5")
+
+
+@pytest.mark.parametrize("k,p", [(1, 1.0), (2, 1.0), (7, 0.5), (0, 0.3), (0, 0.999), (0, 0.0),
+                                 (4999, 1.0), (5000, 1.0), (6000, 0.9), (-1, 0.7)])
+def test_filter_parameter_edges(k, p):
+    rng = np.random.default_rng(5)
+    B, V = 6, 5000
+    l = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    T = [0.9] * B
+    ids, used, keys = _sample(l, T, top_k=[k] * B, top_p=[p] * B)
+    check_sampled(ids, used, T, [k] * B, [p] * B, keys, ctx=f"k={k},p={p}")
+
+
+def test_heavy_ties_and_quantised_logits():
+    rng = np.random.default_rng(6)
+    B, V = 6, 20000
+    l = np.round(rng.standard_normal((B, V)) * 2).astype(np.float32)  # ~9 distinct values
+    l[5] = 1.0  # constant row
+    T = [1.0] * B
+    K = [3, 100, 0, 0, 50, 10]
+    P = [1.0, 0.9, 0.5, 0.95, 0.7, 0.5]
+    ids, used, keys = _sample(l, T, top_k=K, top_p=P)
+    check_sampled(ids, used, T, K, P, keys, ctx="ties")
+
+
+def test_nonfinite_rows():
+    B, V = 5, 4000
+    rng = np.random.default_rng(7)
+    l = rng.standard_normal((B, V)).astype(np.float32)
+    l[0, [10, 20]] = np.nan
+    l[1, [30, 3000]] = np.inf
+    l[2] = -np.inf
+    l[3, :] = -np.inf
+    l[3, 1234] = 2.0  # one finite value
+    l[4, 5] = -np.inf
+    T = [1.0] * B
+    ids, used, keys = _sample(l, T, top_k=[5] * B, top_p=[0.9] * B)
+    assert ids[0] == 10 and ids[1] == 30 and ids[2] == 0 and ids[3] == 1234
+    check_sampled(ids, used, T, [5] * B, [0.9] * B, keys, ctx="nonfinite")
+    # unfiltered temperature rows follow categorical (NaN first, +inf first)
+    ids2, used2, keys2 = _sample(l[:2], [1.0, 1.0])
+    assert ids2[0] == 10 and ids2[1] == 30
+
+
+def test_external_noise_mode():
+    """Identical draws: ids equal argmax over kept of x + noise exactly."""
+    rng = np.random.default_rng(8)
+    B, V = 4, 10000
+    l = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    noise = rng.gumbel(size=(B, V)).astype(np.float32)
+    T, K, P = [0.7, 1.0, 1.3, 0.5], [0, 10, 0, 200], [1.0, 1.0, 0.8, 0.9]
+    ids, used, keys = _sample(l, T, top_k=K, top_p=P, noise=noise)
+    check_sampled(ids, used, T, K, P, keys, noise=noise, ctx="noise")
+
+
+def test_real_logits_row_fixture():
+    """The reference's real Qwen3.5-0.8B logits row (results/qwen08_hf_logits_serving_workloads.npz)."""
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "qwen08_logits_row.npz")
+    row = np.load(path)["logits_0"].astype(np.float32)
+    assert int(np.argmax(row)) == 13
+    l = np.stack([row] * 6)
+    T = [0.0, 0.7, 1.0, 1.0, 0.6, 1.2]
+    K = [0, 0, 50, 0, 20, 1000]
+    P = [1.0, 1.0, 0.9, 0.95, 0.8, 0.99]
+    ids, used, keys = _sample(l, T, top_k=K, top_p=P)
+    assert ids[0] == 13
+    check_sampled(ids, used, T, K, P, keys, ctx="qwen-row")
+
+
+def test_derive_keys_matches_fold_in_chain():
+    slots = np.array([0, 1, 5, 1000, -3, 7], np.int32)
+    counters = np.array([0, 0, 17, 2**31 - 1, 4, -1], np.int32)
+    keys, nxt = nvjsel.derive_rng_keys(torch.from_numpy(slots).cuda(), torch.from_numpy(counters).cuda())
+    torch.cuda.synchronize()
+    got = keys.cpu().numpy().view(np.uint32)
+    for b in range(len(slots)):
+        exp = jr.engine_key(max(0, int(slots[b])), int(counters[b]) & 0xFFFFFFFF)
+        assert tuple(int(x) for x in got[b]) == (int(exp[0]), int(exp[1]))
+    assert np.array_equal(nxt.cpu().numpy(), (counters.astype(np.int64) + 1).astype(np.int32))
+
+
+def test_repeated_calls_leave_workspace_clean():
+    rng = np.random.default_rng(9)
+    for trial in range(3):
+        B, V = [4, 9, 2][trial], [3000, 777, 12000][trial]
+        l = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+        T = [1.0] * B
+        K = [int(x) for x in rng.choice([0, 5], B)]
+        P = [float(x) for x in rng.choice([1.0, 0.8], B)]
+        ids, used, keys = _sample(l, T, top_k=K, top_p=P)
+        check_sampled(ids, used, T, K, P, keys, ctx=f"trial{trial}")
