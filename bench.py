@@ -98,7 +98,7 @@ def build_configs(torch, which):
         w = ws(lib.nvjsel_lm_head_workspace_size(1))
         state = {"i": 0}
 
-        def launch():
+        def launch(Ws=Ws, h=h, out=out, w=w, state=state):
             Wi = Ws[state["i"] & 1]
             state["i"] += 1
             rc = lib.nvjsel_lm_head_top1(h.data_ptr(), 1, Wi.data_ptr(), 1, 0, 1, H_FULL, V_FULL, 1,
@@ -119,7 +119,7 @@ def build_configs(torch, which):
         out = torch.empty(B, dtype=torch.int32, device=dev)
         w = ws(lib.nvjsel_sample_workspace_size(B, V_FULL))
 
-        def launch(l=l, t=t, keys=keys, out=out, w=w):
+        def launch(l=l, t=t, keys=keys, out=out, w=w, B=B):
             rc = lib.nvjsel_sample(l.data_ptr(), 0, B, V_FULL, V_FULL, t.data_ptr(), None, None,
                                    keys.data_ptr(), None, out.data_ptr(), w.data_ptr(), w.numel(), stream())
             assert rc == 0, lib.nvjsel_last_error()
@@ -137,7 +137,7 @@ def build_configs(torch, which):
         out = torch.empty(B, dtype=torch.int32, device=dev)
         w = ws(lib.nvjsel_sample_workspace_size(B, V_FULL))
 
-        def launch(l=l, t=t, k=k, p=p, keys=keys, out=out, w=w):
+        def launch(l=l, t=t, k=k, p=p, keys=keys, out=out, w=w, B=B):
             rc = lib.nvjsel_sample(l.data_ptr(), 0, B, V_FULL, V_FULL, t.data_ptr(), k.data_ptr(),
                                    p.data_ptr(), keys.data_ptr(), None, out.data_ptr(), w.data_ptr(),
                                    w.numel(), stream())
@@ -156,7 +156,7 @@ def build_configs(torch, which):
         w = ws(lib.nvjsel_lm_head_workspace_size(B))
         state = {"i": 0}
 
-        def launch(h=h, t=t, keys=keys, out=out, w=w):
+        def launch(h=h, t=t, keys=keys, out=out, w=w, B=B, Ws=Ws, state=state):
             Wi = Ws[state["i"] & 1]
             state["i"] += 1
             rc = lib.nvjsel_lm_head_sample(h.data_ptr(), 1, Wi.data_ptr(), 1, 0, B, H_FULL, V_FULL, 1,
@@ -179,7 +179,7 @@ def build_configs(torch, which):
         out = torch.empty(B, dtype=torch.int32, device=dev)
         w = ws(lib.nvjsel_sample_workspace_size(B, V_FULL))
 
-        def launch(l=l, t=t, k=k, p=p, keys=keys, out=out, w=w):
+        def launch(l=l, t=t, k=k, p=p, keys=keys, out=out, w=w, B=B):
             rc = lib.nvjsel_sample(l.data_ptr(), 1, B, V_FULL, V_FULL, t.data_ptr(), k.data_ptr(),
                                    p.data_ptr(), keys.data_ptr(), None, out.data_ptr(), w.data_ptr(),
                                    w.numel(), stream())

@@ -26,7 +26,62 @@
 #include "nvjsel_device.h"
 #include "nvjsel_host.h"
 
+// Launch shape; overridable at build time for tuning sweeps.
+#ifndef NVJSEL_LM_WAVES
+#define NVJSEL_LM_WAVES 8  // waves per block
+#endif
+#ifndef NVJSEL_LM_MT1
+#define NVJSEL_LM_MT1 4  // 16-row vocab tiles per wave when B <= 16
+#endif
+#ifndef NVJSEL_LM_MTN
+#define NVJSEL_LM_MTN 2  // ... when B > 16
+#endif
+#ifndef NVJSEL_LM_KU
+#define NVJSEL_LM_KU 4  // 32-wide k-steps per prefetch chunk
+#endif
+#ifndef NVJSEL_LM_NT
+#define NVJSEL_LM_NT 1  // non-temporal (streaming) loads of W
+#endif
+#ifndef NVJSEL_LM_DEPTH
+#define NVJSEL_LM_DEPTH 3  // k-chunks of W in flight per wave
+#endif
+#ifndef NVJSEL_LM_BPC
+#define NVJSEL_LM_BPC 0  // blocks per CU (0 = as many as occupancy allows)
+#endif
+
+#ifndef NVJSEL_GEMV_WAVES
+#define NVJSEL_GEMV_WAVES 4  // waves per block of the streaming GEMV
+#endif
+#ifndef NVJSEL_GEMV_CONTIG
+#define NVJSEL_GEMV_CONTIG 0  // 0 grid-stride groups, 1 slice per wave, 2 per block, 3 rotated slice
+#endif
+#ifndef NVJSEL_GEMV_GRID_NUM
+#define NVJSEL_GEMV_GRID_NUM 1  // grid = CUs * blocks-per-CU * NUM / DEN
+#define NVJSEL_GEMV_GRID_DEN 1
+#endif
+#ifndef NVJSEL_GEMV_NOCOMPUTE
+#define NVJSEL_GEMV_NOCOMPUTE 0
+#endif
+#ifndef NVJSEL_GEMV_DEPTH
+#define NVJSEL_GEMV_DEPTH 4  // row groups in flight per wave
+#endif
+#ifndef NVJSEL_GEMV_BPC
+#define NVJSEL_GEMV_BPC 1  // blocks per CU for the streaming GEMV (0 = occupancy)
+#endif
+#ifndef NVJSEL_GEMV_R
+#define NVJSEL_GEMV_R 4  // rows per wave step of the streaming GEMV
+#endif
+
 namespace nvjsel {
+
+template <typename T>
+__device__ __forceinline__ T stream_load(const T* p) {
+#if NVJSEL_LM_NT
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -124,11 +179,10 @@ __device__ __forceinline__ void block_commit(unsigned long long* red, int B,
 // WT: weight element type (DT_BF16 / DT_F16).  NSPLIT: hidden terms (1, or 3
 // for an exact f32 hidden on bf16 weights).  NB: 16-row batch tiles.  MT:
 // 16-row vocab tiles per wave.  KU: k-steps (32 each) per prefetch chunk.
-template <int WT, int NSPLIT, int NB, int MT, int WAVES, int MODE>
+template <int WT, int NSPLIT, int NB, int MT, int WAVES, int KU, int DEPTH, int MODE>
 __global__ void __launch_bounds__(WAVES * 64)
 lm_head_mfma_kernel(LmArgs a) {
   constexpr int BP = NB * 16;
-  constexpr int KU = 4;
   extern __shared__ u32x4_t lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -187,65 +241,66 @@ lm_head_mfma_kernel(LmArgs a) {
   for (int nb = 0; nb < NB; ++nb) best[nb] = 0;
 
   const int ksteps = H >> 5;
-  const int nch = ksteps / KU;
+  const int nch = ksteps / KU;  // the host guarantees KU divides ksteps
   constexpr int ROWS = 16 * MT;
   const int ntiles = (V + ROWS - 1) / ROWS;
   const uint16_t* W = (const uint16_t*)a.W;
 
-  for (int tile = blockIdx.x * WAVES + wave; tile < ntiles; tile += gridDim.x * WAVES) {
-    const int v0 = tile * ROWS;
-    const u32x4_t* wp[MT];
+  // Each wave walks its tiles (grid-stride) as one sequence of k-chunks q and
+  // keeps DEPTH-1 chunks of W requested ahead of the chunk it multiplies, across
+  // tile boundaries.
+  const int nwaves = gridDim.x * WAVES;
+  const int gw = blockIdx.x * WAVES + wave;
+  const int n_my_tiles = gw < ntiles ? (ntiles - gw + nwaves - 1) / nwaves : 0;
+  const int nq = n_my_tiles * nch;
+  auto load_q = [&](u32x4_t(&A)[KU][MT], int q) {
+    const int tile = gw + (q / nch) * nwaves;
+    const int c = q % nch;
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      int row = v0 + t * 16 + r;
+      int row = tile * ROWS + t * 16 + r;
       row = row < V ? row : V - 1;
-      wp[t] = (const u32x4_t*)(W + (size_t)row * H) + g;
+      const u32x4_t* p = (const u32x4_t*)(W + (size_t)row * H) + g + c * KU * 4;
+#pragma unroll
+      for (int u = 0; u < KU; ++u) A[u][t] = stream_load(p + u * 4);
     }
-    f32x4_t acc[MT][NB];
+    __builtin_amdgcn_sched_barrier(0);  // the whole chunk is requested before any use
+  };
+  f32x4_t acc[MT][NB];
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+  for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[t][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < NB; ++nb) acc[t][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    u32x4_t A0[KU][MT], A1[KU][MT];
-    auto load_chunk = [&](u32x4_t(&A)[KU][MT], int c) {
+  u32x4_t ring[DEPTH][KU][MT];
 #pragma unroll
-      for (int u = 0; u < KU; ++u)
+  for (int d = 0; d < DEPTH - 1; ++d)
+    if (d < nq) load_q(ring[d], d);
+  for (int q = 0; q < nq; ++q) {
+    if (q + DEPTH - 1 < nq) load_q(ring[DEPTH - 1], q + DEPTH - 1);
+    const int c = q % nch;
 #pragma unroll
-        for (int t = 0; t < MT; ++t) A[u][t] = __builtin_nontemporal_load(wp[t] + (c * KU + u) * 4);
-    };
-    auto step = [&](const u32x4_t(&At)[MT], int kb) {
+    for (int u = 0; u < KU; ++u) {
+      const int kb = c * KU + u;
 #pragma unroll
       for (int s = 0; s < NSPLIT; ++s)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           const u32x4_t bfr = lds[((kb * 4 + g) * NSPLIT + s) * BP + nb * 16 + r];
 #pragma unroll
-          for (int t = 0; t < MT; ++t) acc[t][nb] = mfma16x16x32<WT>(At[t], bfr, acc[t][nb]);
+          for (int t = 0; t < MT; ++t) acc[t][nb] = mfma16x16x32<WT>(ring[0][u][t], bfr, acc[t][nb]);
         }
-    };
-    auto comp_chunk = [&](u32x4_t(&A)[KU][MT], int c) {
-#pragma unroll
-      for (int u = 0; u < KU; ++u) step(A[u], c * KU + u);
-    };
-
-    if (nch > 0) load_chunk(A0, 0);
-    for (int c = 0; c < nch; c += 2) {
-      if (c + 1 < nch) load_chunk(A1, c + 1);
-      comp_chunk(A0, c);
-      if (c + 1 < nch) {
-        if (c + 2 < nch) load_chunk(A0, c + 2);
-        comp_chunk(A1, c + 1);
-      }
     }
-    for (int kb = nch * KU; kb < ksteps; ++kb) {
-      u32x4_t At[MT];
 #pragma unroll
-      for (int t = 0; t < MT; ++t) At[t] = __builtin_nontemporal_load(wp[t] + kb * 4);
-      step(At, kb);
-    }
+    for (int d = 0; d < DEPTH - 1; ++d)
+#pragma unroll
+      for (int u = 0; u < KU; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) ring[d][u][t] = ring[d + 1][u][t];
+    if (c != nch - 1) continue;
 
     // ---- epilogue: D[row = 4g + i][col = r] of each 16x16 tile
+    const int v0 = (gw + (q / nch) * nwaves) * ROWS;
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -262,6 +317,7 @@ lm_head_mfma_kernel(LmArgs a) {
             best[nb] = max_u64(best[nb], argmax_key(val, (uint32_t)v));
           }
         }
+        acc[t][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
   }
 
@@ -278,6 +334,179 @@ lm_head_mfma_kernel(LmArgs a) {
     for (int nb = 0; nb < NB; ++nb) red[wave * BP + nb * 16 + r] = best[nb];
   }
   block_commit<WAVES, BP>(red, B, a.row_keys);
+  finish_rows(a.row_keys, a.counter, B, a.out_ids, a.out_best);
+}
+
+// ------------------------------------------------------------------ streaming GEMV kernel
+// Small batch (B <= 2), weight [V,H] bf16 with H = KJ * 512.  Every load
+// instruction of a wave reads 1 KB of W contiguous (64 lanes x 16 B), the
+// pattern that streams HBM at full rate: lane l holds k = 512 j + 8 l .. +7 of
+// each row.  A wave takes R consecutive rows per step (R * 2H bytes
+// contiguous), forms per-lane partial dots against the hidden held in
+// registers, then a butterfly transpose-reduction leaves each group of 64/R
+// lanes with the full dot of one row (log2(64) shuffle rounds, halving the
+// values carried at each of the first log2(R) rounds).
+template <int NB, int R, int KJ, int MODE>
+__global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(LmArgs a) {
+  constexpr int WAVES = NVJSEL_GEMV_WAVES;
+  __shared__ unsigned long long red[WAVES * NB];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int H = KJ * 512, V = a.V, B = a.B;
+  float hv[NB][KJ][8];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int j = 0; j < KJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        hv[b][j][e] = (b < B) ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * H + j * 512 + lane * 8 + e) : 0.0f;
+
+  float tp[NB];
+  bool greedy_row[NB];
+  TfKey key[NB];
+  if constexpr (MODE == MODE_SAMPLE) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float t = (b < B) ? a.temperature[b] : 0.0f;
+      greedy_row[b] = (t <= 0.0f);
+      tp[b] = temp_floor(t);
+      key[b] = (b < B) ? tf_key(a.keys[2 * b], a.keys[2 * b + 1]) : tf_key(0u, 0u);
+    }
+  }
+  unsigned long long best[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) best[b] = 0;
+
+  const uint16_t* W = (const uint16_t*)a.W;
+  const int ngroups = (V + R - 1) / R;
+  const int nwaves = gridDim.x * WAVES;
+  const int gw = blockIdx.x * WAVES + wave;
+#if NVJSEL_GEMV_CONTIG == 1 || NVJSEL_GEMV_CONTIG == 3
+  // each wave streams one contiguous slice of the vocabulary
+  const int per = (ngroups + nwaves - 1) / nwaves;
+  const int g_begin = gw * per;
+  const int g_end = min(g_begin + per, ngroups);
+  const int g_step = 1;
+#elif NVJSEL_GEMV_CONTIG == 2
+  // each block streams one contiguous slice; its waves take adjacent groups
+  const int per = (ngroups + gridDim.x - 1) / gridDim.x;
+  const int g_begin = blockIdx.x * per + wave;
+  const int g_end = min(blockIdx.x * per + per, ngroups);
+  const int g_step = WAVES;
+#else
+  const int g_begin = gw, g_end = ngroups, g_step = nwaves;
+#endif
+
+  auto load_grp = [&](u32x4_t(&w)[R][KJ], int grp) {
+    const int v0 = grp * R;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = (v0 + r < V) ? v0 + r : V - 1;
+#pragma unroll
+      for (int j = 0; j < KJ; ++j)
+        w[r][j] = stream_load((const u32x4_t*)(W + (size_t)row * H + j * 512) + lane);
+    }
+    // keep every load of the step ahead of the first use: R*KJ KB in flight per wave
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  auto proc_grp = [&](const u32x4_t(&w)[R][KJ], int grp) {
+    const int v0 = grp * R;
+#if NVJSEL_GEMV_NOCOMPUTE
+    // timing probe only: consume the loads without the dot products
+    uint32_t xx = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) xx ^= w[r][j].x ^ w[r][j].y ^ w[r][j].z ^ w[r][j].w;
+    best[0] = max_u64(best[0], (unsigned long long)(xx & 1u) << 32 | (uint32_t)~v0);
+    return;
+#endif
+    float p[NB][R];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) {
+          const uint32_t q[4] = {w[r][j].x, w[r][j].y, w[r][j].z, w[r][j].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            acc = fmaf(__uint_as_float(q[e] << 16), hv[b][j][2 * e], acc);
+            acc = fmaf(__uint_as_float(q[e] & 0xFFFF0000u), hv[b][j][2 * e + 1], acc);
+          }
+        }
+        p[b][r] = acc;
+      }
+    // transpose-reduce: after the halving rounds lane holds row `sel` only
+    int sel = 0;
+    int mask = 32;
+#pragma unroll
+    for (int cnt = R; cnt > 1; cnt >>= 1, mask >>= 1) {
+      const int half = cnt >> 1;
+      const bool upper = (lane & mask) != 0;
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+          const float keep = upper ? p[b][i + half] : p[b][i];
+          const float send = upper ? p[b][i] : p[b][i + half];
+          p[b][i] = keep + __shfl_xor(send, mask, 64);
+        }
+      if (upper) sel += half;
+    }
+#pragma unroll
+    for (; mask >= 1; mask >>= 1)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) p[b][0] += __shfl_xor(p[b][0], mask, 64);
+    const int v = v0 + sel;
+    if (v < V) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        if (b >= B) continue;
+        float val = apply_cast(p[b][0], a.reduce_cast);
+        if constexpr (MODE == MODE_SAMPLE) {
+          // every lane of a row group holds the same total; one draws the noise
+          if ((lane & (64 / R - 1)) != 0) continue;
+          if (!greedy_row[b]) val = val / tp[b] + gumbel_at(key[b], (uint32_t)v);
+        }
+        best[b] = max_u64(best[b], argmax_key(val, (uint32_t)v));
+      }
+    }
+  };
+
+  // ring of DEPTH row groups in flight: group i+DEPTH-1 is requested before i is reduced
+  constexpr int DEPTH = NVJSEL_GEMV_DEPTH;
+  const int n_mine = g_end > g_begin ? (g_end - g_begin + g_step - 1) / g_step : 0;
+#if NVJSEL_GEMV_CONTIG == 3
+  // waves advance in lockstep; starting each slice at a different point keeps
+  // simultaneous requests from landing on the same memory channels
+  const int rot = n_mine > 0 ? (gw * 7) % n_mine : 0;
+#else
+  const int rot = 0;
+#endif
+  auto gid = [&](int i) { int k = i + rot; k = k >= n_mine ? k - n_mine : k; return g_begin + k * g_step; };
+  u32x4_t ring[DEPTH][R][KJ];
+#pragma unroll
+  for (int d = 0; d < DEPTH - 1; ++d)
+    if (d < n_mine) load_grp(ring[d], gid(d));
+  for (int i = 0; i < n_mine; ++i) {
+    if (i + DEPTH - 1 < n_mine) load_grp(ring[DEPTH - 1], gid(i + DEPTH - 1));
+    proc_grp(ring[0], gid(i));
+#pragma unroll
+    for (int d = 0; d < DEPTH - 1; ++d)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) ring[d][r][j] = ring[d + 1][r][j];
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    best[b] = wave_max_u64(best[b]);
+    if (lane == 0) red[wave * NB + b] = best[b];
+  }
+  block_commit<WAVES, NB>(red, B, a.row_keys);
   finish_rows(a.row_keys, a.counter, B, a.out_ids, a.out_best);
 }
 
@@ -323,14 +552,14 @@ __global__ void __launch_bounds__(256) lm_head_generic_kernel(LmArgs a) {
 }
 
 // ------------------------------------------------------------------ host side
-static constexpr int kWaves = 8;
+static constexpr int kWaves = NVJSEL_LM_WAVES;
 // LDS reserved for the kernel's static shared variables (finish_rows flag).
 static constexpr size_t kStaticLdsSlack = 256;
 
-template <int WT, int NSPLIT, int NB, int MODE>
-static int launch_mfma(const LmArgs& a, hipStream_t stream) {
-  constexpr int MT = (NB == 1) ? 4 : 2;
-  auto kern = lm_head_mfma_kernel<WT, NSPLIT, NB, MT, kWaves, MODE>;
+template <int WT, int NSPLIT, int NB, int KU, int MODE>
+static int launch_mfma_ku(const LmArgs& a, hipStream_t stream) {
+  constexpr int MT = (NB == 1) ? NVJSEL_LM_MT1 : NVJSEL_LM_MTN;
+  auto kern = lm_head_mfma_kernel<WT, NSPLIT, NB, MT, kWaves, KU, NVJSEL_LM_DEPTH, MODE>;
   size_t lds = (size_t)a.H * NSPLIT * NB * 16 * 2;
   size_t red = (size_t)kWaves * NB * 16 * 8;
   if (lds < red) lds = red;
@@ -341,6 +570,7 @@ static int launch_mfma(const LmArgs& a, hipStream_t stream) {
   int per_cu = 0;
   NVJSEL_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kWaves * 64, lds));
   if (per_cu < 1) per_cu = 1;
+  if (NVJSEL_LM_BPC > 0 && per_cu > NVJSEL_LM_BPC) per_cu = NVJSEL_LM_BPC;
   const int rows = 16 * MT * kWaves;
   const int need = (a.V + rows - 1) / rows;
   int grid = per_cu * device_cu_count();
@@ -348,6 +578,44 @@ static int launch_mfma(const LmArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kWaves * 64), lds, stream, a);
   NVJSEL_CHECK_LAUNCH("lm_head_mfma_kernel");
   return NVJSEL_OK;
+}
+
+// KU must divide the number of 32-wide k-steps; odd hidden sizes use KU = 1.
+template <int WT, int NSPLIT, int NB, int MODE>
+static int launch_mfma(const LmArgs& a, hipStream_t stream) {
+  if (((a.H >> 5) % NVJSEL_LM_KU) == 0) return launch_mfma_ku<WT, NSPLIT, NB, NVJSEL_LM_KU, MODE>(a, stream);
+  return launch_mfma_ku<WT, NSPLIT, NB, 1, MODE>(a, stream);
+}
+
+template <int NB, int KJ, int MODE>
+static int launch_gemv(const LmArgs& a, hipStream_t stream) {
+  constexpr int R = NVJSEL_GEMV_R;
+  auto kern = lm_head_gemv_kernel<NB, R, KJ, MODE>;
+  int per_cu = 0;
+  constexpr int WAVES = NVJSEL_GEMV_WAVES;
+  NVJSEL_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, WAVES * 64, 0));
+  if (per_cu < 1) per_cu = 1;
+  if (NVJSEL_GEMV_BPC > 0 && per_cu > NVJSEL_GEMV_BPC) per_cu = NVJSEL_GEMV_BPC;
+  const int need = (a.V + R * WAVES - 1) / (R * WAVES);
+  int grid = per_cu * device_cu_count() * NVJSEL_GEMV_GRID_NUM / NVJSEL_GEMV_GRID_DEN;
+  if (grid < 1) grid = 1;
+  if (grid > need) grid = need;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(WAVES * 64), 0, stream, a);
+  NVJSEL_CHECK_LAUNCH("lm_head_gemv_kernel");
+  return NVJSEL_OK;
+}
+
+template <int MODE>
+static int dispatch_gemv(const LmArgs& a, hipStream_t s) {
+  const int kj = a.H / 512;
+  if (a.B == 1) {
+    if (kj == 1) return launch_gemv<1, 1, MODE>(a, s);
+    if (kj == 2) return launch_gemv<1, 2, MODE>(a, s);
+    return launch_gemv<1, 4, MODE>(a, s);
+  }
+  if (kj == 1) return launch_gemv<2, 1, MODE>(a, s);
+  if (kj == 2) return launch_gemv<2, 2, MODE>(a, s);
+  return launch_gemv<2, 4, MODE>(a, s);
 }
 
 template <int WT, int NSPLIT, int MODE>
@@ -395,6 +663,8 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   const bool f16_mfma = layout == NVJSEL_W_VH && weight_dtype == NVJSEL_F16 &&
                         hidden_dtype == NVJSEL_F16 && (H % 32) == 0 && aligned;
   const int nsplit = (bf16_mfma && hidden_dtype != NVJSEL_BF16) ? 3 : 1;
+  const bool gemv = layout == NVJSEL_W_VH && weight_dtype == NVJSEL_BF16 && aligned && batch <= 2 &&
+                    (H == 512 || H == 1024 || H == 2048);
   // rows per launch: LDS holds H * nsplit * rows bf16 values
   int chunk = 0;
   if ((bf16_mfma || f16_mfma) && (size_t)H * nsplit * 16 * 2 + kStaticLdsSlack <= device_max_lds_per_block()) {
@@ -406,6 +676,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     if (nsplit == 3 && tiles > 1) tiles = 1;
     chunk = tiles * 16;
   }
+  if (gemv) chunk = 0;
   for (int b0 = 0; b0 < batch; b0 += (chunk > 0 ? chunk : batch)) {
     LmArgs a;
     const int nb = chunk > 0 ? (batch - b0 < chunk ? batch - b0 : chunk) : batch;
@@ -425,7 +696,9 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     a.out_ids = out_ids + b0;
     a.out_best = out_best ? out_best + b0 : nullptr;
     int rc;
-    if (chunk > 0) {
+    if (gemv) {
+      rc = mode == MODE_GREEDY ? dispatch_gemv<MODE_GREEDY>(a, s) : dispatch_gemv<MODE_SAMPLE>(a, s);
+    } else if (chunk > 0) {
       if (f16_mfma)
         rc = mode == MODE_GREEDY ? dispatch_nb<DT_F16, 1, MODE_GREEDY>(a, s) : dispatch_nb<DT_F16, 1, MODE_SAMPLE>(a, s);
       else if (nsplit == 1)

@@ -56,7 +56,7 @@ def test_full_vocab_batch1_with_best_value():
     assert abs(float(best[0]) - sel.round_bf16(np.float32(z[0, i]))) <= 2 ** -7 * abs(z[0, i])
 
 
-@pytest.mark.parametrize("batch", [1, 20])
+@pytest.mark.parametrize("batch", [1, 2, 20])
 def test_f32_hidden_exact_split(batch):
     """f32 activations x bf16 weight: fp32 dot (no logit rounding), as jnp.dot promotes."""
     rng = np.random.default_rng(7 + batch)
@@ -92,22 +92,24 @@ def test_hidden_dim_not_multiple_of_32_uses_generic():
     check_greedy(ids, sel.lm_head_logits(as_f32(h)[:, 0], as_f32(E)), 1, "H=40")
 
 
-def test_ties_resolve_to_lowest_index_across_blocks():
+@pytest.mark.parametrize("H,B", [(256, 2), (512, 2), (512, 1), (1024, 5)])
+def test_ties_resolve_to_lowest_index_across_blocks(H, B):
     """Identical rows far apart in the vocabulary (different blocks/waves)."""
     rng = np.random.default_rng(11)
-    H, V = 256, 70000
+    V = 70000
     Wn = (rng.standard_normal((V, H)) * 0.01).astype(np.float32)
-    h = np.abs(rng.standard_normal((2, H))).astype(np.float32)
+    h = np.abs(rng.standard_normal((B, H))).astype(np.float32)
     hot = np.full(H, 0.5, np.float32)
     for v in (65000, 40000, 12345, 69999):
         Wn[v] = hot
     ids = _run(bf16_tensor(h), bf16_tensor(Wn), weight_layout="vh")
-    assert list(ids) == [12345, 12345]
+    assert list(ids) == [12345] * B
 
 
-def test_nan_logit_wins_first():
+@pytest.mark.parametrize("H", [128, 512, 2048])
+def test_nan_logit_wins_first(H):
     rng = np.random.default_rng(12)
-    H, V = 128, 5000
+    V = 5000
     Wn = (rng.standard_normal((V, H)) * 0.01).astype(np.float32)
     Wn[4000, 3] = np.nan
     Wn[2500, 7] = np.nan
@@ -124,3 +126,17 @@ def test_repeated_calls_reuse_workspace():
         h = bf16_tensor(rng.standard_normal((B, H)))
         ids = _run(h, W, weight_layout="vh")
         check_greedy(ids, sel.lm_head_logits(as_f32(h), as_f32(W)), 1, f"trial{trial}")
+
+
+@pytest.mark.parametrize("H", [512, 1024, 2048])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_streaming_gemv_shapes(H, batch):
+    """The small-batch streaming kernel (H a multiple of 512), odd vocab tail."""
+    rng = np.random.default_rng(H + batch)
+    V = 10007
+    h = bf16_tensor(rng.standard_normal((batch, H)))
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.03)
+    ids, best = nvjsel.lm_head_greedy_top1_hip(h, W, weight_layout="vh", return_best=True)
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(as_f32(h), as_f32(W))
+    check_greedy(ids.cpu().numpy(), z, 1, f"gemv H={H} B={batch}")
