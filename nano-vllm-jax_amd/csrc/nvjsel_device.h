@@ -73,6 +73,18 @@ __device__ __forceinline__ float gumbel_at(const TfKey& k, uint32_t i) {
   return gumbel_from_bits(random_bits32(k, i));
 }
 
+// The same draw with the hardware fp32 log (v_log_f32): within ~2e-5 of
+// gumbel_from_bits over its whole range.  Used only to find the few elements
+// that can be the maximum; the winner is always decided on exact values.
+__device__ __forceinline__ float gumbel_fast_from_bits(uint32_t bits) {
+  float f = __uint_as_float((bits >> 9) | 0x3F800000u) - 1.0f;
+  float u = fmaxf(f + 1.17549435e-38f, 1.17549435e-38f);
+  return -__logf(-__logf(u));
+}
+
+// Upper bound of any Gumbel draw (u = 1 - 2^-23), rounded up.
+#define NVJSEL_GUMBEL_MAX 15.9424f
+
 // ---------------------------------------------------------------- argmax keys
 __device__ __forceinline__ uint32_t ord_f32(float v) {
   uint32_t u = __float_as_uint(v);

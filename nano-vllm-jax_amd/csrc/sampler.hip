@@ -11,54 +11,80 @@
 //   FILTER  T > 0, top-k and/or top-p       kept = {x >= tau}; argmax over kept
 //
 // Kernels, all asynchronous on the caller's stream:
-//   1. scan      grid (chunks, B): GREEDY/FULL rows finish here (64-bit
-//                (value, ~index) key max per chunk -> one atomicMax per
-//                block); FILTER rows record the max of x (with its index, which
-//                is the answer for non-finite rows).
-//   2. threshold grid (B): one 1024-thread block per FILTER row finds tau by
-//                radix descent (11/11/10-bit digits) over the orderable key
-//                of x: first the k-th largest (counts), then the top-p
-//                threshold (masses).  Mass is exp(x - max) in 2^-40 fixed point
-//                summed in 64-bit integers -- exact, order-independent and
-//                deterministic, so the crossing test "mass(x >= v) > p * Z"
-//                is evaluated without accumulation-order noise.
-//   3. gumbel    grid (chunks, B): FILTER rows, elements with key(x) >= tau.
-//   4. finish    ids from the keys; re-zero the accumulators.
+//   1. scan       grid (chunks, B), each block holds an 8192-element chunk in
+//                 registers.  Writes the chunk's (max, ~index) key.  GREEDY rows
+//                 finish here.  FILTER
+//                 rows with 0 < k <= 256 emit a superset of the chunk's top-k:
+//                 every element >= the k-th largest of the 256 per-thread
+//                 maxima (at least k elements reach that value, so the chunk's
+//                 k-th largest is not below it).
+//   2. select     grid (B): FULL rows seed their best score with the exact
+//                 scores of the chunk maxima (a prune level for step 4).
+//                 Small-k FILTER rows: exact top-k over the candidates in
+//                 LDS (radix select), top-p over the survivors (bitonic sort +
+//                 fixed-point mass scan), exact Gumbel-max over what is kept.
+//                 Other FILTER rows (top-p only, k > 256, candidate overflow)
+//                 are marked heavy.
+//   3. threshold  grid (B), heavy rows only: radix descent (11/11/10-bit digits)
+//                 over the whole row for the k-th largest (counts) and the
+//                 top-p crossing (masses).
+//   4. gumbel     grid (chunks, B), FULL rows and heavy rows: Gumbel-max over
+//                 x >= tau (tau = 0 for FULL rows).
+//   5. finish     ids from the keys; re-zero the accumulators.
+//
+// Mass is exp(x - max) in 2^-40 fixed point summed in 64-bit integers -- exact,
+// order-independent and deterministic, so "mass(x >= v) > p * Z" is decided
+// without accumulation-order noise.
+//
+// Gumbel-max with few exact draws: a block computes every score with the
+// hardware fp32 log, takes the block maximum m, then recomputes exactly (fp64
+// logs, one rounding each) only the scores within a margin of m that covers
+// the fast path's error; the winner is the exact maximum.  Elements (and whole
+// chunks) whose x plus the largest possible draw cannot beat the row's best
+// exact score so far are skipped.
 #include "nvjsel_device.h"
 #include "nvjsel_host.h"
 
 namespace nvjsel {
 
 enum { ROW_GREEDY = 0, ROW_FULL = 1, ROW_FILTER = 2 };
-enum { STATE_NEEDS_GUMBEL = 1, STATE_DONE = 2 };
+enum { STATE_DONE = 1, STATE_HEAVY = 2, STATE_NEEDS_GUMBEL = 3 };
 
-static constexpr int kScanThreads = 256;
-static constexpr int kScanPerThread = 16;
-static constexpr int kChunk = kScanThreads * kScanPerThread;  // elements per scan block
-static constexpr int kSelThreads = 1024;
+static constexpr int kThreads = 256;
+static constexpr int kEPT = 32;                    // elements per thread in chunk kernels
+static constexpr int kChunk = kThreads * kEPT;     // 8192 elements per block
+static constexpr int kFastK = 256;                 // top-k resolved from candidates
+static constexpr int kCandCap = 512;               // candidates kept per chunk
+static constexpr int kSelCap = 8192;               // candidates per row held in LDS
+static constexpr int kKeptCap = 2048;              // survivors of top-k sorted for top-p
+static constexpr int kHeavyThreads = 1024;
 
 struct SampleArgs {
   const void* logits;
   int dtype;
   int B;
   int V;
+  int nchunks;
   long long stride;  // elements between rows
   const float* temperature;
   const int32_t* top_k;
   const float* top_p;
   const uint32_t* keys;
   const float* noise;  // optional [B, V] Gumbel override
-  unsigned long long* row_key;
-  uint32_t* row_tau;
-  int32_t* row_state;
+  unsigned long long* row_key;     // [B]   zero at rest
+  uint32_t* row_tau;               // [B]
+  int32_t* row_state;              // [B]
+  unsigned long long* chunk_max;   // [B, nchunks]
+  uint32_t* cand_count;            // [B, nchunks]
+  unsigned long long* cand;        // [B, nchunks, kCandCap]
   int32_t* out_ids;
 };
 
 struct RowParams {
   int mode;
-  float tp;   // max(T, 1e-6), NaN-propagating
-  int k;      // active top-k (0 = off)
-  float p;    // active top-p (1 = off)
+  float tp;  // max(T, 1e-6), NaN-propagating
+  int k;     // active top-k (0 = off)
+  float p;   // active top-p (1 = off)
 };
 
 __device__ __forceinline__ RowParams row_params(const SampleArgs& a, int b) {
@@ -81,13 +107,30 @@ __device__ __forceinline__ float load_logit(const SampleArgs& a, const char* row
   return f16_to_f32(((const uint16_t*)row)[i]);
 }
 
+template <int DT>
+__device__ __forceinline__ float load_logit_t(const char* row, int i) {
+  if constexpr (DT == DT_F32) return ((const float*)row)[i];
+  else if constexpr (DT == DT_BF16) return bf16_to_f32(((const uint16_t*)row)[i]);
+  else return f16_to_f32(((const uint16_t*)row)[i]);
+}
+
 __device__ __forceinline__ const char* row_ptr(const SampleArgs& a, int b) {
   return (const char*)a.logits + (size_t)b * (size_t)a.stride * dtype_size_dev(a.dtype);
 }
 
-__device__ __forceinline__ float noise_at(const SampleArgs& a, int b, const TfKey& key, int i) {
+__device__ __forceinline__ float exact_noise(const SampleArgs& a, int b, const TfKey& key, int i) {
   if (a.noise) return a.noise[(size_t)b * a.V + i];
   return gumbel_at(key, (uint32_t)i);
+}
+
+__device__ __forceinline__ float fast_noise(const SampleArgs& a, int b, const TfKey& key, int i) {
+  if (a.noise) return a.noise[(size_t)b * a.V + i];
+  return gumbel_fast_from_bits(random_bits32(key, (uint32_t)i));
+}
+
+// Inverse of radix_key for non-NaN keys.
+__device__ __forceinline__ float radix_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
 __device__ __forceinline__ uint64_t fixed_mass(float x, float m) {
@@ -96,56 +139,455 @@ __device__ __forceinline__ uint64_t fixed_mass(float x, float m) {
   return (uint64_t)rintf(e * 1099511627776.0f);
 }
 
-// Block max of a 64-bit key; result valid in thread 0.
-template <int THREADS>
+// Block-wide max of a 64-bit key (every thread gets the result).
 __device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v, unsigned long long* sh) {
   v = wave_max_u64(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
   if (lane == 0) sh[wave] = v;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < THREADS / 64; ++w) v = max_u64(v, sh[w]);
+  unsigned long long m = 0;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) m = max_u64(m, sh[w]);
+  return m;
+}
+
+__device__ __forceinline__ unsigned long long load_row_best(const unsigned long long* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Score below which nothing can win: the value of the row's best exact score so far.
+__device__ __forceinline__ float prune_level(unsigned long long best) {
+  if (best == 0) return -INFINITY;
+  const float s = unord_f32((uint32_t)(best >> 32));
+  return (s != s) ? INFINITY : s;  // a NaN score already wins
+}
+
+// The row's prune level, read once by thread 0 so every thread of the block
+// takes the same branches (other blocks keep raising the row's best).
+__device__ __forceinline__ float block_prune_level(const unsigned long long* row_best, float* sh) {
+  __syncthreads();
+  if (threadIdx.x == 0) *sh = prune_level(load_row_best(row_best));
+  __syncthreads();
+  return *sh;
+}
+
+// ------------------------------------------------------------------ element mapping
+// A chunk kernel's thread holds EPT elements as EPT/VEC vectors of VEC
+// contiguous elements (16 bytes); vector q of thread t starts at element
+// base + (q * 256 + t) * VEC, so each load instruction of a wave covers 1 KB.
+template <int VEC>
+__device__ __forceinline__ int elem_index(int base, int j) {
+  return base + ((j / VEC) * kThreads + (int)threadIdx.x) * VEC + (j % VEC);
+}
+
+template <int DT, int VEC>
+__device__ __forceinline__ void load_vec(const char* row, int i0, float* o) {
+  if constexpr (VEC == 1) {
+    o[0] = load_logit_t<DT>(row, i0);
+  } else if constexpr (DT == DT_F32) {
+    static_assert(VEC == 4, "f32 vectors hold 4 elements");
+    const float4 v = *(const float4*)((const float*)row + i0);
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  } else {
+    static_assert(VEC == 8, "16-bit vectors hold 8 elements");
+    const uint4 v = *(const uint4*)((const uint16_t*)row + i0);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if constexpr (DT == DT_BF16) {
+        o[2 * q] = __uint_as_float(w[q] << 16);
+        o[2 * q + 1] = __uint_as_float(w[q] & 0xFFFF0000u);
+      } else {
+        o[2 * q] = f16_to_f32((uint16_t)(w[q] & 0xFFFFu));
+        o[2 * q + 1] = f16_to_f32((uint16_t)(w[q] >> 16));
+      }
+    }
   }
-  return v;
+}
+
+// Loads a thread's EPT elements, divided by tp unless `raw`.  Vectors past
+// the end of the row (V is a multiple of VEC when VEC > 1) reload the last
+// vector and are masked out of `valid`.
+template <int DT, int VEC, int EPT>
+__device__ __forceinline__ void load_chunk_elems(const char* row, int base, int V, bool raw, float tp,
+                                                 float (&x)[EPT], uint32_t& valid) {
+  valid = 0;
+#pragma unroll
+  for (int q = 0; q < EPT / VEC; ++q) {
+    const int i0 = base + (q * kThreads + (int)threadIdx.x) * VEC;
+    const bool ok = i0 < V;
+    load_vec<DT, VEC>(row, ok ? i0 : V - VEC, &x[q * VEC]);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      if (!raw) x[q * VEC + e] = x[q * VEC + e] / tp;
+      valid |= (ok ? 1u : 0u) << (q * VEC + e);
+    }
+  }
+}
+
+// Scratch of the block-level Gumbel-max: exact-rescoring queue.
+static constexpr int kExactCap = 256;
+struct GumbelShared {
+  unsigned long long red[kThreads / 64];
+  float qx[kExactCap];
+  uint32_t qi[kExactCap];
+  uint32_t n;
+  float s_cur;
+};
+
+// Gumbel-max over this thread's elements x[j] (index base + j*256 + tid) whose
+// bit in `act` is set.  Returns the block's exact best key (all threads).  The
+// few near-maximal elements are queued in LDS and rescored exactly by the
+// whole block, so the fp64 path is not unrolled per element.
+template <int EPT, int VEC>
+__device__ __forceinline__ unsigned long long block_gumbel(const SampleArgs& a, int b, const TfKey& key,
+                                                           const float (&x)[EPT], int base, uint32_t act,
+                                                           float s_cur, GumbelShared& sh) {
+  float st[EPT];
+  uint32_t tmax = 0;  // ord of the approximate maximum
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    st[j] = -INFINITY;
+    if (!((act >> j) & 1u)) continue;
+    const float xv = x[j];
+    if (xv + NVJSEL_GUMBEL_MAX < s_cur) {  // cannot beat an exact score already found
+      act &= ~(1u << j);
+      continue;
+    }
+    const int i = elem_index<VEC>(base, j);
+    st[j] = (xv != xv) ? INFINITY : xv + fast_noise(a, b, key, i);
+    const uint32_t o = ord_f32(st[j]);
+    tmax = o > tmax ? o : tmax;
+  }
+  const unsigned long long any = block_max_u64(((unsigned long long)tmax << 32) | (act ? 1u : 0u), sh.red);
+  if ((any & 1ull) == 0 && (any >> 32) == 0) return 0;  // nothing active in the block
+  const float m = unord_f32((uint32_t)(any >> 32));
+  // |fast - exact| <= ~2e-5 on the draw, plus one ulp of the sum
+  const float thr = m - (1e-3f + fabsf(m) * 4.8e-7f);
+  uint32_t cm = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j)
+    if (((act >> j) & 1u) && st[j] >= thr) cm |= 1u << j;
+  unsigned long long best = 0;
+  for (;;) {
+    __syncthreads();
+    if (threadIdx.x == 0) sh.n = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      if (!((cm >> j) & 1u)) continue;
+      const uint32_t slot = atomicAdd(&sh.n, 1u);
+      if (slot < (uint32_t)kExactCap) {
+        sh.qx[slot] = x[j];
+        sh.qi[slot] = (uint32_t)elem_index<VEC>(base, j);
+        cm &= ~(1u << j);
+      }
+    }
+    __syncthreads();
+    const uint32_t n = sh.n;
+    const int lim = n < (uint32_t)kExactCap ? (int)n : kExactCap;
+    for (int e = threadIdx.x; e < lim; e += kThreads) {
+      const uint32_t i = sh.qi[e];
+      const float sc = sh.qx[e] + exact_noise(a, b, key, (int)i);
+      best = max_u64(best, argmax_key(sc, i));
+    }
+    if (n <= (uint32_t)kExactCap) break;
+  }
+  return block_max_u64(best, sh.red);
+}
+
+// ------------------------------------------------------------------ bitonic sort (descending)
+__device__ void bitonic_desc(unsigned long long* v, int n) {  // n: power of two
+  for (int size = 2; size <= n; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      __syncthreads();
+      for (int t = threadIdx.x; t < (n >> 1); t += blockDim.x) {
+        const int lo = 2 * t - (t & (stride - 1));
+        const int hi = lo + stride;
+        const bool desc = ((lo & size) == 0);
+        const unsigned long long x = v[lo], y = v[hi];
+        if ((x < y) == desc) { v[lo] = y; v[hi] = x; }
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// Exclusive prefix sum across the block in thread order (every thread calls);
+// `ws` holds one slot per wave.  Returns the exclusive value and the total.
+template <typename T>
+__device__ __forceinline__ T block_exclusive_scan(T v, T* ws, T& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  T incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    T o;
+    if constexpr (sizeof(T) == 8) {
+      const uint32_t lo = __shfl_up((uint32_t)incl, d, 64), hi = __shfl_up((uint32_t)(incl >> 32), d, 64);
+      o = ((T)hi << 32) | lo;
+    } else {
+      o = __shfl_up(incl, d, 64);
+    }
+    if (lane >= d) incl += o;
+  }
+  __syncthreads();
+  if (lane == 63) ws[wave] = incl;
+  __syncthreads();
+  T before = 0, tot = 0;
+  for (int w = 0; w < nw; ++w) {
+    const T t = ws[w];
+    if (w < wave) before += t;
+    tot += t;
+  }
+  total = tot;
+  return before + incl - v;
 }
 
 // ------------------------------------------------------------------ 1. scan
-__global__ void __launch_bounds__(kScanThreads) sample_scan_kernel(SampleArgs a) {
-  __shared__ unsigned long long sh[kScanThreads / 64];
-  const int b = blockIdx.y;
+struct ScanShared {
+  GumbelShared g;
+  uint32_t hist[256];
+  uint32_t wsum[kThreads / 64];
+  uint32_t sel, rem, cnt;
+};
+
+template <int DT, int VEC>
+__global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
+  __shared__ ScanShared sh;
+  const int b = blockIdx.y, c = blockIdx.x;
   const RowParams rp = row_params(a, b);
   const char* row = row_ptr(a, b);
-  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
-  const int base = blockIdx.x * kChunk;
-  unsigned long long best = 0;
-#pragma unroll 4
-  for (int j = 0; j < kScanPerThread; ++j) {
-    const int i = base + j * kScanThreads + threadIdx.x;
-    if (i < a.V) {
-      const float l = load_logit(a, row, i);
-      float s;
-      if (rp.mode == ROW_GREEDY) s = l;
-      else if (rp.mode == ROW_FULL) s = l / rp.tp + noise_at(a, b, key, i);
-      else s = l / rp.tp;
-      best = max_u64(best, argmax_key(s, (uint32_t)i));
-    }
+  const int base = c * kChunk;
+  float x[kEPT];
+  uint32_t valid;
+  load_chunk_elems<DT, VEC, kEPT>(row, base, a.V, rp.mode == ROW_GREEDY, rp.tp, x, valid);
+  unsigned long long cbest = 0;
+#pragma unroll
+  for (int j = 0; j < kEPT; ++j)
+    cbest = max_u64(cbest, ((valid >> j) & 1u) ? argmax_key(x[j], (uint32_t)elem_index<VEC>(base, j)) : 0ull);
+  cbest = block_max_u64(cbest, sh.g.red);
+  if (threadIdx.x == 0) {
+    a.chunk_max[(size_t)b * a.nchunks + c] = cbest;
+    if (rp.mode == ROW_GREEDY) atomicMax(&a.row_key[b], cbest);
   }
-  best = block_max_u64<kScanThreads>(best, sh);
-  if (threadIdx.x == 0 && best) atomicMax(&a.row_key[b], best);
+  // GREEDY rows are done; FULL rows are drawn by the gumbel kernel
+  if (rp.mode != ROW_FILTER || rp.k == 0 || rp.k > kFastK) return;
+
+  // FILTER with small k: theta = top 16 bits of the k-th largest per-thread
+  // maximum (two 8-bit radix passes); every element >= theta is a candidate.
+  uint32_t tmax = 0;
+#pragma unroll
+  for (int j = 0; j < kEPT; ++j)
+    if ((valid >> j) & 1u) {
+      const uint32_t k = radix_key(x[j]);
+      tmax = k > tmax ? k : tmax;
+    }
+  uint32_t prefix = 0, rem = (uint32_t)rp.k;
+#pragma unroll 1
+  for (int pass = 0; pass < 2; ++pass) {
+    const int shift = pass == 0 ? 24 : 16;
+    __syncthreads();
+    sh.hist[threadIdx.x] = 0;
+    __syncthreads();
+    if (pass == 0 || (tmax >> 24) == (prefix >> 24)) atomicAdd(&sh.hist[(tmax >> shift) & 255u], 1u);
+    __syncthreads();
+    const uint32_t h = sh.hist[255 - threadIdx.x];
+    uint32_t tot;
+    const uint32_t above = block_exclusive_scan<uint32_t>(h, sh.wsum, tot);
+    if (above < rem && rem <= above + h) { sh.sel = prefix | ((uint32_t)(255 - threadIdx.x) << shift); sh.rem = rem - above; }
+    __syncthreads();
+    prefix = sh.sel;
+    rem = sh.rem;
+  }
+  const uint32_t theta = prefix;
+  if (threadIdx.x == 0) sh.cnt = 0;
+  __syncthreads();
+  unsigned long long* out = a.cand + ((size_t)b * a.nchunks + c) * kCandCap;
+#pragma unroll
+  for (int j = 0; j < kEPT; ++j)
+    if ((valid >> j) & 1u) {
+      const uint32_t k = radix_key(x[j]);
+      if (k >= theta) {
+        const uint32_t slot = atomicAdd(&sh.cnt, 1u);
+        if (slot < (uint32_t)kCandCap) out[slot] = ((unsigned long long)k << 32) | (uint32_t)elem_index<VEC>(base, j);
+      }
+    }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    a.cand_count[(size_t)b * a.nchunks + c] = sh.cnt > (uint32_t)kCandCap ? kCandCap + 1 : sh.cnt;
 }
 
-// ------------------------------------------------------------------ 2. threshold
-struct SelShared {
+// ------------------------------------------------------------------ 2. select
+struct SelectShared {
+  unsigned long long cand[kSelCap];
+  unsigned long long kept[kKeptCap];
+  unsigned long long red[kThreads / 64];
+  uint32_t hist[256];
+  uint32_t off[1025];
+  uint32_t wsum32[kThreads / 64];
+  unsigned long long wsum64[kThreads / 64];
+  uint32_t n, nk;
+  uint32_t prefix, rem;
+  int flag;
+};
+
+// k-th largest high word among v[0..n), counting multiplicity (4 passes of 8
+// bits; thread t owns digit 255 - t, so one block scan finds each digit).
+__device__ uint32_t lds_kth_largest(SelectShared& s, const unsigned long long* v, int n, uint32_t k) {
+  uint32_t prefix = 0, mask = 0, rem = k;
+  for (int sh = 24; sh >= 0; sh -= 8) {
+    s.hist[threadIdx.x] = 0;
+    __syncthreads();
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+      const uint32_t kk = (uint32_t)(v[e] >> 32);
+      if ((kk & mask) == prefix) atomicAdd(&s.hist[(kk >> sh) & 255u], 1u);
+    }
+    __syncthreads();
+    const uint32_t h = s.hist[255 - threadIdx.x];
+    uint32_t tot;
+    const uint32_t above = block_exclusive_scan<uint32_t>(h, s.wsum32, tot);
+    if (above < rem && rem <= above + h) { s.prefix = prefix | ((uint32_t)(255 - threadIdx.x) << sh); s.rem = rem - above; }
+    __syncthreads();
+    prefix = s.prefix;
+    rem = s.rem;
+    mask |= 255u << sh;
+  }
+  return prefix;
+}
+
+__global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
+  __shared__ SelectShared s;
+  const int b = blockIdx.x;
+  const RowParams rp = row_params(a, b);
+  if (rp.mode == ROW_GREEDY) return;
+  const int NC = a.nchunks;
+  if (rp.mode == ROW_FULL) {
+    // seed the row's best with the exact scores of the chunk maxima: a prune
+    // level for the gumbel kernel before any of its blocks has run
+    const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+    unsigned long long best = 0;
+    for (int c = threadIdx.x; c < NC; c += blockDim.x) {
+      const unsigned long long ck = a.chunk_max[(size_t)b * NC + c];
+      const uint32_t i = ~(uint32_t)ck;
+      const float xv = unord_f32((uint32_t)(ck >> 32));
+      best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
+    }
+    best = block_max_u64(best, s.red);
+    if (threadIdx.x == 0) a.row_key[b] = best;
+    return;
+  }
+  unsigned long long mk = 0;
+  for (int c = threadIdx.x; c < NC; c += blockDim.x) mk = max_u64(mk, a.chunk_max[(size_t)b * NC + c]);
+  mk = block_max_u64(mk, s.red);
+  const float m = unord_f32((uint32_t)(mk >> 32));
+  if (!isfinite(m)) {  // NaN / +inf / all -inf: the first maximum is the answer
+    if (threadIdx.x == 0) { a.row_key[b] = mk; a.row_state[b] = STATE_DONE; }
+    return;
+  }
+  bool fast = rp.k > 0 && rp.k <= kFastK && NC < 1024;
+  if (fast) {
+    // candidate counts -> offsets (thread t owns chunks 4t..4t+3)
+    uint32_t cnt[4], local = 0;
+    int bad = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = threadIdx.x * 4 + q;
+      cnt[q] = c < NC ? a.cand_count[(size_t)b * NC + c] : 0u;
+      bad |= cnt[q] > (uint32_t)kCandCap;
+      local += cnt[q];
+    }
+    uint32_t tot;
+    uint32_t o = block_exclusive_scan<uint32_t>(local, s.wsum32, tot);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = threadIdx.x * 4 + q;
+      if (c <= NC) s.off[c] = o;
+      o += cnt[q];
+    }
+    const int anybad = __syncthreads_or(bad);
+    fast = !anybad && tot <= (uint32_t)kSelCap;
+  }
+  if (!fast) {
+    if (threadIdx.x == 0) a.row_state[b] = STATE_HEAVY;
+    return;
+  }
+  const int n = (int)s.off[NC];
+  for (int c = 0; c < NC; ++c) {
+    const int o = (int)s.off[c], cnt = (int)s.off[c + 1] - o;
+    const unsigned long long* src = a.cand + ((size_t)b * NC + c) * kCandCap;
+    for (int e = threadIdx.x; e < cnt; e += blockDim.x) s.cand[o + e] = src[e];
+  }
+  __syncthreads();
+  // exact top-k threshold
+  const uint32_t tk = lds_kth_largest(s, s.cand, n, (uint32_t)rp.k);
+  if (threadIdx.x == 0) s.nk = 0;
+  __syncthreads();
+  for (int e = threadIdx.x; e < n; e += blockDim.x) {
+    if ((uint32_t)(s.cand[e] >> 32) >= tk) {
+      const uint32_t slot = atomicAdd(&s.nk, 1u);
+      if (slot < (uint32_t)kKeptCap) s.kept[slot] = s.cand[e];
+    }
+  }
+  __syncthreads();
+  const int nk = (int)s.nk;
+  if (nk > kKeptCap) {  // too many ties at the k-th value for the LDS path
+    if (threadIdx.x == 0) a.row_state[b] = STATE_HEAVY;
+    return;
+  }
+  uint32_t tau = tk;
+  if (rp.p < 1.0f) {
+    int np2 = 1;
+    while (np2 < nk) np2 <<= 1;
+    for (int e = nk + threadIdx.x; e < np2; e += blockDim.x) s.kept[e] = 0;
+    bitonic_desc(s.kept, np2);
+    // inclusive prefix of masses in sorted order: thread t owns [t*per, (t+1)*per)
+    const int per = (nk + kThreads - 1) / kThreads;
+    const int e0 = threadIdx.x * per;
+    unsigned long long local = 0;
+    for (int e = e0; e < e0 + per && e < nk; ++e) local += fixed_mass(radix_value((uint32_t)(s.kept[e] >> 32)), m);
+    unsigned long long run;
+    unsigned long long cum = block_exclusive_scan<unsigned long long>(local, s.wsum64, run);
+    double pz = floor((double)rp.p * (double)run);
+    if (!(pz >= 0.0)) pz = 0.0;
+    unsigned long long P = (unsigned long long)pz;
+    if (run > 0 && P > run - 1) P = run - 1;
+    const unsigned long long target = P + 1;  // first cumulative mass >= P + 1
+    if (threadIdx.x == 0) s.flag = -1;
+    __syncthreads();
+    for (int e = e0; e < e0 + per && e < nk; ++e) {
+      const unsigned long long nc = cum + fixed_mass(radix_value((uint32_t)(s.kept[e] >> 32)), m);
+      if (cum < target && nc >= target) s.flag = e;
+      cum = nc;
+    }
+    __syncthreads();
+    const int jstar = s.flag >= 0 ? s.flag : nk - 1;
+    tau = (uint32_t)(s.kept[jstar] >> 32);
+  }
+  // exact Gumbel-max over the survivors
+  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+  unsigned long long best = 0;
+  for (int e = threadIdx.x; e < nk; e += blockDim.x) {
+    const unsigned long long ce = s.kept[e];
+    const uint32_t kk = (uint32_t)(ce >> 32);
+    if (kk < tau) continue;
+    const uint32_t i = (uint32_t)ce;
+    const float sc = radix_value(kk) + exact_noise(a, b, key, (int)i);
+    best = max_u64(best, argmax_key(sc, i));
+  }
+  best = block_max_u64(best, s.red);
+  if (threadIdx.x == 0) { a.row_key[b] = best; a.row_state[b] = STATE_DONE; }
+}
+
+// ------------------------------------------------------------------ 3. heavy threshold
+struct HeavyShared {
   unsigned long long hist[2048];
-  unsigned long long wave_tot[kSelThreads / 64];
+  unsigned long long wave_tot[kHeavyThreads / 64];
   unsigned long long res_above;
   unsigned long long total;
   uint32_t res_digit;
 };
 
-// Inclusive prefix sum across the block (thread order); returns inclusive
-// value, writes the block total to s.total.
-__device__ __forceinline__ unsigned long long block_inclusive_scan(unsigned long long v, SelShared& s) {
+__device__ __forceinline__ unsigned long long heavy_inclusive_scan(unsigned long long v, HeavyShared& s) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -157,7 +599,7 @@ __device__ __forceinline__ unsigned long long block_inclusive_scan(unsigned long
   __syncthreads();
   if (threadIdx.x == 0) {
     unsigned long long run = 0;
-    for (int w = 0; w < kSelThreads / 64; ++w) {
+    for (int w = 0; w < kHeavyThreads / 64; ++w) {
       unsigned long long t = s.wave_tot[w];
       s.wave_tot[w] = run;
       run += t;
@@ -168,14 +610,13 @@ __device__ __forceinline__ unsigned long long block_inclusive_scan(unsigned long
   return v + s.wave_tot[wave];
 }
 
-// First digit d, scanning from the top, whose cumulative sum (bins >= d)
-// reaches `target`; writes d and the sum of bins above d.
-__device__ __forceinline__ void find_desc(SelShared& s, int nbins, unsigned long long target) {
-  const int per = nbins / kSelThreads;  // 1 or 2
-  const int j0 = threadIdx.x * per;     // descending position
+// First digit d from the top whose cumulative weight (bins >= d) reaches target.
+__device__ __forceinline__ void heavy_find_desc(HeavyShared& s, int nbins, unsigned long long target) {
+  const int per = nbins / kHeavyThreads;
+  const int j0 = threadIdx.x * per;
   unsigned long long local = 0;
   for (int q = 0; q < per; ++q) local += s.hist[nbins - 1 - (j0 + q)];
-  const unsigned long long incl = block_inclusive_scan(local, s);
+  const unsigned long long incl = heavy_inclusive_scan(local, s);
   const unsigned long long excl = incl - local;
   if (excl < target && target <= incl) {
     unsigned long long cum = excl;
@@ -192,22 +633,21 @@ __device__ __forceinline__ void find_desc(SelShared& s, int nbins, unsigned long
   __syncthreads();
 }
 
-// Radix descent for the largest key v with weight(key >= v, key >= low) >= target
-// where weight is a count (MASS=false) or fixed-point mass (MASS=true).  For
-// MASS the target is derived from the pass-1 total Z: floor(p * Z) + 1.
+// Largest key v with weight(key >= v, key >= low) >= target; weight is a count
+// (MASS=false) or fixed-point mass (MASS=true, target = floor(p * Z) + 1).
 template <bool MASS>
 __device__ uint32_t radix_descend(const SampleArgs& a, const char* row, float tp, float m,
-                                  uint32_t low, unsigned long long target, float p, SelShared& s) {
+                                  uint32_t low, unsigned long long target, float p, HeavyShared& s) {
   uint32_t prefix = 0;
   const int shifts[3] = {21, 10, 0};
   const int widths[3] = {11, 11, 10};
 #pragma unroll 1
   for (int pass = 0; pass < 3; ++pass) {
     const int sh = shifts[pass], nb = 1 << widths[pass];
-    const int top = sh + widths[pass];  // bits above this digit are fixed by prefix
-    for (int d = threadIdx.x; d < nb; d += kSelThreads) s.hist[d] = 0;
+    const int top = sh + widths[pass];
+    for (int d = threadIdx.x; d < nb; d += kHeavyThreads) s.hist[d] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < a.V; i += kSelThreads) {
+    for (int i = threadIdx.x; i < a.V; i += kHeavyThreads) {
       const float x = load_logit(a, row, i) / tp;
       const uint32_t key = radix_key(x);
       if (key < low) continue;
@@ -217,19 +657,18 @@ __device__ uint32_t radix_descend(const SampleArgs& a, const char* row, float tp
     }
     __syncthreads();
     if (MASS && pass == 0) {
-      // pass 1 sees every survivor: its total is Z
       unsigned long long local = 0;
-      for (int d = threadIdx.x; d < nb; d += kSelThreads) local += s.hist[d];
-      block_inclusive_scan(local, s);
+      for (int d = threadIdx.x; d < nb; d += kHeavyThreads) local += s.hist[d];
+      heavy_inclusive_scan(local, s);
       const unsigned long long Z = s.total;
       double pz = floor((double)p * (double)Z);
-      if (!(pz >= 0.0)) pz = 0.0;  // p <= 0 or NaN keeps only the maximum
+      if (!(pz >= 0.0)) pz = 0.0;
       unsigned long long P = (unsigned long long)pz;
       if (P > Z - 1) P = Z - 1;
       target = P + 1;
       __syncthreads();
     }
-    find_desc(s, nb, target);
+    heavy_find_desc(s, nb, target);
     target -= s.res_above;
     prefix |= s.res_digit << sh;
     __syncthreads();
@@ -237,53 +676,78 @@ __device__ uint32_t radix_descend(const SampleArgs& a, const char* row, float tp
   return prefix;
 }
 
-__global__ void __launch_bounds__(kSelThreads) sample_threshold_kernel(SampleArgs a) {
-  __shared__ SelShared s;
+__global__ void __launch_bounds__(kHeavyThreads) sample_threshold_kernel(SampleArgs a) {
+  __shared__ HeavyShared s;
   const int b = blockIdx.x;
   const RowParams rp = row_params(a, b);
   if (rp.mode != ROW_FILTER) return;
-  const unsigned long long k0 = a.row_key[b];
-  const float m = unord_f32((uint32_t)(k0 >> 32));
-  if (!isfinite(m)) {  // NaN / +inf / all -inf: the max key already holds the answer
-    if (threadIdx.x == 0) a.row_state[b] = STATE_DONE;
-    return;
-  }
+  if (a.row_state[b] != STATE_HEAVY) return;
+  unsigned long long mk = 0;
+  for (int c = threadIdx.x; c < a.nchunks; c += blockDim.x) mk = max_u64(mk, a.chunk_max[(size_t)b * a.nchunks + c]);
+  mk = wave_max_u64(mk);
+  if ((threadIdx.x & 63) == 0) s.wave_tot[threadIdx.x >> 6] = mk;
+  __syncthreads();
+  mk = 0;
+  for (int w = 0; w < kHeavyThreads / 64; ++w) mk = max_u64(mk, s.wave_tot[w]);
+  __syncthreads();
+  const float m = unord_f32((uint32_t)(mk >> 32));
   const char* row = row_ptr(a, b);
   uint32_t thr = 0;
   if (rp.k > 0) thr = radix_descend<false>(a, row, rp.tp, m, 0u, (unsigned long long)rp.k, 1.0f, s);
   if (rp.p < 1.0f) thr = radix_descend<true>(a, row, rp.tp, m, thr, 1ull, rp.p, s);
+  // seed the row's best with the exact scores of the kept chunk maxima
+  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+  unsigned long long best = 0;
+  for (int c = threadIdx.x; c < a.nchunks; c += blockDim.x) {
+    const unsigned long long ck = a.chunk_max[(size_t)b * a.nchunks + c];
+    const float xv = unord_f32((uint32_t)(ck >> 32));
+    if (radix_key(xv) < thr) continue;
+    const uint32_t i = ~(uint32_t)ck;
+    best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
+  }
+  best = wave_max_u64(best);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) s.wave_tot[threadIdx.x >> 6] = best;
+  __syncthreads();
   if (threadIdx.x == 0) {
+    for (int w = 0; w < kHeavyThreads / 64; ++w) best = max_u64(best, s.wave_tot[w]);
+    a.row_key[b] = best;
     a.row_tau[b] = thr;
-    a.row_key[b] = 0;
     a.row_state[b] = STATE_NEEDS_GUMBEL;
   }
 }
 
-// ------------------------------------------------------------------ 3. gumbel over kept
-__global__ void __launch_bounds__(kScanThreads) sample_gumbel_kernel(SampleArgs a) {
-  __shared__ unsigned long long sh[kScanThreads / 64];
-  const int b = blockIdx.y;
+// ------------------------------------------------------------------ 4. gumbel over kept (heavy rows)
+// A block covers a quarter chunk (2048 elements): four times the blocks of
+// the scan, for rows that need the VALU-heavy noise.
+static constexpr int kGumbelEPT = 8;
+static constexpr int kGumbelSplit = kEPT / kGumbelEPT;
+
+template <int DT, int VEC>
+__global__ void __launch_bounds__(kThreads) sample_gumbel_kernel(SampleArgs a) {
+  __shared__ GumbelShared sh;
+  const int b = blockIdx.y, sub = blockIdx.x, c = sub / kGumbelSplit;
   const RowParams rp = row_params(a, b);
-  if (rp.mode != ROW_FILTER) return;
-  if (a.row_state[b] != STATE_NEEDS_GUMBEL) return;
-  const uint32_t tau = a.row_tau[b];
+  if (rp.mode == ROW_GREEDY) return;
+  if (rp.mode == ROW_FILTER && a.row_state[b] != STATE_NEEDS_GUMBEL) return;
+  const float s_cur = block_prune_level(&a.row_key[b], &sh.s_cur);
+  const float cmax = unord_f32((uint32_t)(a.chunk_max[(size_t)b * a.nchunks + c] >> 32));
+  if (cmax + NVJSEL_GUMBEL_MAX < s_cur) return;  // the whole chunk is out of reach
+  const uint32_t tau = rp.mode == ROW_FILTER ? a.row_tau[b] : 0u;
   const char* row = row_ptr(a, b);
+  const int base = sub * (kThreads * kGumbelEPT);
+  float x[kGumbelEPT];
+  uint32_t valid;
+  load_chunk_elems<DT, VEC, kGumbelEPT>(row, base, a.V, false, rp.tp, x, valid);
+  uint32_t act = 0;
+#pragma unroll
+  for (int j = 0; j < kGumbelEPT; ++j) act |= (((valid >> j) & 1u) && radix_key(x[j]) >= tau ? 1u : 0u) << j;
   const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
-  const int base = blockIdx.x * kChunk;
-  unsigned long long best = 0;
-#pragma unroll 4
-  for (int j = 0; j < kScanPerThread; ++j) {
-    const int i = base + j * kScanThreads + threadIdx.x;
-    if (i < a.V) {
-      const float x = load_logit(a, row, i) / rp.tp;
-      if (radix_key(x) >= tau) best = max_u64(best, argmax_key(x + noise_at(a, b, key, i), (uint32_t)i));
-    }
-  }
-  best = block_max_u64<kScanThreads>(best, sh);
+  const unsigned long long best = block_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, act, s_cur, sh);
   if (threadIdx.x == 0 && best) atomicMax(&a.row_key[b], best);
 }
 
-// ------------------------------------------------------------------ 4. finish
+// ------------------------------------------------------------------ 5. finish
 __global__ void sample_finish_kernel(SampleArgs a) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= a.B) return;
@@ -292,17 +756,31 @@ __global__ void sample_finish_kernel(SampleArgs a) {
   a.row_key[b] = 0;
 }
 
-static size_t ws_off_tau(int B) { return align_up((size_t)B * 8, 256); }
-static size_t ws_off_state(int B) { return ws_off_tau(B) + align_up((size_t)B * 4, 256); }
+struct WsLayout {
+  size_t row_key, row_tau, row_state, chunk_max, cand_count, cand, total;
+};
+
+static WsLayout ws_layout(int B, int V) {
+  const size_t nc = (size_t)((V + kChunk - 1) / kChunk);
+  WsLayout w;
+  size_t o = 0;
+  w.row_key = o;    o += align_up((size_t)B * 8, 256);
+  w.row_tau = o;    o += align_up((size_t)B * 4, 256);
+  w.row_state = o;  o += align_up((size_t)B * 4, 256);
+  w.chunk_max = o;  o += align_up((size_t)B * nc * 8, 256);
+  w.cand_count = o; o += align_up((size_t)B * nc * 4, 256);
+  w.cand = o;       o += align_up((size_t)B * nc * kCandCap * 8, 256);
+  w.total = o;
+  return w;
+}
 
 }  // namespace nvjsel
 
 using namespace nvjsel;
 
 extern "C" size_t nvjsel_sample_workspace_size(int batch, int vocab) {
-  (void)vocab;
-  if (batch <= 0) return 0;
-  return ws_off_state(batch) + align_up((size_t)batch * 4, 256);
+  if (batch <= 0 || vocab <= 0) return 0;
+  return ws_layout(batch, vocab).total;
 }
 
 extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab, int64_t row_stride,
@@ -325,31 +803,56 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
     return NVJSEL_EWORKSPACE;
   }
   if (batch > 65535) return fail(NVJSEL_EUNSUPPORTED, "sample: batch > 65535");
+  const WsLayout w = ws_layout(batch, vocab);
+  char* ws = (char*)workspace;
   SampleArgs a;
   a.logits = logits;
   a.dtype = dtype;
   a.B = batch;
   a.V = vocab;
+  a.nchunks = (vocab + kChunk - 1) / kChunk;
   a.stride = row_stride;
   a.temperature = temperature;
   a.top_k = top_k;
   a.top_p = top_p;
   a.keys = keys;
   a.noise = noise;
-  a.row_key = (unsigned long long*)workspace;
-  a.row_tau = (uint32_t*)((char*)workspace + ws_off_tau(batch));
-  a.row_state = (int32_t*)((char*)workspace + ws_off_state(batch));
+  a.row_key = (unsigned long long*)(ws + w.row_key);
+  a.row_tau = (uint32_t*)(ws + w.row_tau);
+  a.row_state = (int32_t*)(ws + w.row_state);
+  a.chunk_max = (unsigned long long*)(ws + w.chunk_max);
+  a.cand_count = (uint32_t*)(ws + w.cand_count);
+  a.cand = (unsigned long long*)(ws + w.cand);
   a.out_ids = out_ids;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid_scan((vocab + kChunk - 1) / kChunk, batch);
-  hipLaunchKernelGGL(sample_scan_kernel, grid_scan, dim3(kScanThreads), 0, s, a);
-  NVJSEL_CHECK_LAUNCH("sample_scan_kernel");
+  const dim3 grid_chunks(a.nchunks, batch);
+  const size_t esz = dtype_size(dtype);
+  const int vec = (int)(16 / esz);
+  const bool vec_ok = (vocab % vec) == 0 && (row_stride % vec) == 0 && (((uintptr_t)logits) & 15) == 0;
+  const dim3 grid_gumbel(a.nchunks * kGumbelSplit, batch);
+#define NVJSEL_LAUNCH_CHUNK(KERN, GRID)                                                          \
+  do {                                                                                          \
+    if (dtype == NVJSEL_F32) {                                                                  \
+      if (vec_ok) hipLaunchKernelGGL((KERN<DT_F32, 4>), GRID, dim3(kThreads), 0, s, a);         \
+      else hipLaunchKernelGGL((KERN<DT_F32, 1>), GRID, dim3(kThreads), 0, s, a);                \
+    } else if (dtype == NVJSEL_BF16) {                                                          \
+      if (vec_ok) hipLaunchKernelGGL((KERN<DT_BF16, 8>), GRID, dim3(kThreads), 0, s, a);        \
+      else hipLaunchKernelGGL((KERN<DT_BF16, 1>), GRID, dim3(kThreads), 0, s, a);               \
+    } else {                                                                                    \
+      if (vec_ok) hipLaunchKernelGGL((KERN<DT_F16, 8>), GRID, dim3(kThreads), 0, s, a);         \
+      else hipLaunchKernelGGL((KERN<DT_F16, 1>), GRID, dim3(kThreads), 0, s, a);                \
+    }                                                                                           \
+    NVJSEL_CHECK_LAUNCH(#KERN);                                                                 \
+  } while (0)
+  NVJSEL_LAUNCH_CHUNK(sample_scan_kernel, grid_chunks);
+  hipLaunchKernelGGL(sample_select_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+  NVJSEL_CHECK_LAUNCH("sample_select_kernel");
   if (top_k || top_p) {
-    hipLaunchKernelGGL(sample_threshold_kernel, dim3(batch), dim3(kSelThreads), 0, s, a);
+    hipLaunchKernelGGL(sample_threshold_kernel, dim3(batch), dim3(kHeavyThreads), 0, s, a);
     NVJSEL_CHECK_LAUNCH("sample_threshold_kernel");
-    hipLaunchKernelGGL(sample_gumbel_kernel, grid_scan, dim3(kScanThreads), 0, s, a);
-    NVJSEL_CHECK_LAUNCH("sample_gumbel_kernel");
   }
+  NVJSEL_LAUNCH_CHUNK(sample_gumbel_kernel, grid_gumbel);
+#undef NVJSEL_LAUNCH_CHUNK
   hipLaunchKernelGGL(sample_finish_kernel, dim3((batch + 255) / 256), dim3(256), 0, s, a);
   NVJSEL_CHECK_LAUNCH("sample_finish_kernel");
   return NVJSEL_OK;

@@ -172,3 +172,22 @@ def test_repeated_calls_leave_workspace_clean():
         P = [float(x) for x in rng.choice([1.0, 0.8], B)]
         ids, used, keys = _sample(l, T, top_k=K, top_p=P)
         check_sampled(ids, used, T, K, P, keys, ctx=f"trial{trial}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_strided_rows_and_unaligned_vocab(dtype):
+    """Rows taken from a wider buffer (row stride > V) and V not a multiple of
+    the 16-byte vector: the scalar-load variants."""
+    rng = np.random.default_rng(10)
+    B, V, W = 5, 9001, 9016
+    full = (rng.standard_normal((B, W)) * 2).astype(np.float32)
+    lt = torch.from_numpy(full).to(dtype).cuda()[:, :V]
+    assert lt.stride(0) == W
+    keys = engine_keys(B, 3)
+    T, K, P = [0.0, 0.8, 1.0, 0.5, 1.2], [0, 0, 30, 5, 0], [1.0, 1.0, 0.9, 1.0, 0.7]
+    out = nvjsel.sample_token_ids(
+        lt, torch.tensor(T, dtype=torch.float32).cuda(), keys_tensor(keys),
+        top_k=torch.tensor(K, dtype=torch.int32).cuda(), top_p=torch.tensor(P, dtype=torch.float32).cuda())
+    torch.cuda.synchronize()
+    used = lt.float().cpu().numpy()
+    check_sampled(out.cpu().numpy(), used, T, K, P, keys, ctx="strided")
