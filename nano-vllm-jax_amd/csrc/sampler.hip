@@ -21,8 +21,9 @@
 //   2. select     grid (B): FULL rows seed their best score with the exact
 //                 scores of the chunk maxima (a prune level for step 4).
 //                 Small-k FILTER rows: exact top-k over the candidates in
-//                 LDS (radix select), top-p over the survivors (bitonic sort +
-//                 fixed-point mass scan), exact Gumbel-max over what is kept.
+//                 LDS (radix select), top-p over the survivors (radix descent
+//                 weighted by fixed-point mass), exact Gumbel-max over what is
+//                 kept.
 //                 Other FILTER rows (top-p only, k > 256, candidate overflow)
 //                 are marked heavy.
 //   3. threshold  grid (B), heavy rows only: radix descent (11/11/10-bit digits)
@@ -48,7 +49,7 @@
 namespace nvjsel {
 
 enum { ROW_GREEDY = 0, ROW_FULL = 1, ROW_FILTER = 2 };
-enum { STATE_DONE = 1, STATE_HEAVY = 2, STATE_NEEDS_GUMBEL = 3 };
+enum { STATE_DONE = 1, STATE_HEAVY = 2, STATE_NEEDS_GUMBEL = 3, STATE_TOPP = 4 };
 
 static constexpr int kThreads = 256;
 static constexpr int kEPT = 32;                    // elements per thread in chunk kernels
@@ -58,6 +59,9 @@ static constexpr int kCandCap = 512;               // candidates kept per chunk
 static constexpr int kSelCap = 8192;               // candidates per row held in LDS
 static constexpr int kKeptCap = 2048;              // survivors of top-k sorted for top-p
 static constexpr int kHeavyThreads = 1024;
+static constexpr int kToppBins = 1024;             // 1/32-nat mass bins below the row max
+static constexpr float kToppBinScale = 32.0f;
+static constexpr int kToppCap = 8192;              // elements of the crossing bin
 
 struct SampleArgs {
   const void* logits;
@@ -77,6 +81,10 @@ struct SampleArgs {
   unsigned long long* chunk_max;   // [B, nchunks]
   uint32_t* cand_count;            // [B, nchunks]
   unsigned long long* cand;        // [B, nchunks, kCandCap]
+  float* row_m;                    // [B]   max of x (top-p rows)
+  unsigned long long* topp_hist;   // [B, kToppBins] zero at rest
+  unsigned long long* topp_cand;   // [B, kToppCap]
+  uint32_t* topp_n;                // [B]   zero at rest
   int32_t* out_ids;
 };
 
@@ -296,23 +304,6 @@ __device__ __forceinline__ unsigned long long block_gumbel(const SampleArgs& a, 
   return block_max_u64(best, sh.red);
 }
 
-// ------------------------------------------------------------------ bitonic sort (descending)
-__device__ void bitonic_desc(unsigned long long* v, int n) {  // n: power of two
-  for (int size = 2; size <= n; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      __syncthreads();
-      for (int t = threadIdx.x; t < (n >> 1); t += blockDim.x) {
-        const int lo = 2 * t - (t & (stride - 1));
-        const int hi = lo + stride;
-        const bool desc = ((lo & size) == 0);
-        const unsigned long long x = v[lo], y = v[hi];
-        if ((x < y) == desc) { v[lo] = y; v[hi] = x; }
-      }
-    }
-  }
-  __syncthreads();
-}
-
 // Exclusive prefix sum across the block in thread order (every thread calls);
 // `ws` holds one slot per wave.  Returns the exclusive value and the total.
 template <typename T>
@@ -366,10 +357,7 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   for (int j = 0; j < kEPT; ++j)
     cbest = max_u64(cbest, ((valid >> j) & 1u) ? argmax_key(x[j], (uint32_t)elem_index<VEC>(base, j)) : 0ull);
   cbest = block_max_u64(cbest, sh.g.red);
-  if (threadIdx.x == 0) {
-    a.chunk_max[(size_t)b * a.nchunks + c] = cbest;
-    if (rp.mode == ROW_GREEDY) atomicMax(&a.row_key[b], cbest);
-  }
+  if (threadIdx.x == 0) a.chunk_max[(size_t)b * a.nchunks + c] = cbest;
   // GREEDY rows are done; FULL rows are drawn by the gumbel kernel
   if (rp.mode != ROW_FILTER || rp.k == 0 || rp.k > kFastK) return;
 
@@ -418,34 +406,33 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
 }
 
 // ------------------------------------------------------------------ 2. select
-struct SelectShared {
-  unsigned long long cand[kSelCap];
-  unsigned long long kept[kKeptCap];
-  unsigned long long red[kThreads / 64];
-  uint32_t hist[256];
-  uint32_t off[1025];
-  uint32_t wsum32[kThreads / 64];
-  unsigned long long wsum64[kThreads / 64];
-  uint32_t n, nk;
-  uint32_t prefix, rem;
-  int flag;
+// Largest high word K among v[0..n) with weight(entries >= K) >= target:
+// weight 1 (MASS = false: the target-th largest, counting multiplicity) or
+// fixed-point mass exp(value - m) (MASS = true).  Four passes of 8 bits; thread
+// t owns digit 255 - t, so one block scan finds each digit.
+struct DescShared {
+  unsigned long long hist[256];
+  unsigned long long wsum[kThreads / 64];
+  uint32_t prefix;
+  unsigned long long rem;
 };
 
-// k-th largest high word among v[0..n), counting multiplicity (4 passes of 8
-// bits; thread t owns digit 255 - t, so one block scan finds each digit).
-__device__ uint32_t lds_kth_largest(SelectShared& s, const unsigned long long* v, int n, uint32_t k) {
-  uint32_t prefix = 0, mask = 0, rem = k;
+template <bool MASS>
+__device__ uint32_t lds_desc(DescShared& s, const unsigned long long* v, int n, unsigned long long target, float m) {
+  uint32_t prefix = 0, mask = 0;
+  unsigned long long rem = target;
   for (int sh = 24; sh >= 0; sh -= 8) {
     s.hist[threadIdx.x] = 0;
     __syncthreads();
     for (int e = threadIdx.x; e < n; e += blockDim.x) {
       const uint32_t kk = (uint32_t)(v[e] >> 32);
-      if ((kk & mask) == prefix) atomicAdd(&s.hist[(kk >> sh) & 255u], 1u);
+      if ((kk & mask) == prefix)
+        atomicAdd(&s.hist[(kk >> sh) & 255u], MASS ? (unsigned long long)fixed_mass(radix_value(kk), m) : 1ull);
     }
     __syncthreads();
-    const uint32_t h = s.hist[255 - threadIdx.x];
-    uint32_t tot;
-    const uint32_t above = block_exclusive_scan<uint32_t>(h, s.wsum32, tot);
+    const unsigned long long h = s.hist[255 - threadIdx.x];
+    unsigned long long tot;
+    const unsigned long long above = block_exclusive_scan<unsigned long long>(h, s.wsum, tot);
     if (above < rem && rem <= above + h) { s.prefix = prefix | ((uint32_t)(255 - threadIdx.x) << sh); s.rem = rem - above; }
     __syncthreads();
     prefix = s.prefix;
@@ -455,11 +442,32 @@ __device__ uint32_t lds_kth_largest(SelectShared& s, const unsigned long long* v
   return prefix;
 }
 
+// floor(p * Z) + 1, clamped to [1, Z]: the cumulative mass that must be reached.
+__device__ __forceinline__ unsigned long long topp_target(float p, unsigned long long Z) {
+  double pz = floor((double)p * (double)Z);
+  if (!(pz >= 0.0)) pz = 0.0;
+  unsigned long long P = (unsigned long long)pz;
+  if (Z > 0 && P > Z - 1) P = Z - 1;
+  return P + 1;
+}
+
+struct SelectShared {
+  unsigned long long cand[kSelCap];
+  unsigned long long kept[kKeptCap];
+  unsigned long long red[kThreads / 64];
+  DescShared d;
+  uint32_t off[1025];
+  uint32_t wsum32[kThreads / 64];
+  unsigned long long wsum64[kThreads / 64];
+  uint32_t n, nk;
+  uint32_t prefix, rem;
+  int flag;
+};
+
 __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
   __shared__ SelectShared s;
   const int b = blockIdx.x;
   const RowParams rp = row_params(a, b);
-  if (rp.mode == ROW_GREEDY) return;
   const int NC = a.nchunks;
   if (rp.mode == ROW_FULL) {
     // seed the row's best with the exact scores of the chunk maxima: a prune
@@ -479,6 +487,10 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
   unsigned long long mk = 0;
   for (int c = threadIdx.x; c < NC; c += blockDim.x) mk = max_u64(mk, a.chunk_max[(size_t)b * NC + c]);
   mk = block_max_u64(mk, s.red);
+  if (rp.mode == ROW_GREEDY) {  // the row's first maximum
+    if (threadIdx.x == 0) a.row_key[b] = mk;
+    return;
+  }
   const float m = unord_f32((uint32_t)(mk >> 32));
   if (!isfinite(m)) {  // NaN / +inf / all -inf: the first maximum is the answer
     if (threadIdx.x == 0) { a.row_key[b] = mk; a.row_state[b] = STATE_DONE; }
@@ -508,18 +520,29 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     fast = !anybad && tot <= (uint32_t)kSelCap;
   }
   if (!fast) {
-    if (threadIdx.x == 0) a.row_state[b] = STATE_HEAVY;
+    const bool topp_only = rp.k == 0 && rp.p < 1.0f;
+    if (topp_only) {  // the histogram pass accumulates into these
+      for (int d = threadIdx.x; d < kToppBins; d += blockDim.x) a.topp_hist[(size_t)b * kToppBins + d] = 0;
+      if (threadIdx.x == 0) a.topp_n[b] = 0;
+    }
+    if (threadIdx.x == 0) {
+      a.row_state[b] = topp_only ? STATE_TOPP : STATE_HEAVY;
+      a.row_m[b] = m;
+    }
     return;
   }
   const int n = (int)s.off[NC];
-  for (int c = 0; c < NC; ++c) {
-    const int o = (int)s.off[c], cnt = (int)s.off[c + 1] - o;
-    const unsigned long long* src = a.cand + ((size_t)b * NC + c) * kCandCap;
-    for (int e = threadIdx.x; e < cnt; e += blockDim.x) s.cand[o + e] = src[e];
+  for (int e = threadIdx.x; e < n; e += blockDim.x) {
+    int lo = 0, hi = NC;  // chunk c with off[c] <= e < off[c + 1]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if ((int)s.off[mid] <= e) lo = mid; else hi = mid;
+    }
+    s.cand[e] = a.cand[((size_t)b * NC + lo) * kCandCap + (e - (int)s.off[lo])];
   }
   __syncthreads();
   // exact top-k threshold
-  const uint32_t tk = lds_kth_largest(s, s.cand, n, (uint32_t)rp.k);
+  const uint32_t tk = lds_desc<false>(s.d, s.cand, n, (unsigned long long)rp.k, 0.0f);
   if (threadIdx.x == 0) s.nk = 0;
   __syncthreads();
   for (int e = threadIdx.x; e < n; e += blockDim.x) {
@@ -536,32 +559,11 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
   }
   uint32_t tau = tk;
   if (rp.p < 1.0f) {
-    int np2 = 1;
-    while (np2 < nk) np2 <<= 1;
-    for (int e = nk + threadIdx.x; e < np2; e += blockDim.x) s.kept[e] = 0;
-    bitonic_desc(s.kept, np2);
-    // inclusive prefix of masses in sorted order: thread t owns [t*per, (t+1)*per)
-    const int per = (nk + kThreads - 1) / kThreads;
-    const int e0 = threadIdx.x * per;
     unsigned long long local = 0;
-    for (int e = e0; e < e0 + per && e < nk; ++e) local += fixed_mass(radix_value((uint32_t)(s.kept[e] >> 32)), m);
-    unsigned long long run;
-    unsigned long long cum = block_exclusive_scan<unsigned long long>(local, s.wsum64, run);
-    double pz = floor((double)rp.p * (double)run);
-    if (!(pz >= 0.0)) pz = 0.0;
-    unsigned long long P = (unsigned long long)pz;
-    if (run > 0 && P > run - 1) P = run - 1;
-    const unsigned long long target = P + 1;  // first cumulative mass >= P + 1
-    if (threadIdx.x == 0) s.flag = -1;
-    __syncthreads();
-    for (int e = e0; e < e0 + per && e < nk; ++e) {
-      const unsigned long long nc = cum + fixed_mass(radix_value((uint32_t)(s.kept[e] >> 32)), m);
-      if (cum < target && nc >= target) s.flag = e;
-      cum = nc;
-    }
-    __syncthreads();
-    const int jstar = s.flag >= 0 ? s.flag : nk - 1;
-    tau = (uint32_t)(s.kept[jstar] >> 32);
+    for (int e = threadIdx.x; e < nk; e += blockDim.x) local += fixed_mass(radix_value((uint32_t)(s.kept[e] >> 32)), m);
+    unsigned long long Z;
+    block_exclusive_scan<unsigned long long>(local, s.wsum64, Z);
+    tau = lds_desc<true>(s.d, s.kept, nk, topp_target(rp.p, Z), m);
   }
   // exact Gumbel-max over the survivors
   const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
@@ -576,6 +578,132 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
   }
   best = block_max_u64(best, s.red);
   if (threadIdx.x == 0) { a.row_key[b] = best; a.row_state[b] = STATE_DONE; }
+}
+
+// ------------------------------------------------------------------ 2b. top-p rows (no top-k)
+// mass(x >= v) is found in two steps: a histogram of masses over 1/32-nat
+// bins below the row max (bins are monotone in x, equal values share a bin),
+// then an exact scan of the one bin where the cumulative mass crosses
+// floor(p * Z) + 1.
+
+__device__ __forceinline__ int topp_bin(float x, float m) {
+  const float d = (m - x) * kToppBinScale;
+  return d < (float)(kToppBins - 1) ? (int)d : kToppBins - 1;
+}
+
+struct ToppShared {
+  unsigned long long hist[kToppBins];
+  unsigned long long wsum[kThreads / 64];
+  uint32_t bin;
+  unsigned long long target;
+};
+
+template <int DT, int VEC>
+__global__ void __launch_bounds__(kThreads) sample_topp_hist_kernel(SampleArgs a) {
+  __shared__ ToppShared sh;
+  const int b = blockIdx.y, c = blockIdx.x;
+  const RowParams rp = row_params(a, b);
+  if (rp.mode != ROW_FILTER || a.row_state[b] != STATE_TOPP) return;
+  const float m = a.row_m[b];
+  for (int d = threadIdx.x; d < kToppBins; d += kThreads) sh.hist[d] = 0;
+  __syncthreads();
+  float x[kEPT];
+  uint32_t valid;
+  load_chunk_elems<DT, VEC, kEPT>(row_ptr(a, b), c * kChunk, a.V, false, rp.tp, x, valid);
+#pragma unroll
+  for (int j = 0; j < kEPT; ++j) {
+    if (!((valid >> j) & 1u)) continue;
+    const uint64_t w = fixed_mass(x[j], m);
+    if (w) atomicAdd(&sh.hist[topp_bin(x[j], m)], (unsigned long long)w);
+  }
+  __syncthreads();
+  unsigned long long* gh = a.topp_hist + (size_t)b * kToppBins;
+  for (int d = threadIdx.x; d < kToppBins; d += kThreads)
+    if (sh.hist[d]) atomicAdd(&gh[d], sh.hist[d]);
+}
+
+// Crossing bin of the row's histogram and the mass still needed inside it.
+__device__ __forceinline__ void topp_crossing(const unsigned long long* gh, float p, ToppShared& sh) {
+  constexpr int PER = kToppBins / kThreads;
+  unsigned long long h[PER], local = 0;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) { h[q] = gh[threadIdx.x * PER + q]; local += h[q]; }
+  unsigned long long Z;
+  unsigned long long cum = block_exclusive_scan<unsigned long long>(local, sh.wsum, Z);
+  const unsigned long long target = topp_target(p, Z);
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    if (cum < target && target <= cum + h[q]) {
+      sh.bin = (uint32_t)(threadIdx.x * PER + q);
+      sh.target = target - cum;
+    }
+    cum += h[q];
+  }
+  __syncthreads();
+}
+
+template <int DT, int VEC>
+__global__ void __launch_bounds__(kThreads) sample_topp_collect_kernel(SampleArgs a) {
+  __shared__ ToppShared sh;
+  const int b = blockIdx.y, c = blockIdx.x;
+  const RowParams rp = row_params(a, b);
+  if (rp.mode != ROW_FILTER || a.row_state[b] != STATE_TOPP) return;
+  const float m = a.row_m[b];
+  topp_crossing(a.topp_hist + (size_t)b * kToppBins, rp.p, sh);
+  const int bin = (int)sh.bin;
+  float x[kEPT];
+  uint32_t valid;
+  const int base = c * kChunk;
+  load_chunk_elems<DT, VEC, kEPT>(row_ptr(a, b), base, a.V, false, rp.tp, x, valid);
+#pragma unroll
+  for (int j = 0; j < kEPT; ++j) {
+    if (!((valid >> j) & 1u)) continue;
+    if (topp_bin(x[j], m) != bin) continue;
+    const uint32_t slot = atomicAdd(&a.topp_n[b], 1u);
+    if (slot < (uint32_t)kToppCap)
+      a.topp_cand[(size_t)b * kToppCap + slot] =
+          ((unsigned long long)radix_key(x[j]) << 32) | (uint32_t)elem_index<VEC>(base, j);
+  }
+}
+
+struct ToppFinalShared {
+  ToppShared t;
+  DescShared d;
+  unsigned long long v[kToppCap];
+};
+
+__global__ void __launch_bounds__(kThreads) sample_topp_final_kernel(SampleArgs a) {
+  __shared__ ToppFinalShared sh;
+  const int b = blockIdx.x;
+  const RowParams rp = row_params(a, b);
+  if (rp.mode != ROW_FILTER || a.row_state[b] != STATE_TOPP) return;
+  const float m = a.row_m[b];
+  topp_crossing(a.topp_hist + (size_t)b * kToppBins, rp.p, sh.t);
+  const unsigned long long target = sh.t.target;
+  const uint32_t n = a.topp_n[b];
+  if (n > (uint32_t)kToppCap) {  // crossing bin too crowded: exact radix path
+    if (threadIdx.x == 0) a.row_state[b] = STATE_HEAVY;
+    return;
+  }
+  for (int e = threadIdx.x; e < (int)n; e += kThreads) sh.v[e] = a.topp_cand[(size_t)b * kToppCap + e];
+  __syncthreads();
+  const uint32_t tau = lds_desc<true>(sh.d, sh.v, (int)n, target, m);
+  // seed the row's best with the exact scores of the kept chunk maxima
+  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+  unsigned long long best = 0;
+  for (int c = threadIdx.x; c < a.nchunks; c += kThreads) {
+    const unsigned long long ck = a.chunk_max[(size_t)b * a.nchunks + c];
+    const float xv = unord_f32((uint32_t)(ck >> 32));
+    if (radix_key(xv) < tau) continue;
+    const uint32_t i = ~(uint32_t)ck;
+    best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
+  }
+  best = block_max_u64(best, sh.t.wsum);
+  if (threadIdx.x == 0) {
+    a.row_key[b] = best;
+    a.row_tau[b] = tau;
+    a.row_state[b] = STATE_NEEDS_GUMBEL;
+  }
 }
 
 // ------------------------------------------------------------------ 3. heavy threshold
@@ -753,11 +881,10 @@ __global__ void sample_finish_kernel(SampleArgs a) {
   if (b >= a.B) return;
   const unsigned long long k = a.row_key[b];
   a.out_ids[b] = (int32_t)(~(uint32_t)k);
-  a.row_key[b] = 0;
 }
 
 struct WsLayout {
-  size_t row_key, row_tau, row_state, chunk_max, cand_count, cand, total;
+  size_t row_key, row_tau, row_state, chunk_max, cand_count, cand, row_m, topp_hist, topp_cand, topp_n, total;
 };
 
 static WsLayout ws_layout(int B, int V) {
@@ -770,6 +897,10 @@ static WsLayout ws_layout(int B, int V) {
   w.chunk_max = o;  o += align_up((size_t)B * nc * 8, 256);
   w.cand_count = o; o += align_up((size_t)B * nc * 4, 256);
   w.cand = o;       o += align_up((size_t)B * nc * kCandCap * 8, 256);
+  w.row_m = o;      o += align_up((size_t)B * 4, 256);
+  w.topp_hist = o;  o += align_up((size_t)B * kToppBins * 8, 256);
+  w.topp_cand = o;  o += align_up((size_t)B * kToppCap * 8, 256);
+  w.topp_n = o;     o += align_up((size_t)B * 4, 256);
   w.total = o;
   return w;
 }
@@ -823,6 +954,10 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   a.chunk_max = (unsigned long long*)(ws + w.chunk_max);
   a.cand_count = (uint32_t*)(ws + w.cand_count);
   a.cand = (unsigned long long*)(ws + w.cand);
+  a.row_m = (float*)(ws + w.row_m);
+  a.topp_hist = (unsigned long long*)(ws + w.topp_hist);
+  a.topp_cand = (unsigned long long*)(ws + w.topp_cand);
+  a.topp_n = (uint32_t*)(ws + w.topp_n);
   a.out_ids = out_ids;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid_chunks(a.nchunks, batch);
@@ -847,6 +982,12 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   NVJSEL_LAUNCH_CHUNK(sample_scan_kernel, grid_chunks);
   hipLaunchKernelGGL(sample_select_kernel, dim3(batch), dim3(kThreads), 0, s, a);
   NVJSEL_CHECK_LAUNCH("sample_select_kernel");
+  if (top_p) {
+    NVJSEL_LAUNCH_CHUNK(sample_topp_hist_kernel, grid_chunks);
+    NVJSEL_LAUNCH_CHUNK(sample_topp_collect_kernel, grid_chunks);
+    hipLaunchKernelGGL(sample_topp_final_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+    NVJSEL_CHECK_LAUNCH("sample_topp_final_kernel");
+  }
   if (top_k || top_p) {
     hipLaunchKernelGGL(sample_threshold_kernel, dim3(batch), dim3(kHeavyThreads), 0, s, a);
     NVJSEL_CHECK_LAUNCH("sample_threshold_kernel");
