@@ -138,31 +138,11 @@ __device__ __forceinline__ uint32_t f16_bits(float v) {
   return b;
 }
 
-// Last block to arrive converts the per-row keys into ids and re-zeroes the
-// accumulators and the ticket counter for the next call.
-__device__ __forceinline__ void finish_rows(unsigned long long* row_keys, unsigned int* counter,
-                                            int B, int32_t* out_ids, float* out_best) {
-  __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned int t = atomicAdd(counter, 1u);
-    s_last = (t == gridDim.x - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  for (int b = threadIdx.x; b < B; b += blockDim.x) {
-    unsigned long long k =
-        __hip_atomic_load(&row_keys[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    out_ids[b] = (int32_t)(~(uint32_t)k);
-    if (out_best) out_best[b] = unord_f32((uint32_t)(k >> 32));
-    __hip_atomic_store(&row_keys[b], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Block-wide max of per-(wave, row) keys held in LDS, then one atomic per row.
+// Each thread waits for its atomics to be performed (their returned values
+// feed an opaque use) before the block barrier, so the ticket taken after the
+// barrier is ordered after every max of the block -- no release fence, which
+// on gfx950 writes back and invalidates the XCD's L2.
 template <int WAVES, int BP>
 __device__ __forceinline__ void block_commit(unsigned long long* red, int B,
                                              unsigned long long* row_keys) {
@@ -171,8 +151,30 @@ __device__ __forceinline__ void block_commit(unsigned long long* red, int B,
     unsigned long long m = 0;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) m = max_u64(m, red[w * BP + b]);
-    if (m) atomicMax(&row_keys[b], m);
+    if (m) (void)after(atomicMax(&row_keys[b], m));
   }
+}
+
+// Last block to arrive converts the per-row keys into ids and re-zeroes the
+// accumulators and the ticket counter for the next call.
+__device__ __forceinline__ void finish_rows(unsigned long long* row_keys, unsigned int* counter,
+                                            int B, int32_t* out_ids, float* out_best) {
+  __shared__ int s_last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned int t = atomicAdd(counter, 1u);
+    s_last = (t == gridDim.x - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    unsigned long long k =
+        __hip_atomic_load(&row_keys[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    out_ids[b] = (int32_t)(~(uint32_t)k);
+    if (out_best) out_best[b] = unord_f32((uint32_t)(k >> 32));
+    __hip_atomic_store(&row_keys[b], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------------ MFMA kernel
@@ -544,7 +546,7 @@ __global__ void __launch_bounds__(256) lm_head_generic_kernel(LmArgs a) {
     for (int bb = threadIdx.x; bb < nb; bb += blockDim.x) {
       unsigned long long m = 0;
       for (int w = 0; w < 4; ++w) m = max_u64(m, red[w * 64 + bb]);
-      if (m) atomicMax(&a.row_keys[b0 + bb], m);
+      if (m) (void)after(atomicMax(&a.row_keys[b0 + bb], m));
     }
     __syncthreads();
   }

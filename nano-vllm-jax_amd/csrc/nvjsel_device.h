@@ -131,6 +131,17 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return v;
 }
 
+// An opaque 0 that the compiler must compute from `v`: placed in the address of
+// a later atomic it makes that atomic wait for the value `v` returned by an
+// earlier one.  Device-scope atomics are performed at the device-wide
+// coherence point, so "returned" means "performed": this orders two atomics
+// without a release fence (which on gfx950 writes back the XCD's L2).
+__device__ __forceinline__ uint32_t after(uint64_t v) {
+  uint32_t z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z) : "v"((uint32_t)v), "v"((uint32_t)(v >> 32)));
+  return z;
+}
+
 // ---------------------------------------------------------------- number formats
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 

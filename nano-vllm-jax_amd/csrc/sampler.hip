@@ -58,7 +58,6 @@ static constexpr int kFastK = 256;                 // top-k resolved from candid
 static constexpr int kCandCap = 512;               // candidates kept per chunk
 static constexpr int kSelCap = 8192;               // candidates per row held in LDS
 static constexpr int kKeptCap = 2048;              // survivors of top-k sorted for top-p
-static constexpr int kHeavyThreads = 1024;
 static constexpr int kToppBins = 1024;             // 1/32-nat mass bins below the row max
 static constexpr float kToppBinScale = 32.0f;
 static constexpr int kToppCap = 8192;              // elements of the crossing bin
@@ -84,9 +83,19 @@ struct SampleArgs {
   float* row_m;                    // [B]   max of x (top-p rows)
   unsigned long long* topp_hist;   // [B, kToppBins] zero at rest
   unsigned long long* topp_cand;   // [B, kToppCap]
-  uint32_t* topp_n;                // [B]   zero at rest
+  uint32_t* topp_n;                // [B]
+  uint32_t* list_n;                // [2]   rows queued for gumbel, for top-p
+  uint32_t* list_gumbel;           // [B]
+  uint32_t* row_done;              // [B]   gumbel items finished per row
+  uint32_t* list_topp;             // [B]
   int32_t* out_ids;
 };
+
+
+__device__ __forceinline__ void queue_row(uint32_t* n, uint32_t* list, int b) {
+  const uint32_t slot = atomicAdd(n, 1u);
+  list[slot] = (uint32_t)b;
+}
 
 struct RowParams {
   int mode;
@@ -349,27 +358,38 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   const RowParams rp = row_params(a, b);
   const char* row = row_ptr(a, b);
   const int base = c * kChunk;
-  float x[kEPT];
+  // Raw logits: x = l / T' is monotone in l, so maxima and the candidate test
+  // run on l and only candidates pay for the division.
+  float l[kEPT];
   uint32_t valid;
-  load_chunk_elems<DT, VEC, kEPT>(row, base, a.V, rp.mode == ROW_GREEDY, rp.tp, x, valid);
-  unsigned long long cbest = 0;
+  load_chunk_elems<DT, VEC, kEPT>(row, base, a.V, true, 1.0f, l, valid);
+  // first maximum with plain float compares: ties keep the earlier index and
+  // -0 == +0; NaN compares false, so the first NaN is tracked on its own
+  float bv = -INFINITY;
+  int bi = -1, ni = -1;
 #pragma unroll
-  for (int j = 0; j < kEPT; ++j)
-    cbest = max_u64(cbest, ((valid >> j) & 1u) ? argmax_key(x[j], (uint32_t)elem_index<VEC>(base, j)) : 0ull);
-  cbest = block_max_u64(cbest, sh.g.red);
-  if (threadIdx.x == 0) a.chunk_max[(size_t)b * a.nchunks + c] = cbest;
-  // GREEDY rows are done; FULL rows are drawn by the gumbel kernel
+  for (int j = 0; j < kEPT; ++j) {
+    const bool ok = (valid >> j) & 1u;
+    const float v = l[j];
+    const int i = elem_index<VEC>(base, j);
+    if (ok && (v > bv || bi < 0)) { bv = v; bi = i; }
+    if (ok && v != v && ni < 0) ni = i;
+  }
+  if (ni >= 0) { bv = __uint_as_float(0x7FFFFFFFu); bi = ni; }
+  // (the first valid element seeds the maximum, so an all -inf chunk keeps index 0)
+  const unsigned long long tkey = bi >= 0 ? argmax_key(bv, (uint32_t)bi) : 0ull;
+  const unsigned long long cbest = block_max_u64(tkey, sh.g.red);
+  if (threadIdx.x == 0) {
+    a.chunk_max[(size_t)b * a.nchunks + c] = cbest;
+    if (c == 0) a.row_done[b] = 0;
+    if (b == 0 && c == 0) { a.list_n[0] = 0; a.list_n[1] = 0; }  // this call's work lists
+  }
   if (rp.mode != ROW_FILTER || rp.k == 0 || rp.k > kFastK) return;
+  const uint32_t bo = bi >= 0 ? ord_f32(bv) : 0u;
 
   // FILTER with small k: theta = top 16 bits of the k-th largest per-thread
-  // maximum (two 8-bit radix passes); every element >= theta is a candidate.
-  uint32_t tmax = 0;
-#pragma unroll
-  for (int j = 0; j < kEPT; ++j)
-    if ((valid >> j) & 1u) {
-      const uint32_t k = radix_key(x[j]);
-      tmax = k > tmax ? k : tmax;
-    }
+  // maximum (two 8-bit radix passes), less a margin of 8 orderable units for
+  // values the division by T' may merge; every element >= theta is a candidate.
   uint32_t prefix = 0, rem = (uint32_t)rp.k;
 #pragma unroll 1
   for (int pass = 0; pass < 2; ++pass) {
@@ -377,7 +397,7 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
     __syncthreads();
     sh.hist[threadIdx.x] = 0;
     __syncthreads();
-    if (pass == 0 || (tmax >> 24) == (prefix >> 24)) atomicAdd(&sh.hist[(tmax >> shift) & 255u], 1u);
+    if (pass == 0 || (bo >> 24) == (prefix >> 24)) atomicAdd(&sh.hist[(bo >> shift) & 255u], 1u);
     __syncthreads();
     const uint32_t h = sh.hist[255 - threadIdx.x];
     uint32_t tot;
@@ -387,22 +407,28 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
     prefix = sh.sel;
     rem = sh.rem;
   }
-  const uint32_t theta = prefix;
+  const uint32_t theta = prefix > 8u ? prefix - 8u : 0u;
+  // keys below ord(-inf) = 0x007FFFFF are NaN patterns: clamp to -inf
+  const float theta_v = theta > 0x007FFFFFu ? radix_value(theta) : -INFINITY;
   if (threadIdx.x == 0) sh.cnt = 0;
   __syncthreads();
   unsigned long long* out = a.cand + ((size_t)b * a.nchunks + c) * kCandCap;
 #pragma unroll
   for (int j = 0; j < kEPT; ++j)
-    if ((valid >> j) & 1u) {
-      const uint32_t k = radix_key(x[j]);
-      if (k >= theta) {
-        const uint32_t slot = atomicAdd(&sh.cnt, 1u);
-        if (slot < (uint32_t)kCandCap) out[slot] = ((unsigned long long)k << 32) | (uint32_t)elem_index<VEC>(base, j);
-      }
+    if (((valid >> j) & 1u) && l[j] >= theta_v) {
+      const uint32_t slot = atomicAdd(&sh.cnt, 1u);
+      if (slot < (uint32_t)kCandCap)
+        out[slot] = ((unsigned long long)radix_key(l[j] / rp.tp) << 32) | (uint32_t)elem_index<VEC>(base, j);
     }
   __syncthreads();
   if (threadIdx.x == 0)
     a.cand_count[(size_t)b * a.nchunks + c] = sh.cnt > (uint32_t)kCandCap ? kCandCap + 1 : sh.cnt;
+}
+
+// Value of a chunk-max key in the row's x space (the keys hold raw logits).
+__device__ __forceinline__ float chunk_max_x(const RowParams& rp, unsigned long long ck) {
+  const float l = unord_f32((uint32_t)(ck >> 32));
+  return rp.mode == ROW_GREEDY ? l : l / rp.tp;
 }
 
 // ------------------------------------------------------------------ 2. select
@@ -419,16 +445,43 @@ struct DescShared {
 
 template <bool MASS>
 __device__ uint32_t lds_desc(DescShared& s, const unsigned long long* v, int n, unsigned long long target, float m) {
-  uint32_t prefix = 0, mask = 0;
+  // bytes shared by every key need no pass
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0;
+  for (int e = threadIdx.x; e < n; e += blockDim.x) {
+    const uint32_t kk = (uint32_t)(v[e] >> 32);
+    kmin = kk < kmin ? kk : kmin;
+    kmax = kk > kmax ? kk : kmax;
+  }
+  kmax = (uint32_t)(block_max_u64(kmax, s.wsum));
+  kmin = ~(uint32_t)(block_max_u64(~kmin, s.wsum));
+  if (kmin == kmax) return kmax;
+  int top = 24;
+  while (top > 0 && ((kmin ^ kmax) >> top) == 0) top -= 8;
+  const uint32_t common_mask = top >= 24 ? 0u : (0xFFFFFFFFu << (top + 8));
+  uint32_t prefix = kmax & common_mask, mask = common_mask;
   unsigned long long rem = target;
-  for (int sh = 24; sh >= 0; sh -= 8) {
+  // each thread walks a contiguous run of entries and flushes its running sum
+  // only when the digit changes: equal keys do not pile onto one LDS address
+  const int per = (n + (int)blockDim.x - 1) / (int)blockDim.x;
+  const int e0 = threadIdx.x * per, e1 = min(n, e0 + per);
+  for (int sh = top; sh >= 0; sh -= 8) {
     s.hist[threadIdx.x] = 0;
     __syncthreads();
-    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+    int cur = -1;
+    unsigned long long acc = 0;
+    for (int e = e0; e < e1; ++e) {
       const uint32_t kk = (uint32_t)(v[e] >> 32);
-      if ((kk & mask) == prefix)
-        atomicAdd(&s.hist[(kk >> sh) & 255u], MASS ? (unsigned long long)fixed_mass(radix_value(kk), m) : 1ull);
+      if ((kk & mask) != prefix) continue;
+      const int d = (int)((kk >> sh) & 255u);
+      const unsigned long long w = MASS ? (unsigned long long)fixed_mass(radix_value(kk), m) : 1ull;
+      if (d != cur) {
+        if (cur >= 0 && acc) atomicAdd(&s.hist[cur], acc);
+        cur = d;
+        acc = 0;
+      }
+      acc += w;
     }
+    if (cur >= 0 && acc) atomicAdd(&s.hist[cur], acc);
     __syncthreads();
     const unsigned long long h = s.hist[255 - threadIdx.x];
     unsigned long long tot;
@@ -477,23 +530,37 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     for (int c = threadIdx.x; c < NC; c += blockDim.x) {
       const unsigned long long ck = a.chunk_max[(size_t)b * NC + c];
       const uint32_t i = ~(uint32_t)ck;
-      const float xv = unord_f32((uint32_t)(ck >> 32));
+      const float xv = chunk_max_x(rp, ck);
       best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
     }
     best = block_max_u64(best, s.red);
-    if (threadIdx.x == 0) a.row_key[b] = best;
+    if (threadIdx.x == 0) {
+      a.row_key[b] = best;
+      queue_row(&a.list_n[0], a.list_gumbel, b);
+    }
     return;
   }
   unsigned long long mk = 0;
   for (int c = threadIdx.x; c < NC; c += blockDim.x) mk = max_u64(mk, a.chunk_max[(size_t)b * NC + c]);
   mk = block_max_u64(mk, s.red);
   if (rp.mode == ROW_GREEDY) {  // the row's first maximum
-    if (threadIdx.x == 0) a.row_key[b] = mk;
+    if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)mk);
     return;
   }
-  const float m = unord_f32((uint32_t)(mk >> 32));
+  const float ml = unord_f32((uint32_t)(mk >> 32));
+  const float m = ml / rp.tp;
   if (!isfinite(m)) {  // NaN / +inf / all -inf: the first maximum is the answer
-    if (threadIdx.x == 0) { a.row_key[b] = mk; a.row_state[b] = STATE_DONE; }
+    unsigned long long ans = mk;
+    if (m > 0.0f && ml == ml) {
+      // x = +inf: finite logits may overflow to +inf too, so find the first
+      // index whose x is +inf (T' is tiny and the logits huge; never hot)
+      const char* row = row_ptr(a, b);
+      unsigned long long first = 0;
+      for (int i = threadIdx.x; i < a.V; i += blockDim.x)
+        if (load_logit(a, row, i) / rp.tp == INFINITY) first = max_u64(first, argmax_key(INFINITY, (uint32_t)i));
+      ans = block_max_u64(first, s.red);
+    }
+    if (threadIdx.x == 0) { a.out_ids[b] = (int32_t)(~(uint32_t)ans); a.row_state[b] = STATE_DONE; }
     return;
   }
   bool fast = rp.k > 0 && rp.k <= kFastK && NC < 1024;
@@ -528,6 +595,7 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     if (threadIdx.x == 0) {
       a.row_state[b] = topp_only ? STATE_TOPP : STATE_HEAVY;
       a.row_m[b] = m;
+      if (topp_only) queue_row(&a.list_n[1], a.list_topp, b);
     }
     return;
   }
@@ -577,176 +645,29 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     best = max_u64(best, argmax_key(sc, i));
   }
   best = block_max_u64(best, s.red);
-  if (threadIdx.x == 0) { a.row_key[b] = best; a.row_state[b] = STATE_DONE; }
+  if (threadIdx.x == 0) { a.out_ids[b] = (int32_t)(~(uint32_t)best); a.row_state[b] = STATE_DONE; }
 }
 
-// ------------------------------------------------------------------ 2b. top-p rows (no top-k)
-// mass(x >= v) is found in two steps: a histogram of masses over 1/32-nat
-// bins below the row max (bins are monotone in x, equal values share a bin),
-// then an exact scan of the one bin where the cumulative mass crosses
-// floor(p * Z) + 1.
-
-__device__ __forceinline__ int topp_bin(float x, float m) {
-  const float d = (m - x) * kToppBinScale;
-  return d < (float)(kToppBins - 1) ? (int)d : kToppBins - 1;
-}
-
-struct ToppShared {
-  unsigned long long hist[kToppBins];
-  unsigned long long wsum[kThreads / 64];
-  uint32_t bin;
-  unsigned long long target;
-};
-
-template <int DT, int VEC>
-__global__ void __launch_bounds__(kThreads) sample_topp_hist_kernel(SampleArgs a) {
-  __shared__ ToppShared sh;
-  const int b = blockIdx.y, c = blockIdx.x;
-  const RowParams rp = row_params(a, b);
-  if (rp.mode != ROW_FILTER || a.row_state[b] != STATE_TOPP) return;
-  const float m = a.row_m[b];
-  for (int d = threadIdx.x; d < kToppBins; d += kThreads) sh.hist[d] = 0;
-  __syncthreads();
-  float x[kEPT];
-  uint32_t valid;
-  load_chunk_elems<DT, VEC, kEPT>(row_ptr(a, b), c * kChunk, a.V, false, rp.tp, x, valid);
-#pragma unroll
-  for (int j = 0; j < kEPT; ++j) {
-    if (!((valid >> j) & 1u)) continue;
-    const uint64_t w = fixed_mass(x[j], m);
-    if (w) atomicAdd(&sh.hist[topp_bin(x[j], m)], (unsigned long long)w);
-  }
-  __syncthreads();
-  unsigned long long* gh = a.topp_hist + (size_t)b * kToppBins;
-  for (int d = threadIdx.x; d < kToppBins; d += kThreads)
-    if (sh.hist[d]) atomicAdd(&gh[d], sh.hist[d]);
-}
-
-// Crossing bin of the row's histogram and the mass still needed inside it.
-__device__ __forceinline__ void topp_crossing(const unsigned long long* gh, float p, ToppShared& sh) {
-  constexpr int PER = kToppBins / kThreads;
-  unsigned long long h[PER], local = 0;
-#pragma unroll
-  for (int q = 0; q < PER; ++q) { h[q] = gh[threadIdx.x * PER + q]; local += h[q]; }
-  unsigned long long Z;
-  unsigned long long cum = block_exclusive_scan<unsigned long long>(local, sh.wsum, Z);
-  const unsigned long long target = topp_target(p, Z);
-#pragma unroll
-  for (int q = 0; q < PER; ++q) {
-    if (cum < target && target <= cum + h[q]) {
-      sh.bin = (uint32_t)(threadIdx.x * PER + q);
-      sh.target = target - cum;
-    }
-    cum += h[q];
-  }
-  __syncthreads();
-}
-
-template <int DT, int VEC>
-__global__ void __launch_bounds__(kThreads) sample_topp_collect_kernel(SampleArgs a) {
-  __shared__ ToppShared sh;
-  const int b = blockIdx.y, c = blockIdx.x;
-  const RowParams rp = row_params(a, b);
-  if (rp.mode != ROW_FILTER || a.row_state[b] != STATE_TOPP) return;
-  const float m = a.row_m[b];
-  topp_crossing(a.topp_hist + (size_t)b * kToppBins, rp.p, sh);
-  const int bin = (int)sh.bin;
-  float x[kEPT];
-  uint32_t valid;
-  const int base = c * kChunk;
-  load_chunk_elems<DT, VEC, kEPT>(row_ptr(a, b), base, a.V, false, rp.tp, x, valid);
-#pragma unroll
-  for (int j = 0; j < kEPT; ++j) {
-    if (!((valid >> j) & 1u)) continue;
-    if (topp_bin(x[j], m) != bin) continue;
-    const uint32_t slot = atomicAdd(&a.topp_n[b], 1u);
-    if (slot < (uint32_t)kToppCap)
-      a.topp_cand[(size_t)b * kToppCap + slot] =
-          ((unsigned long long)radix_key(x[j]) << 32) | (uint32_t)elem_index<VEC>(base, j);
-  }
-}
-
-struct ToppFinalShared {
-  ToppShared t;
-  DescShared d;
-  unsigned long long v[kToppCap];
-};
-
-__global__ void __launch_bounds__(kThreads) sample_topp_final_kernel(SampleArgs a) {
-  __shared__ ToppFinalShared sh;
-  const int b = blockIdx.x;
-  const RowParams rp = row_params(a, b);
-  if (rp.mode != ROW_FILTER || a.row_state[b] != STATE_TOPP) return;
-  const float m = a.row_m[b];
-  topp_crossing(a.topp_hist + (size_t)b * kToppBins, rp.p, sh.t);
-  const unsigned long long target = sh.t.target;
-  const uint32_t n = a.topp_n[b];
-  if (n > (uint32_t)kToppCap) {  // crossing bin too crowded: exact radix path
-    if (threadIdx.x == 0) a.row_state[b] = STATE_HEAVY;
-    return;
-  }
-  for (int e = threadIdx.x; e < (int)n; e += kThreads) sh.v[e] = a.topp_cand[(size_t)b * kToppCap + e];
-  __syncthreads();
-  const uint32_t tau = lds_desc<true>(sh.d, sh.v, (int)n, target, m);
-  // seed the row's best with the exact scores of the kept chunk maxima
-  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
-  unsigned long long best = 0;
-  for (int c = threadIdx.x; c < a.nchunks; c += kThreads) {
-    const unsigned long long ck = a.chunk_max[(size_t)b * a.nchunks + c];
-    const float xv = unord_f32((uint32_t)(ck >> 32));
-    if (radix_key(xv) < tau) continue;
-    const uint32_t i = ~(uint32_t)ck;
-    best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
-  }
-  best = block_max_u64(best, sh.t.wsum);
-  if (threadIdx.x == 0) {
-    a.row_key[b] = best;
-    a.row_tau[b] = tau;
-    a.row_state[b] = STATE_NEEDS_GUMBEL;
-  }
-}
-
-// ------------------------------------------------------------------ 3. heavy threshold
+// ------------------------------------------------------------------ 3. exact radix fallback
+// Rows the candidate and histogram paths cannot settle (k > 256, crowded ties):
+// radix descent (11/11/10-bit digits) over the whole row, counts for the k-th
+// largest, then masses for the top-p crossing.
 struct HeavyShared {
   unsigned long long hist[2048];
-  unsigned long long wave_tot[kHeavyThreads / 64];
-  unsigned long long res_above;
-  unsigned long long total;
+  unsigned long long wsum[kThreads / 64];
+  unsigned long long res_above, total;
   uint32_t res_digit;
 };
 
-__device__ __forceinline__ unsigned long long heavy_inclusive_scan(unsigned long long v, HeavyShared& s) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    uint32_t lo = __shfl_up((uint32_t)v, d, 64), hi = __shfl_up((uint32_t)(v >> 32), d, 64);
-    unsigned long long o = ((unsigned long long)hi << 32) | lo;
-    if (lane >= d) v += o;
-  }
-  if (lane == 63) s.wave_tot[wave] = v;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned long long run = 0;
-    for (int w = 0; w < kHeavyThreads / 64; ++w) {
-      unsigned long long t = s.wave_tot[w];
-      s.wave_tot[w] = run;
-      run += t;
-    }
-    s.total = run;
-  }
-  __syncthreads();
-  return v + s.wave_tot[wave];
-}
-
 // First digit d from the top whose cumulative weight (bins >= d) reaches target.
 __device__ __forceinline__ void heavy_find_desc(HeavyShared& s, int nbins, unsigned long long target) {
-  const int per = nbins / kHeavyThreads;
+  const int per = nbins / (int)blockDim.x;
   const int j0 = threadIdx.x * per;
   unsigned long long local = 0;
   for (int q = 0; q < per; ++q) local += s.hist[nbins - 1 - (j0 + q)];
-  const unsigned long long incl = heavy_inclusive_scan(local, s);
-  const unsigned long long excl = incl - local;
-  if (excl < target && target <= incl) {
+  unsigned long long tot;
+  const unsigned long long excl = block_exclusive_scan<unsigned long long>(local, s.wsum, tot);
+  if (excl < target && target <= excl + local) {
     unsigned long long cum = excl;
     for (int q = 0; q < per; ++q) {
       const int d = nbins - 1 - (j0 + q);
@@ -773,9 +694,10 @@ __device__ uint32_t radix_descend(const SampleArgs& a, const char* row, float tp
   for (int pass = 0; pass < 3; ++pass) {
     const int sh = shifts[pass], nb = 1 << widths[pass];
     const int top = sh + widths[pass];
-    for (int d = threadIdx.x; d < nb; d += kHeavyThreads) s.hist[d] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < a.V; i += kHeavyThreads) {
+    for (int d = threadIdx.x; d < nb; d += blockDim.x) s.hist[d] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < a.V; i += blockDim.x) {
       const float x = load_logit(a, row, i) / tp;
       const uint32_t key = radix_key(x);
       if (key < low) continue;
@@ -786,62 +708,182 @@ __device__ uint32_t radix_descend(const SampleArgs& a, const char* row, float tp
     __syncthreads();
     if (MASS && pass == 0) {
       unsigned long long local = 0;
-      for (int d = threadIdx.x; d < nb; d += kHeavyThreads) local += s.hist[d];
-      heavy_inclusive_scan(local, s);
-      const unsigned long long Z = s.total;
-      double pz = floor((double)p * (double)Z);
-      if (!(pz >= 0.0)) pz = 0.0;
-      unsigned long long P = (unsigned long long)pz;
-      if (P > Z - 1) P = Z - 1;
-      target = P + 1;
-      __syncthreads();
+      for (int d = threadIdx.x; d < nb; d += blockDim.x) local += s.hist[d];
+      unsigned long long Z;
+      block_exclusive_scan<unsigned long long>(local, s.wsum, Z);
+      target = topp_target(p, Z);
     }
     heavy_find_desc(s, nb, target);
     target -= s.res_above;
     prefix |= s.res_digit << sh;
-    __syncthreads();
   }
   return prefix;
 }
 
-__global__ void __launch_bounds__(kHeavyThreads) sample_threshold_kernel(SampleArgs a) {
-  __shared__ HeavyShared s;
+// ------------------------------------------------------------------ 2b. top-p rows (no top-k)
+// mass(x >= v) is found in two steps: a histogram of masses over 1/32-nat
+// bins below the row max (bins are monotone in x, equal values share a bin),
+// then an exact scan of the one bin where the cumulative mass crosses
+// floor(p * Z) + 1.
+
+__device__ __forceinline__ int topp_bin(float x, float m) {
+  const float d = (m - x) * kToppBinScale;
+  return d < (float)(kToppBins - 1) ? (int)d : kToppBins - 1;
+}
+
+struct ToppShared {
+  unsigned long long hist[kToppBins];
+  unsigned long long wsum[kThreads / 64];
+  uint32_t bin, n, base;
+  unsigned long long target;
+};
+
+template <int DT, int VEC>
+__global__ void __launch_bounds__(kThreads) sample_topp_hist_kernel(SampleArgs a) {
+  __shared__ ToppShared sh;
+  const long long items = (long long)a.list_n[1] * a.nchunks;
+  for (long long it = blockIdx.x; it < items; it += gridDim.x) {
+    const int b = (int)a.list_topp[it / a.nchunks], c = (int)(it % a.nchunks);
+    const RowParams rp = row_params(a, b);
+    const float m = a.row_m[b];
+    __syncthreads();
+    for (int d = threadIdx.x; d < kToppBins; d += kThreads) sh.hist[d] = 0;
+    __syncthreads();
+    float x[kEPT];
+    uint32_t valid;
+    load_chunk_elems<DT, VEC, kEPT>(row_ptr(a, b), c * kChunk, a.V, false, rp.tp, x, valid);
+#pragma unroll
+    for (int j = 0; j < kEPT; ++j) {
+      if (!((valid >> j) & 1u)) continue;
+      const uint64_t w = fixed_mass(x[j], m);
+      if (w) atomicAdd(&sh.hist[topp_bin(x[j], m)], (unsigned long long)w);
+    }
+    __syncthreads();
+    unsigned long long* gh = a.topp_hist + (size_t)b * kToppBins;
+    for (int d = threadIdx.x; d < kToppBins; d += kThreads)
+      if (sh.hist[d]) atomicAdd(&gh[d], sh.hist[d]);
+  }
+}
+
+// Crossing bin of the row's histogram and the mass still needed inside it.
+__device__ __forceinline__ void topp_crossing(const unsigned long long* gh, float p, ToppShared& sh) {
+  constexpr int PER = kToppBins / kThreads;
+  unsigned long long h[PER], local = 0;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) { h[q] = gh[threadIdx.x * PER + q]; local += h[q]; }
+  unsigned long long Z;
+  unsigned long long cum = block_exclusive_scan<unsigned long long>(local, sh.wsum, Z);
+  const unsigned long long target = topp_target(p, Z);
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    if (cum < target && target <= cum + h[q]) {
+      sh.bin = (uint32_t)(threadIdx.x * PER + q);
+      sh.target = target - cum;
+    }
+    cum += h[q];
+  }
+  __syncthreads();
+}
+
+template <int DT, int VEC>
+__global__ void __launch_bounds__(kThreads) sample_topp_collect_kernel(SampleArgs a) {
+  __shared__ ToppShared sh;
+  const long long items = (long long)a.list_n[1] * a.nchunks;
+  for (long long it = blockIdx.x; it < items; it += gridDim.x) {
+    const int b = (int)a.list_topp[it / a.nchunks], c = (int)(it % a.nchunks);
+    const RowParams rp = row_params(a, b);
+    const float m = a.row_m[b];
+    __syncthreads();
+    topp_crossing(a.topp_hist + (size_t)b * kToppBins, rp.p, sh);
+    const int bin = (int)sh.bin;
+    float x[kEPT];
+    uint32_t valid;
+    const int base = c * kChunk;
+    load_chunk_elems<DT, VEC, kEPT>(row_ptr(a, b), base, a.V, false, rp.tp, x, valid);
+    uint32_t in_bin = 0;
+#pragma unroll
+    for (int j = 0; j < kEPT; ++j)
+      in_bin |= (((valid >> j) & 1u) && topp_bin(x[j], m) == bin ? 1u : 0u) << j;
+    // one global reservation per block: the row's counter is shared by all chunks
+    if (threadIdx.x == 0) sh.n = 0;
+    __syncthreads();
+    const uint32_t mine = __popc(in_bin);
+    const uint32_t off = mine ? atomicAdd(&sh.n, mine) : 0u;
+    __syncthreads();
+    if (threadIdx.x == 0) sh.base = sh.n ? atomicAdd(&a.topp_n[b], sh.n) : 0u;
+    __syncthreads();
+    uint32_t slot = sh.base + off;
+#pragma unroll
+    for (int j = 0; j < kEPT; ++j) {
+      if (!((in_bin >> j) & 1u)) continue;
+      if (slot < (uint32_t)kToppCap)
+        a.topp_cand[(size_t)b * kToppCap + slot] =
+            ((unsigned long long)radix_key(x[j]) << 32) | (uint32_t)elem_index<VEC>(base, j);
+      ++slot;
+    }
+  }
+}
+
+struct ToppFinalShared {
+  ToppShared t;
+  DescShared d;
+  unsigned long long v[kToppCap];
+};
+
+union FinalizeShared {
+  ToppFinalShared tf;
+  HeavyShared hv;
+};
+
+// Rows left by select: top-p-only rows (crossing bin of the histogram ->
+// exact threshold) and rows for the exact radix fallback.  Each ends with its
+// threshold, its best score seeded from the kept chunk maxima, and a place in
+// the gumbel queue.
+__global__ void __launch_bounds__(kThreads) sample_finalize_kernel(SampleArgs a) {
+  __shared__ FinalizeShared sh;
   const int b = blockIdx.x;
   const RowParams rp = row_params(a, b);
   if (rp.mode != ROW_FILTER) return;
-  if (a.row_state[b] != STATE_HEAVY) return;
-  unsigned long long mk = 0;
-  for (int c = threadIdx.x; c < a.nchunks; c += blockDim.x) mk = max_u64(mk, a.chunk_max[(size_t)b * a.nchunks + c]);
-  mk = wave_max_u64(mk);
-  if ((threadIdx.x & 63) == 0) s.wave_tot[threadIdx.x >> 6] = mk;
-  __syncthreads();
-  mk = 0;
-  for (int w = 0; w < kHeavyThreads / 64; ++w) mk = max_u64(mk, s.wave_tot[w]);
-  __syncthreads();
-  const float m = unord_f32((uint32_t)(mk >> 32));
-  const char* row = row_ptr(a, b);
-  uint32_t thr = 0;
-  if (rp.k > 0) thr = radix_descend<false>(a, row, rp.tp, m, 0u, (unsigned long long)rp.k, 1.0f, s);
-  if (rp.p < 1.0f) thr = radix_descend<true>(a, row, rp.tp, m, thr, 1ull, rp.p, s);
+  int state = a.row_state[b];
+  if (state != STATE_TOPP && state != STATE_HEAVY) return;
+  const float m = a.row_m[b];
+  uint32_t tau = 0;
+  if (state == STATE_TOPP) {
+    topp_crossing(a.topp_hist + (size_t)b * kToppBins, rp.p, sh.tf.t);
+    const unsigned long long target = sh.tf.t.target;
+    const uint32_t n = a.topp_n[b];
+    if (n > (uint32_t)kToppCap) {
+      state = STATE_HEAVY;  // crossing bin too crowded: exact radix path
+    } else {
+      for (int e = threadIdx.x; e < (int)n; e += kThreads) sh.tf.v[e] = a.topp_cand[(size_t)b * kToppCap + e];
+      __syncthreads();
+      tau = lds_desc<true>(sh.tf.d, sh.tf.v, (int)n, target, m);
+    }
+  }
+  if (state == STATE_HEAVY) {
+    __syncthreads();
+    const char* row = row_ptr(a, b);
+    tau = 0;
+    if (rp.k > 0) tau = radix_descend<false>(a, row, rp.tp, m, 0u, (unsigned long long)rp.k, 1.0f, sh.hv);
+    if (rp.p < 1.0f) tau = radix_descend<true>(a, row, rp.tp, m, tau, 1ull, rp.p, sh.hv);
+  }
   // seed the row's best with the exact scores of the kept chunk maxima
   const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
   unsigned long long best = 0;
-  for (int c = threadIdx.x; c < a.nchunks; c += blockDim.x) {
+  for (int c = threadIdx.x; c < a.nchunks; c += kThreads) {
     const unsigned long long ck = a.chunk_max[(size_t)b * a.nchunks + c];
-    const float xv = unord_f32((uint32_t)(ck >> 32));
-    if (radix_key(xv) < thr) continue;
+    const float xv = chunk_max_x(rp, ck);
+    if (radix_key(xv) < tau) continue;
     const uint32_t i = ~(uint32_t)ck;
     best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
   }
-  best = wave_max_u64(best);
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) s.wave_tot[threadIdx.x >> 6] = best;
-  __syncthreads();
+  best = block_max_u64(best, sh.tf.t.wsum);
   if (threadIdx.x == 0) {
-    for (int w = 0; w < kHeavyThreads / 64; ++w) best = max_u64(best, s.wave_tot[w]);
     a.row_key[b] = best;
-    a.row_tau[b] = thr;
+    a.row_tau[b] = tau;
     a.row_state[b] = STATE_NEEDS_GUMBEL;
+    queue_row(&a.list_n[0], a.list_gumbel, b);
   }
 }
 
@@ -852,39 +894,51 @@ static constexpr int kGumbelEPT = 8;
 static constexpr int kGumbelSplit = kEPT / kGumbelEPT;
 
 template <int DT, int VEC>
+__device__ __forceinline__ void gumbel_item(const SampleArgs& a, int b, int sub, GumbelShared& sh) {
+  const int c = sub / kGumbelSplit;
+  const RowParams rp = row_params(a, b);
+  const float s_cur = block_prune_level(&a.row_key[b], &sh.s_cur);
+  const float cmax = chunk_max_x(rp, a.chunk_max[(size_t)b * a.nchunks + c]);
+  unsigned long long best = 0;
+  if (!(cmax + NVJSEL_GUMBEL_MAX < s_cur)) {  // else the whole chunk is out of reach
+    const uint32_t tau = rp.mode == ROW_FILTER ? a.row_tau[b] : 0u;
+    const char* row = row_ptr(a, b);
+    const int base = sub * (kThreads * kGumbelEPT);
+    float x[kGumbelEPT];
+    uint32_t valid;
+    load_chunk_elems<DT, VEC, kGumbelEPT>(row, base, a.V, false, rp.tp, x, valid);
+    uint32_t act = 0;
+#pragma unroll
+    for (int j = 0; j < kGumbelEPT; ++j) act |= (((valid >> j) & 1u) && radix_key(x[j]) >= tau ? 1u : 0u) << j;
+    const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+    best = block_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, act, s_cur, sh);
+  }
+  // the row's last item writes its id; counters are per row, so rows do not
+  // contend on one address
+  if (threadIdx.x == 0) {
+    const unsigned long long prev = best ? atomicMax(&a.row_key[b], best) : 0ull;
+    const uint32_t nsub = (uint32_t)(a.nchunks * kGumbelSplit);
+    if (atomicAdd(&a.row_done[b] + after(prev), 1u) == nsub - 1)
+      a.out_ids[b] = (int32_t)(~(uint32_t)load_row_best(&a.row_key[b]));
+  }
+}
+
+// Grid over (queued row, quarter chunk) items: rows that need no noise cost
+// nothing here.
+template <int DT, int VEC>
 __global__ void __launch_bounds__(kThreads) sample_gumbel_kernel(SampleArgs a) {
   __shared__ GumbelShared sh;
-  const int b = blockIdx.y, sub = blockIdx.x, c = sub / kGumbelSplit;
-  const RowParams rp = row_params(a, b);
-  if (rp.mode == ROW_GREEDY) return;
-  if (rp.mode == ROW_FILTER && a.row_state[b] != STATE_NEEDS_GUMBEL) return;
-  const float s_cur = block_prune_level(&a.row_key[b], &sh.s_cur);
-  const float cmax = unord_f32((uint32_t)(a.chunk_max[(size_t)b * a.nchunks + c] >> 32));
-  if (cmax + NVJSEL_GUMBEL_MAX < s_cur) return;  // the whole chunk is out of reach
-  const uint32_t tau = rp.mode == ROW_FILTER ? a.row_tau[b] : 0u;
-  const char* row = row_ptr(a, b);
-  const int base = sub * (kThreads * kGumbelEPT);
-  float x[kGumbelEPT];
-  uint32_t valid;
-  load_chunk_elems<DT, VEC, kGumbelEPT>(row, base, a.V, false, rp.tp, x, valid);
-  uint32_t act = 0;
-#pragma unroll
-  for (int j = 0; j < kGumbelEPT; ++j) act |= (((valid >> j) & 1u) && radix_key(x[j]) >= tau ? 1u : 0u) << j;
-  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
-  const unsigned long long best = block_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, act, s_cur, sh);
-  if (threadIdx.x == 0 && best) atomicMax(&a.row_key[b], best);
+  const long long nsub = (long long)a.nchunks * kGumbelSplit;
+  const long long items = (long long)a.list_n[0] * nsub;
+  for (long long it = blockIdx.x; it < items; it += gridDim.x)
+    gumbel_item<DT, VEC>(a, (int)a.list_gumbel[it / nsub], (int)(it % nsub), sh);
 }
-
-// ------------------------------------------------------------------ 5. finish
-__global__ void sample_finish_kernel(SampleArgs a) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= a.B) return;
-  const unsigned long long k = a.row_key[b];
-  a.out_ids[b] = (int32_t)(~(uint32_t)k);
-}
+// (launched with one block per possible item: queued items take the lowest
+// block indices, the rest exit at once, and the hardware balances the load)
 
 struct WsLayout {
-  size_t row_key, row_tau, row_state, chunk_max, cand_count, cand, row_m, topp_hist, topp_cand, topp_n, total;
+  size_t row_key, row_tau, row_state, chunk_max, cand_count, cand, row_m, topp_hist, topp_cand, topp_n;
+  size_t list_n, list_gumbel, list_topp, row_done, total;
 };
 
 static WsLayout ws_layout(int B, int V) {
@@ -901,6 +955,10 @@ static WsLayout ws_layout(int B, int V) {
   w.topp_hist = o;  o += align_up((size_t)B * kToppBins * 8, 256);
   w.topp_cand = o;  o += align_up((size_t)B * kToppCap * 8, 256);
   w.topp_n = o;     o += align_up((size_t)B * 4, 256);
+  w.list_n = o;     o += 256;
+  w.list_gumbel = o; o += align_up((size_t)B * 4, 256);
+  w.list_topp = o;  o += align_up((size_t)B * 4, 256);
+  w.row_done = o;   o += align_up((size_t)B * 4, 256);
   w.total = o;
   return w;
 }
@@ -958,13 +1016,16 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   a.topp_hist = (unsigned long long*)(ws + w.topp_hist);
   a.topp_cand = (unsigned long long*)(ws + w.topp_cand);
   a.topp_n = (uint32_t*)(ws + w.topp_n);
+  a.list_n = (uint32_t*)(ws + w.list_n);
+  a.list_gumbel = (uint32_t*)(ws + w.list_gumbel);
+  a.list_topp = (uint32_t*)(ws + w.list_topp);
+  a.row_done = (uint32_t*)(ws + w.row_done);
   a.out_ids = out_ids;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid_chunks(a.nchunks, batch);
   const size_t esz = dtype_size(dtype);
   const int vec = (int)(16 / esz);
   const bool vec_ok = (vocab % vec) == 0 && (row_stride % vec) == 0 && (((uintptr_t)logits) & 15) == 0;
-  const dim3 grid_gumbel(a.nchunks * kGumbelSplit, batch);
 #define NVJSEL_LAUNCH_CHUNK(KERN, GRID)                                                          \
   do {                                                                                          \
     if (dtype == NVJSEL_F32) {                                                                  \
@@ -982,19 +1043,17 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   NVJSEL_LAUNCH_CHUNK(sample_scan_kernel, grid_chunks);
   hipLaunchKernelGGL(sample_select_kernel, dim3(batch), dim3(kThreads), 0, s, a);
   NVJSEL_CHECK_LAUNCH("sample_select_kernel");
+  const dim3 grid_rows_chunks((unsigned)((long long)batch * a.nchunks));
+  const dim3 grid_items((unsigned)((long long)batch * a.nchunks * kGumbelSplit));
   if (top_p) {
-    NVJSEL_LAUNCH_CHUNK(sample_topp_hist_kernel, grid_chunks);
-    NVJSEL_LAUNCH_CHUNK(sample_topp_collect_kernel, grid_chunks);
-    hipLaunchKernelGGL(sample_topp_final_kernel, dim3(batch), dim3(kThreads), 0, s, a);
-    NVJSEL_CHECK_LAUNCH("sample_topp_final_kernel");
+    NVJSEL_LAUNCH_CHUNK(sample_topp_hist_kernel, grid_rows_chunks);
+    NVJSEL_LAUNCH_CHUNK(sample_topp_collect_kernel, grid_rows_chunks);
   }
   if (top_k || top_p) {
-    hipLaunchKernelGGL(sample_threshold_kernel, dim3(batch), dim3(kHeavyThreads), 0, s, a);
-    NVJSEL_CHECK_LAUNCH("sample_threshold_kernel");
+    hipLaunchKernelGGL(sample_finalize_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+    NVJSEL_CHECK_LAUNCH("sample_finalize_kernel");
   }
-  NVJSEL_LAUNCH_CHUNK(sample_gumbel_kernel, grid_gumbel);
+  NVJSEL_LAUNCH_CHUNK(sample_gumbel_kernel, grid_items);
 #undef NVJSEL_LAUNCH_CHUNK
-  hipLaunchKernelGGL(sample_finish_kernel, dim3((batch + 255) / 256), dim3(256), 0, s, a);
-  NVJSEL_CHECK_LAUNCH("sample_finish_kernel");
   return NVJSEL_OK;
 }
