@@ -37,7 +37,35 @@ def _parse():
     ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 512 MiB device copy (rocprofv3 counter calibration)")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "lm_head_gemv_c1_traffic.txt")
+
+
+def committed_traffic():
+    """HBM bytes per launch of the C1 kernel from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def calibrate_copy(torch):
+    n = 512 * 1024 * 1024
+    src = torch.ones(n // 4, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_copy_bytes": n}))
 
 
 class Cfg:
@@ -80,13 +108,15 @@ def build_configs(torch, which):
         return W
 
     def keys_for(batch, row_seed=False):
-        from oracle import jax_random as jr  # key derivation only (setup, untimed)
+        if row_seed:  # PRNGKey(seed) = (0, seed) for 32-bit seeds
+            k = np.stack([np.zeros(batch, np.uint32), np.arange(batch, dtype=np.uint32)], axis=1)
+            return torch.from_numpy(k.view(np.int32).copy()).to(dev)
+        # the executor's keys fold_in(fold_in(PRNGKey(0), slot), counter), derived on device
+        from nvjsel import derive_rng_keys
 
-        if row_seed:
-            k = [[int(v) for v in jr.prng_key(b)] for b in range(batch)]
-        else:
-            k = [[int(v) for v in jr.engine_key(b, 0)] for b in range(batch)]
-        return torch.from_numpy(np.array(k, np.uint32).view(np.int32).copy()).to(dev)
+        keys, _ = derive_rng_keys(torch.arange(batch, dtype=torch.int32, device=dev),
+                                  torch.zeros(batch, dtype=torch.int32, device=dev))
+        return keys
 
     def ws(nbytes):
         return torch.zeros(max(int(nbytes), 4096), dtype=torch.uint8, device=dev)
@@ -106,7 +136,7 @@ def build_configs(torch, which):
             assert rc == 0, lib.nvjsel_last_error()
 
         cfgs.append(Cfg("c1_greedy_lm_head_b1", 1, V_FULL * H_FULL * 2 + H_FULL * 2, launch,
-                        "lm_head_mfma_kernel", "greedy LM-head top-1, B=1, bf16 W[248320,1024]"))
+                        "lm_head_gemv_kernel", "greedy LM-head top-1, B=1, bf16 W[248320,1024]"))
 
     if "c2" in which:
         B = 8
@@ -124,7 +154,7 @@ def build_configs(torch, which):
                                    keys.data_ptr(), None, out.data_ptr(), w.data_ptr(), w.numel(), stream())
             assert rc == 0, lib.nvjsel_last_error()
 
-        cfgs.append(Cfg("c2_temperature_b8", B, B * V_FULL * 4, launch, "sample_scan_kernel",
+        cfgs.append(Cfg("c2_temperature_b8", B, B * V_FULL * 4, launch, "sample_gumbel_kernel",
                         "temperature sampling, f32 logits [8,248320], T=0.7"))
 
     if "c3" in which:
@@ -143,7 +173,7 @@ def build_configs(torch, which):
                                    w.numel(), stream())
             assert rc == 0, lib.nvjsel_last_error()
 
-        cfgs.append(Cfg("c3_topk_topp_b64", B, B * V_FULL * 4, launch, "sample_threshold_kernel",
+        cfgs.append(Cfg("c3_topk_topp_b64", B, B * V_FULL * 4, launch, "sample_select_kernel",
                         "top-k=50 / top-p=0.9 / T=0.8, f32 logits [64,248320] Zipf(1.1)"))
 
     if "c4" in which:
@@ -185,7 +215,7 @@ def build_configs(torch, which):
                                    w.numel(), stream())
             assert rc == 0, lib.nvjsel_last_error()
 
-        cfgs.append(Cfg("c5_mixed_b256_bf16", B, B * V_FULL * 2, launch, "sample_threshold_kernel",
+        cfgs.append(Cfg("c5_mixed_b256_bf16", B, B * V_FULL * 2, launch, "sample_gumbel_kernel",
                         "mixed per-row T/top-k/top-p, bf16 logits [256,248320]"))
     torch.cuda.synchronize()
     return cfgs
@@ -243,6 +273,9 @@ def main():
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    if args.calibrate_copy:
+        calibrate_copy(torch)
+        return
     which = set(args.configs.split(","))
     which.add("c1")
     cfgs = build_configs(torch, which)
@@ -283,7 +316,7 @@ def main():
                                "W [248320,1024] bf16, fp32 accumulate, bf16-rounded logits",
                    "batch": 1, "vocab": V_FULL, "hidden": H_FULL},
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": committed_traffic()},
         "cpu_baseline": cpu,
         "per_config": per,
     }

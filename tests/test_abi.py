@@ -113,3 +113,12 @@ def test_host_api_rejects_bad_shapes_before_launch():
         nvjsel.lm_head_greedy_top1_hip(torch.zeros(3, 1, 32, dtype=torch.bfloat16), w)
     with pytest.raises(ValueError, match="non-empty"):
         nvjsel.lm_head_greedy_top1_hip(torch.zeros(0, 1, 32, dtype=torch.bfloat16), w)
+
+
+def test_product_code_never_imports_the_oracle():
+    """The oracle is the checker only: the package and bench's GPU path do not use it."""
+    root = Path(__file__).resolve().parents[1]
+    for f in list((root / "nano-vllm-jax_amd").rglob("*.py")) + list((root / "nano-vllm-jax_amd").rglob("*.hip")):
+        assert "oracle" not in f.read_text(), f
+    bench = (root / "bench.py").read_text()
+    assert "import oracle" not in bench and "from oracle" not in bench
