@@ -195,7 +195,7 @@ def build_configs(torch, which):
             assert rc == 0, lib.nvjsel_last_error()
 
         cfgs.append(Cfg("c4_fused_lm_head_gumbel_b64", B, V_FULL * H_FULL * 2 + B * H_FULL * 2, launch,
-                        "lm_head_mfma_kernel", "fused LM-head + Gumbel-max, B=64, T=1"))
+                        "lm_head_tile_kernel", "fused LM-head + Gumbel-max, B=64, T=1"))
 
     if "c5" in which:
         B = 256

@@ -23,6 +23,8 @@
 //     and re-zeroes the workspace -- a single launch per call.
 // Any other dtype/layout/shape goes through a generic VALU kernel with the same
 // reduction and epilogue.
+#include <type_traits>
+
 #include "nvjsel_device.h"
 #include "nvjsel_host.h"
 
@@ -49,6 +51,9 @@
 #define NVJSEL_LM_BPC 0  // blocks per CU (0 = as many as occupancy allows)
 #endif
 
+#ifndef NVJSEL_USE_TILE
+#define NVJSEL_USE_TILE 1  // LDS-staged MFMA kernel for bf16 x bf16, H = 1024, B >= 3
+#endif
 #ifndef NVJSEL_GEMV_WAVES
 #define NVJSEL_GEMV_WAVES 4  // waves per block of the streaming GEMV
 #endif
@@ -81,6 +86,47 @@ __device__ __forceinline__ T stream_load(const T* p) {
 #else
   return *p;
 #endif
+}
+
+// Lambdas that take a register array by reference must inline, or the array
+// is placed in scratch memory.
+#define NVJSEL_INLINE __attribute__((always_inline))
+
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
+// Software pipeline over items 0..n-1 with a DEPTH-slot register ring:
+// load(slot, j) requests item j into ring slot `slot`; body(slot, i) consumes
+// item i.  The loop is unrolled by DEPTH so every slot index is a compile-time
+// constant and no register holding an in-flight load is ever copied (a copy
+// would wait for the load, collapsing the ring to one item in flight).  The
+// main loop issues its loads unconditionally, so the compiler's wait counts
+// keep DEPTH - 1 items in flight; only the tail tests bounds.
+template <int DEPTH, typename Load, typename Body>
+__device__ __forceinline__ void ring_pipeline(int n, Load&& load, Body&& body) {
+  static_for<DEPTH - 1>([&](auto D) NVJSEL_INLINE {
+    if (decltype(D)::value < n) load(D, (int)decltype(D)::value);
+  });
+  int i = 0;
+  for (; i + 2 * DEPTH - 2 < n; i += DEPTH)
+    static_for<DEPTH>([&](auto D) NVJSEL_INLINE {
+      constexpr int d = decltype(D)::value;
+      load(std::integral_constant<int, (d + DEPTH - 1) % DEPTH>{}, i + d + DEPTH - 1);
+      body(D, i + d);
+    });
+  for (; i < n; i += DEPTH)
+    static_for<DEPTH>([&](auto D) NVJSEL_INLINE {
+      constexpr int d = decltype(D)::value;
+      if (i + d < n) {
+        if (i + d + DEPTH - 1 < n) load(std::integral_constant<int, (d + DEPTH - 1) % DEPTH>{}, i + d + DEPTH - 1);
+        body(D, i + d);
+      }
+    });
 }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -177,6 +223,51 @@ __device__ __forceinline__ void finish_rows(unsigned long long* row_keys, unsign
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Scores N consecutive vocabulary entries v0.. of one batch row (raw fp32
+// dots).  Greedy: folds argmax keys into `best`.  Sample: computes the fast
+// approximate scores for all N in one straight-line block (N independent
+// Threefry chains the scheduler interleaves), then queues with push(x, v) every
+// entry that can still be the row's exact maximum:
+// |approx - exact| <= d(s) = 1e-4 + 4.8e-7 |s| (hardware log error ~1e-6 on the
+// draw, plus one ulp of the sum), so the exact maximum j has
+// approx_j >= approx_k - d(s_j) - d(s_k) for every k and is queued when it
+// arrives, whatever set of approximate scores `amax` is the maximum of.
+// Magnitudes are clamped so -inf stays -inf; a NaN scaled logit scores +inf.
+template <int MODE, int N, typename Push>
+__device__ __forceinline__ void score_run(const float (&raw)[N], int v0, int V, int reduce_cast, bool greedy_row,
+                                          bool unit_tp, float tp, const TfKey& key, float& amax,
+                                          unsigned long long& best, Push&& push) {
+  float val[N];
+#pragma unroll
+  for (int e = 0; e < N; ++e) val[e] = apply_cast(raw[e], reduce_cast);
+  if (MODE == MODE_SAMPLE && !greedy_row) {
+    float xv[N], ap[N];
+    uint32_t bits[N];
+#pragma unroll
+    for (int e = 0; e < N; ++e) xv[e] = val[e];
+    if (!unit_tp) {
+#pragma unroll
+      for (int e = 0; e < N; ++e) xv[e] = val[e] / tp;
+    }
+    random_bits32_n<N>(key, (uint32_t)v0, bits);
+#pragma unroll
+    for (int e = 0; e < N; ++e) ap[e] = (xv[e] != xv[e]) ? INFINITY : xv[e] + gumbel_fast_from_bits(bits[e]);
+    const float am = amax;
+    const float sam = fminf(fabsf(am), 1e30f);
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      if (v0 + e >= V) continue;
+      const float slack = 2e-4f + 4.8e-7f * (fminf(fabsf(ap[e]), 1e30f) + sam);
+      if (!(ap[e] + slack < am)) push(xv[e], v0 + e);
+      amax = fmaxf(amax, ap[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; ++e)
+      if (v0 + e < V) best = max_u64(best, argmax_key(val[e], (uint32_t)(v0 + e)));
+  }
+}
+
 // ------------------------------------------------------------------ MFMA kernel
 // WT: weight element type (DT_BF16 / DT_F16).  NSPLIT: hidden terms (1, or 3
 // for an exact f32 hidden on bf16 weights).  NB: 16-row batch tiles.  MT:
@@ -255,7 +346,7 @@ lm_head_mfma_kernel(LmArgs a) {
   const int gw = blockIdx.x * WAVES + wave;
   const int n_my_tiles = gw < ntiles ? (ntiles - gw + nwaves - 1) / nwaves : 0;
   const int nq = n_my_tiles * nch;
-  auto load_q = [&](u32x4_t(&A)[KU][MT], int q) {
+  auto load_q = [&](u32x4_t(&A)[KU][MT], int q) NVJSEL_INLINE {
     const int tile = gw + (q / nch) * nwaves;
     const int c = q % nch;
 #pragma unroll
@@ -399,7 +490,7 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
   const int g_begin = gw, g_end = ngroups, g_step = nwaves;
 #endif
 
-  auto load_grp = [&](u32x4_t(&w)[R][KJ], int grp) {
+  auto load_grp = [&](u32x4_t(&w)[R][KJ], int grp) NVJSEL_INLINE {
     const int v0 = grp * R;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -412,7 +503,7 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  auto proc_grp = [&](const u32x4_t(&w)[R][KJ], int grp) {
+  auto proc_grp = [&](const u32x4_t(&w)[R][KJ], int grp) NVJSEL_INLINE {
     const int v0 = grp * R;
 #if NVJSEL_GEMV_NOCOMPUTE
     // timing probe only: consume the loads without the dot products
@@ -479,7 +570,8 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
   };
 
   // ring of DEPTH row groups in flight: group i+DEPTH-1 is requested before i is reduced
-  constexpr int DEPTH = NVJSEL_GEMV_DEPTH;
+  // ring of DEPTH * R * KJ 16-byte loads per lane
+  constexpr int DEPTH = MODE == MODE_SAMPLE ? (KJ >= 4 ? 2 : 3) : NVJSEL_GEMV_DEPTH;
   const int n_mine = g_end > g_begin ? (g_end - g_begin + g_step - 1) / g_step : 0;
 #if NVJSEL_GEMV_CONTIG == 3
   // waves advance in lockstep; starting each slice at a different point keeps
@@ -490,18 +582,27 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
 #endif
   auto gid = [&](int i) { int k = i + rot; k = k >= n_mine ? k - n_mine : k; return g_begin + k * g_step; };
   u32x4_t ring[DEPTH][R][KJ];
-#pragma unroll
-  for (int d = 0; d < DEPTH - 1; ++d)
-    if (d < n_mine) load_grp(ring[d], gid(d));
-  for (int i = 0; i < n_mine; ++i) {
-    if (i + DEPTH - 1 < n_mine) load_grp(ring[DEPTH - 1], gid(i + DEPTH - 1));
-    proc_grp(ring[0], gid(i));
+  if constexpr (MODE == MODE_SAMPLE) {
+    ring_pipeline<DEPTH>(
+        n_mine, [&](auto S, int j) NVJSEL_INLINE { load_grp(ring[decltype(S)::value], gid(j)); },
+        [&](auto S, int i) NVJSEL_INLINE { proc_grp(ring[decltype(S)::value], gid(i)); });
+  } else {
+    // Greedy streams fastest (measured) with the shifting ring: the register
+    // copies wait for every outstanding load at the top of each step, so one
+    // group is in flight while the previous one is reduced.
 #pragma unroll
     for (int d = 0; d < DEPTH - 1; ++d)
+      if (d < n_mine) load_grp(ring[d], gid(d));
+    for (int i = 0; i < n_mine; ++i) {
+      if (i + DEPTH - 1 < n_mine) load_grp(ring[DEPTH - 1], gid(i + DEPTH - 1));
+      proc_grp(ring[0], gid(i));
 #pragma unroll
-      for (int r = 0; r < R; ++r)
+      for (int d = 0; d < DEPTH - 1; ++d)
 #pragma unroll
-        for (int j = 0; j < KJ; ++j) ring[d][r][j] = ring[d + 1][r][j];
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int j = 0; j < KJ; ++j) ring[d][r][j] = ring[d + 1][r][j];
+    }
   }
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
@@ -510,6 +611,225 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
   }
   block_commit<WAVES, NB>(red, B, a.row_keys);
   finish_rows(a.row_keys, a.counter, B, a.out_ids, a.out_best);
+}
+
+// ------------------------------------------------------------------ LDS-staged MFMA tile kernel
+// bf16 hidden x bf16 W [V, 1024], 3 <= B <= 64.  A block holds GW "GEMM" waves
+// and NB "epilogue" waves.
+//  * GEMM waves load each 16-row W tile (32 KB, contiguous) with 16-byte loads
+//    covering 4 KB per block instruction -- the streaming pattern -- keeping
+//    DEPTH-1 tiles in flight in a register ring, and store it to LDS in
+//    A-fragment order (row XOR-swizzled so both the stores and the 16-lane
+//    fragment reads are conflict-free).  Hidden fragments stay in registers:
+//    GEMM wave w owns batch tile w % NB and k-steps [(w / NB) * KPW, +KPW), and
+//    leaves its k-split partial sums of tile i in an LDS ring.
+//  * Epilogue waves meanwhile sum, cast and score tile i-1.  Epilogue lane L
+//    (of NB * 64) owns batch row L % (NB * 16) and vocabulary rows
+//    4 * (L / (NB * 16)) .. +3 of every tile.  Sample mode scores with the
+//    hardware log and rescores exactly (fp64 logs), a wave at a time, only the
+//    entries that can still be a row's maximum.
+// One barrier per tile orders both rings, so a tile costs max(GEMM, epilogue)
+// rather than their sum, and the epilogue's VALU work (Threefry + logs) runs
+// beside the GEMM waves' LDS, MFMA and memory waits on the same SIMDs.
+template <int NB, int GW, int MODE, int DEPTH>
+__global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) {
+  constexpr int NT = (GW + NB) * 64;
+  constexpr int NTG = GW * 64;
+  constexpr int KSPLIT = GW / NB;
+  static_assert(KSPLIT >= 1 && GW % NB == 0, "GEMM waves split k evenly");
+  constexpr int KS = 32;  // 32-wide k-steps of H = 1024
+  constexpr int KPW = KS / KSPLIT;
+  static_assert(KS % KSPLIT == 0, "k-steps split evenly");
+  constexpr int LPT = 2048 / NTG;  // 16-byte loads per GEMM thread per 32 KB tile
+  static_assert(2048 % NTG == 0, "tile loads split evenly");
+  constexpr int ROWS = NB * 16;    // batch rows of the block
+  constexpr int QCAP = 64 * 4 + 64;
+  __shared__ u32x4_t wt[2][16 * 128];
+  __shared__ f32x4_t part[2][KSPLIT * NB * 64];
+  __shared__ float qx[MODE == MODE_SAMPLE ? NB : 1][QCAP];
+  __shared__ uint32_t qv[MODE == MODE_SAMPLE ? NB : 1][QCAP];
+  __shared__ uint32_t qn[NB];
+  __shared__ unsigned long long qbest[MODE == MODE_SAMPLE ? NB : 1][64];
+  __shared__ unsigned long long red[NB * 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool gemm = wave < GW;
+  const int B = a.B, V = a.V;
+  const uint16_t* W = (const uint16_t*)a.W;
+  const int ntiles = (V + 15) >> 4;
+  const int grid = gridDim.x;
+  const int my_tiles = blockIdx.x < ntiles ? (ntiles - blockIdx.x + grid - 1) / grid : 0;
+
+  // ---- GEMM-wave state
+  const int g = lane >> 4, r = lane & 15;
+  const int nb = wave % NB, ks = wave / NB;  // meaningful for GEMM waves
+  u32x4_t hb[KPW];
+  u32x4_t ring[DEPTH][LPT];
+  // ---- epilogue-wave state
+  const int ew = wave - GW;                      // epilogue wave index
+  const int el = (ew < 0 ? 0 : ew) * 64 + lane;  // epilogue lane id
+  const int erow = el % ROWS, evq = el / ROWS;   // batch row, vocab quad
+  float tp = 1.0f;
+  bool greedy_row = true, unit_tp = true;
+  TfKey key = tf_key(0u, 0u);
+  unsigned long long best = 0;
+  float amax = -INFINITY;
+
+  auto load_tile = [&](u32x4_t(&dst)[LPT], int i) NVJSEL_INLINE {
+    const int tile = blockIdx.x + i * grid;
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int c = tid + NTG * u;
+      int row = tile * 16 + (c >> 7);
+      row = row < V ? row : V - 1;
+      dst[u] = stream_load((const u32x4_t*)(W + (size_t)row * 1024) + (c & 127));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // exact scores of the queued elements, a full wave at a time; an entry holds
+  // x and (vocab << 6 | lane that found it); results fold into qbest[lane]
+  auto flush = [&]() {
+    if constexpr (MODE == MODE_SAMPLE) {
+      const uint32_t n = qn[ew];
+      for (uint32_t e0 = 0; e0 < n; e0 += 64) {  // wave-uniform trip count
+        const uint32_t e = e0 + lane;
+        const bool live = e < n;
+        const uint32_t pv = live ? qv[ew][e] : 0u;
+        const uint32_t v = pv >> 6, src = pv & 63u;
+        // the shuffles run with the whole wave active
+        const TfKey k2{(uint32_t)__shfl((int)key.k0, (int)src, 64), (uint32_t)__shfl((int)key.k1, (int)src, 64),
+                       (uint32_t)__shfl((int)key.k2, (int)src, 64)};
+        if (live) atomicMax(&qbest[ew][src], argmax_key(qx[ew][e] + gumbel_at(k2, v), v));
+      }
+      if (lane == 0) qn[ew] = 0;
+    }
+  };
+
+  if (gemm) {
+    const int brow = nb * 16 + r;
+    const uint16_t* hp = (const uint16_t*)a.hidden + (size_t)(brow < B ? brow : 0) * 1024;
+#pragma unroll
+    for (int kk = 0; kk < KPW; ++kk) {
+      const int kb = ks * KPW + kk;
+      hb[kk] = brow < B ? *(const u32x4_t*)(hp + kb * 32 + g * 8) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  } else {
+    if constexpr (MODE == MODE_SAMPLE) {
+      const float t = erow < B ? a.temperature[erow] : 0.0f;
+      greedy_row = (t <= 0.0f);
+      tp = temp_floor(t);
+      unit_tp = (tp == 1.0f);  // x / 1 == x exactly
+      if (erow < B) key = tf_key(a.keys[2 * erow], a.keys[2 * erow + 1]);
+      if (lane == 0) qn[ew] = 0;
+      qbest[ew][lane] = 0;
+    }
+  }
+
+  // The two roles run separate loops with one barrier per iteration each
+  // (my_tiles + 1 of them), so neither keeps the other's registers live.  The
+  // barrier orders: W(i) stores before its fragment reads; partials of tile i-1
+  // before the epilogue reads them; every read of a slot before it is rewritten.
+  if (gemm) {
+    ring_pipeline<DEPTH>(my_tiles, [&](auto S, int j) NVJSEL_INLINE { load_tile(ring[decltype(S)::value], j); },
+                         [&](auto S, int i) NVJSEL_INLINE {
+      u32x4_t* buf = wt[i & 1];
+#pragma unroll
+      for (int u = 0; u < LPT; ++u) {
+        const int c = tid + NTG * u;
+        const int row = c >> 7, q = c & 127;
+        buf[q * 16 + (row ^ (q & 15))] = ring[decltype(S)::value][u];
+      }
+      __syncthreads();
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KPW; ++kk) {
+        const int q = (ks * KPW + kk) * 4 + g;
+        acc = mfma16x16x32<DT_BF16>(buf[q * 16 + (r ^ (q & 15))], hb[kk], acc);
+      }
+      part[i & 1][(ks * NB + nb) * 64 + lane] = acc;
+    });
+    __syncthreads();  // the epilogue waves' last iteration
+  } else {
+    for (int i = 0; i <= my_tiles; ++i) {
+      __syncthreads();
+      if (i == 0) continue;
+      // tile i-1: sum the k-split partials of (row erow, vocab rows 4 evq + e)
+      const int pnb = erow >> 4, pl = evq * 16 + (erow & 15);
+      f32x4_t s = part[(i - 1) & 1][pnb * 64 + pl];
+#pragma unroll
+      for (int s2 = 1; s2 < KSPLIT; ++s2) {
+        const f32x4_t p = part[(i - 1) & 1][(s2 * NB + pnb) * 64 + pl];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[e] += p[e];
+      }
+      const int v0 = (blockIdx.x + (i - 1) * grid) * 16 + 4 * evq;
+      if constexpr (MODE == MODE_SAMPLE) {
+        if constexpr (ROWS < 64) {
+          // lanes holding the same batch row share their approximate maximum
+#pragma unroll
+          for (int m = ROWS; m < 64; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+        }
+        if (qn[ew] >= 64u) flush();  // full waves of exact work; room for this tile
+      }
+      if (erow < B) {
+        const float raw[4] = {s[0], s[1], s[2], s[3]};
+        score_run<MODE, 4>(raw, v0, V, a.reduce_cast, greedy_row, unit_tp, tp, key, amax, best,
+                           [&](float x, int v) {
+                             const uint32_t slot = atomicAdd(&qn[ew], 1u);
+                             qx[ew][slot] = x;
+                             qv[ew][slot] = ((uint32_t)v << 6) | (uint32_t)lane;
+                           });
+      }
+    }
+  }
+  if (!gemm) {
+    if constexpr (MODE == MODE_SAMPLE) {
+      flush();
+      if (!greedy_row) best = max_u64(best, qbest[ew][lane]);
+    }
+    red[el] = best;
+  }
+  __syncthreads();
+  for (int b = tid; b < B && b < ROWS; b += NT) {
+    unsigned long long m = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) m = max_u64(m, red[q * ROWS + b]);
+    if (m) (void)after(atomicMax(&a.row_keys[b], m));
+  }
+  finish_rows(a.row_keys, a.counter, B, a.out_ids, a.out_best);
+}
+
+#ifndef NVJSEL_TILE_DEPTH
+#define NVJSEL_TILE_DEPTH 2  // W tiles in flight per block (registers)
+#endif
+#ifndef NVJSEL_TILE_W1
+#define NVJSEL_TILE_W1 4  // waves per block by batch tiles: 1, 2, 4
+#endif
+#ifndef NVJSEL_TILE_W2
+#define NVJSEL_TILE_W2 8
+#endif
+#ifndef NVJSEL_TILE_W4
+#define NVJSEL_TILE_W4 8
+#endif
+#ifndef NVJSEL_TILE_BPC
+#define NVJSEL_TILE_BPC 1  // blocks per CU of the tile kernel
+#endif
+
+template <int NB, int GW, int MODE>
+static int launch_tile(const LmArgs& a, hipStream_t stream) {
+  auto kern = lm_head_tile_kernel<NB, GW, MODE, NVJSEL_TILE_DEPTH>;
+  int grid = NVJSEL_TILE_BPC * device_cu_count();
+  const int ntiles = (a.V + 15) / 16;
+  if (grid > ntiles) grid = ntiles;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3((GW + NB) * 64), 0, stream, a);
+  NVJSEL_CHECK_LAUNCH("lm_head_tile_kernel");
+  return NVJSEL_OK;
+}
+
+template <int MODE>
+static int dispatch_tile(const LmArgs& a, hipStream_t s) {
+  if (a.B <= 16) return launch_tile<1, NVJSEL_TILE_W1, MODE>(a, s);
+  if (a.B <= 32) return launch_tile<2, NVJSEL_TILE_W2, MODE>(a, s);
+  return launch_tile<4, NVJSEL_TILE_W4, MODE>(a, s);
 }
 
 // ------------------------------------------------------------------ generic kernel
@@ -678,6 +998,9 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     if (nsplit == 3 && tiles > 1) tiles = 1;
     chunk = tiles * 16;
   }
+  const bool tile = !gemv && bf16_mfma && hidden_dtype == NVJSEL_BF16 && H == 1024 &&
+                    (((uintptr_t)hidden) & 15) == 0 && NVJSEL_USE_TILE;
+  if (tile) chunk = 64;
   if (gemv) chunk = 0;
   for (int b0 = 0; b0 < batch; b0 += (chunk > 0 ? chunk : batch)) {
     LmArgs a;
@@ -700,6 +1023,8 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     int rc;
     if (gemv) {
       rc = mode == MODE_GREEDY ? dispatch_gemv<MODE_GREEDY>(a, s) : dispatch_gemv<MODE_SAMPLE>(a, s);
+    } else if (tile) {
+      rc = mode == MODE_GREEDY ? dispatch_tile<MODE_GREEDY>(a, s) : dispatch_tile<MODE_SAMPLE>(a, s);
     } else if (chunk > 0) {
       if (f16_mfma)
         rc = mode == MODE_GREEDY ? dispatch_nb<DT_F16, 1, MODE_GREEDY>(a, s) : dispatch_nb<DT_F16, 1, MODE_SAMPLE>(a, s);

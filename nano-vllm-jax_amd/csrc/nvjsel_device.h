@@ -50,6 +50,34 @@ __device__ __forceinline__ void threefry2x32(const TfKey& k, uint32_t c0, uint32
 }
 #undef NVJSEL_TF_ROUND
 
+// random_bits32 for the N consecutive indices i0 .. i0+N-1, written round by
+// round across the N counters so the independent chains interleave (one
+// chain alone is a serial dependence of ~80 VALU operations).
+template <int N>
+__device__ __forceinline__ void random_bits32_n(const TfKey& k, uint32_t i0, uint32_t (&out)[N]) {
+  uint32_t x0[N], x1[N];
+#pragma unroll
+  for (int e = 0; e < N; ++e) { x0[e] = k.k0; x1[e] = i0 + (uint32_t)e + k.k1; }
+#define NVJSEL_TF_ROUND_N(r) \
+  _Pragma("unroll") for (int e = 0; e < N; ++e) { x0[e] += x1[e]; x1[e] = rotl32(x1[e], r); x1[e] ^= x0[e]; }
+#define NVJSEL_TF_INJECT_N(a, b, c) \
+  _Pragma("unroll") for (int e = 0; e < N; ++e) { x0[e] += (a); x1[e] += (b) + (uint32_t)(c); }
+  NVJSEL_TF_ROUND_N(13) NVJSEL_TF_ROUND_N(15) NVJSEL_TF_ROUND_N(26) NVJSEL_TF_ROUND_N(6)
+  NVJSEL_TF_INJECT_N(k.k1, k.k2, 1)
+  NVJSEL_TF_ROUND_N(17) NVJSEL_TF_ROUND_N(29) NVJSEL_TF_ROUND_N(16) NVJSEL_TF_ROUND_N(24)
+  NVJSEL_TF_INJECT_N(k.k2, k.k0, 2)
+  NVJSEL_TF_ROUND_N(13) NVJSEL_TF_ROUND_N(15) NVJSEL_TF_ROUND_N(26) NVJSEL_TF_ROUND_N(6)
+  NVJSEL_TF_INJECT_N(k.k0, k.k1, 3)
+  NVJSEL_TF_ROUND_N(17) NVJSEL_TF_ROUND_N(29) NVJSEL_TF_ROUND_N(16) NVJSEL_TF_ROUND_N(24)
+  NVJSEL_TF_INJECT_N(k.k1, k.k2, 4)
+  NVJSEL_TF_ROUND_N(13) NVJSEL_TF_ROUND_N(15) NVJSEL_TF_ROUND_N(26) NVJSEL_TF_ROUND_N(6)
+  NVJSEL_TF_INJECT_N(k.k2, k.k0, 5)
+#undef NVJSEL_TF_ROUND_N
+#undef NVJSEL_TF_INJECT_N
+#pragma unroll
+  for (int e = 0; e < N; ++e) out[e] = x0[e] ^ x1[e];
+}
+
 // random_bits(key, 32, shape)[i] in JAX's partitionable layout: counter (hi, lo) of i.
 __device__ __forceinline__ uint32_t random_bits32(const TfKey& k, uint32_t i) {
   uint32_t o0, o1;
@@ -76,10 +104,14 @@ __device__ __forceinline__ float gumbel_at(const TfKey& k, uint32_t i) {
 // The same draw with the hardware fp32 log (v_log_f32): within ~2e-5 of
 // gumbel_from_bits over its whole range.  Used only to find the few elements
 // that can be the maximum; the winner is always decided on exact values.
+// Both logs take normal arguments (u >= FLT_MIN, and -log2(u) >= 1.7e-7), so
+// the hardware log2 (v_log_f32) is used bare:
+//   -ln(-ln u) = -ln2 * log2(-log2 u) - ln(ln2).
 __device__ __forceinline__ float gumbel_fast_from_bits(uint32_t bits) {
   float f = __uint_as_float((bits >> 9) | 0x3F800000u) - 1.0f;
-  float u = fmaxf(f + 1.17549435e-38f, 1.17549435e-38f);
-  return -__logf(-__logf(u));
+  float u = fmaxf(f, 1.17549435e-38f);
+  float l = -__builtin_amdgcn_logf(u);
+  return __builtin_fmaf(-0.693147180559945f, __builtin_amdgcn_logf(l), 0.366512920581664f);
 }
 
 // Upper bound of any Gumbel draw (u = 1 - 2^-23), rounded up.

@@ -70,3 +70,35 @@ def zipf_logits(rng, batch: int, vocab: int, s_lo: float, s_hi: float, noise_sd:
         row = lp[rng.permutation(vocab)] + rng.normal(0.0, noise_sd, vocab)
         out[b] = row.astype(np.float32)
     return out
+
+
+def check_fused_sampled(ids, z64, temps, keys, reduce_cast=1, ctx=""):
+    """Fused LM-head sampling: per row, T <= 0 -> greedy check; else the oracle
+    scores s_v = rnd(z_v)/T' + g_v.  The kernel's fp32 dot can flip a logit's
+    rounding by one bf16/f16 ulp, so rows whose best two scores are closer
+    than that flip are ambiguous: the id must then be within the flip of the
+    best score.  Returns the ambiguous-row count."""
+    ids = np.asarray(ids).reshape(-1)
+    rnd = sel.round_bf16 if reduce_cast == 1 else (sel.round_f16 if reduce_cast == 2 else None)
+    namb = 0
+    for b in range(len(ids)):
+        t = np.float32(temps[b])
+        if t <= 0:
+            namb += check_greedy(ids[b:b + 1], z64[b:b + 1], reduce_cast, ctx)
+            continue
+        l = z64[b].astype(np.float32)
+        if rnd is not None:
+            l = rnd(l)
+        x = sel.scale_logits(l, t)
+        key = (np.uint32(keys[b][0]), np.uint32(keys[b][1]))
+        s = (x + jr.gumbel(key, len(x))).astype(np.float64)
+        ulp = (2.0 ** -7 if reduce_cast == 1 else 2.0 ** -10 if reduce_cast == 2 else 2.0 ** -20)
+        tol = np.abs(l.astype(np.float64)) * ulp / float(max(t, np.float32(1e-6))) + 1e-4
+        best = int(np.argmax(s))
+        if int(ids[b]) == best:
+            continue
+        j = int(ids[b])
+        assert s[j] >= s[best] - tol[j] - tol[best], (
+            f"{ctx} row {b}: got {j} (score {s[j]:.6f}), oracle {best} (score {s[best]:.6f})")
+        namb += 1
+    return namb

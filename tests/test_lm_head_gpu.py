@@ -140,3 +140,39 @@ def test_streaming_gemv_shapes(H, batch):
     torch.cuda.synchronize()
     z = sel.lm_head_logits(as_f32(h), as_f32(W))
     check_greedy(ids.cpu().numpy(), z, 1, f"gemv H={H} B={batch}")
+
+
+@pytest.mark.parametrize("batch", [1, 2, 5, 16, 33, 64, 70])
+def test_fused_lm_head_sample(batch):
+    """nvjsel_lm_head_sample vs the oracle: greedy rows, temperature rows (JAX keys)."""
+    from tests.gpu_helpers import check_fused_sampled, engine_keys, keys_tensor
+
+    rng = np.random.default_rng(500 + batch)
+    H, V = 1024, 20011
+    h = bf16_tensor(rng.standard_normal((batch, H)))
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    T = [float(x) for x in rng.choice([0.0, 0.7, 1.0, 1.5], batch)]
+    keys = engine_keys(batch, 11)
+    ids = nvjsel.lm_head_sample_token_ids(h, W, temperatures=torch.tensor(T).cuda(),
+                                          rng_keys=keys_tensor(keys), weight_layout="vh")
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(as_f32(h), as_f32(W))
+    namb = check_fused_sampled(ids.cpu().numpy(), z, T, keys, 1, f"fused B={batch}")
+    assert namb <= max(1, batch // 8)
+
+
+def test_fused_lm_head_sample_full_vocab_c4():
+    """hidden [64,1024] bf16 ~N(0,1), W [248320,1024] ~N(0,0.02), T=1."""
+    from tests.gpu_helpers import check_fused_sampled, engine_keys, keys_tensor
+
+    g = torch.Generator().manual_seed(3)
+    B, H, V = 64, 1024, 248320
+    h = torch.randn(B, H, generator=g).to(torch.bfloat16)
+    W = (torch.randn(V, H, generator=g) * 0.02).to(torch.bfloat16)
+    keys = engine_keys(B, 5)
+    ids = nvjsel.lm_head_sample_token_ids(h.cuda(), W.cuda(), temperatures=torch.ones(B).cuda(),
+                                          rng_keys=keys_tensor(keys), weight_layout="vh")
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(h.float().numpy(), W.float().numpy())
+    namb = check_fused_sampled(ids.cpu().numpy(), z, [1.0] * B, keys, 1, "C4")
+    assert namb <= 4
