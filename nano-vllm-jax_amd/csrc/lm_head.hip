@@ -250,17 +250,27 @@ __device__ __forceinline__ void score_run(const float (&raw)[N], int v0, int V, 
       for (int e = 0; e < N; ++e) xv[e] = val[e] / tp;
     }
     random_bits32_n<N>(key, (uint32_t)v0, bits);
-#pragma unroll
-    for (int e = 0; e < N; ++e) ap[e] = (xv[e] != xv[e]) ? INFINITY : xv[e] + gumbel_fast_from_bits(bits[e]);
-    const float am = amax;
-    const float sam = fminf(fabsf(am), 1e30f);
+    // NaN only from a NaN logit (the draw is finite); selecting on the sum
+    // keeps the draws unconditional, so the N chains stay one straight block
 #pragma unroll
     for (int e = 0; e < N; ++e) {
-      if (v0 + e >= V) continue;
-      const float slack = 2e-4f + 4.8e-7f * (fminf(fabsf(ap[e]), 1e30f) + sam);
-      if (!(ap[e] + slack < am)) push(xv[e], v0 + e);
-      amax = fmaxf(amax, ap[e]);
+      const float t = xv[e] + gumbel_fast_from_bits(bits[e]);
+      ap[e] = (t != t) ? INFINITY : t;
     }
+    // every draw feeds an unconditional select, so none is sunk into a branch
+    const float am = amax;
+    const float sam = fminf(fabsf(am), 1e30f);
+    bool q[N];
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      const bool ok = v0 + e < V;
+      const float slack = 2e-4f + 4.8e-7f * (fminf(fabsf(ap[e]), 1e30f) + sam);
+      q[e] = ok && !(ap[e] + slack < am);
+      amax = fmaxf(amax, ok ? ap[e] : -INFINITY);
+    }
+#pragma unroll
+    for (int e = 0; e < N; ++e)
+      if (q[e]) push(xv[e], v0 + e);
   } else {
 #pragma unroll
     for (int e = 0; e < N; ++e)

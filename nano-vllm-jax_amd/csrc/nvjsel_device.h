@@ -53,13 +53,32 @@ __device__ __forceinline__ void threefry2x32(const TfKey& k, uint32_t c0, uint32
 // random_bits32 for the N consecutive indices i0 .. i0+N-1, written round by
 // round across the N counters so the independent chains interleave (one
 // chain alone is a serial dependence of ~80 VALU operations).
+// For N == 4 each round is one asm block that issues the four chains'
+// add / rotate / xor interleaved (the compiler's scheduler otherwise emits the
+// chains one after another to save registers, and a lone dependent chain
+// issues at a fraction of the VALU rate).  Only vector instructions.
+#define NVJSEL_TF4_ROUND(r)                                                             \
+  asm volatile(                                                                         \
+      "v_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\t"                                \
+      "v_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\t"                                \
+      "v_alignbit_b32 %4, %4, %4, %8\n\tv_alignbit_b32 %5, %5, %5, %8\n\t"              \
+      "v_alignbit_b32 %6, %6, %6, %8\n\tv_alignbit_b32 %7, %7, %7, %8\n\t"              \
+      "v_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\t"                                \
+      "v_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3"                                     \
+      : "+v"(x0[0]), "+v"(x0[1]), "+v"(x0[2]), "+v"(x0[3]), "+v"(x1[0]), "+v"(x1[1]), \
+        "+v"(x1[2]), "+v"(x1[3])                                                        \
+      : "n"(32 - (r)))
 template <int N>
 __device__ __forceinline__ void random_bits32_n(const TfKey& k, uint32_t i0, uint32_t (&out)[N]) {
   uint32_t x0[N], x1[N];
 #pragma unroll
   for (int e = 0; e < N; ++e) { x0[e] = k.k0; x1[e] = i0 + (uint32_t)e + k.k1; }
-#define NVJSEL_TF_ROUND_N(r) \
-  _Pragma("unroll") for (int e = 0; e < N; ++e) { x0[e] += x1[e]; x1[e] = rotl32(x1[e], r); x1[e] ^= x0[e]; }
+#define NVJSEL_TF_ROUND_N(r)                                                                      \
+  if constexpr (N == 4) {                                                                         \
+    NVJSEL_TF4_ROUND(r);                                                                          \
+  } else {                                                                                        \
+    _Pragma("unroll") for (int e = 0; e < N; ++e) { x0[e] += x1[e]; x1[e] = rotl32(x1[e], r); x1[e] ^= x0[e]; } \
+  }
 #define NVJSEL_TF_INJECT_N(a, b, c) \
   _Pragma("unroll") for (int e = 0; e < N; ++e) { x0[e] += (a); x1[e] += (b) + (uint32_t)(c); }
   NVJSEL_TF_ROUND_N(13) NVJSEL_TF_ROUND_N(15) NVJSEL_TF_ROUND_N(26) NVJSEL_TF_ROUND_N(6)
@@ -73,6 +92,7 @@ __device__ __forceinline__ void random_bits32_n(const TfKey& k, uint32_t i0, uin
   NVJSEL_TF_ROUND_N(13) NVJSEL_TF_ROUND_N(15) NVJSEL_TF_ROUND_N(26) NVJSEL_TF_ROUND_N(6)
   NVJSEL_TF_INJECT_N(k.k2, k.k0, 5)
 #undef NVJSEL_TF_ROUND_N
+#undef NVJSEL_TF4_ROUND
 #undef NVJSEL_TF_INJECT_N
 #pragma unroll
   for (int e = 0; e < N; ++e) out[e] = x0[e] ^ x1[e];
