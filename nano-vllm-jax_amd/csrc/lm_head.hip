@@ -225,9 +225,9 @@ __device__ __forceinline__ void finish_rows(unsigned long long* row_keys, unsign
 
 // Scores N consecutive vocabulary entries v0.. of one batch row (raw fp32
 // dots).  Greedy: folds argmax keys into `best`.  Sample: computes the fast
-// approximate scores for all N in one straight-line block (N independent
-// Threefry chains the scheduler interleaves), then queues with push(x, v) every
-// entry that can still be the row's exact maximum:
+// approximate scores for all N in one straight-line block (N interleaved
+// Threefry chains), then queues with push(x, v) every entry that can still be
+// the row's exact maximum:
 // |approx - exact| <= d(s) = 1e-4 + 4.8e-7 |s| (hardware log error ~1e-6 on the
 // draw, plus one ulp of the sum), so the exact maximum j has
 // approx_j >= approx_k - d(s_j) - d(s_k) for every k and is queued when it
@@ -249,7 +249,10 @@ __device__ __forceinline__ void score_run(const float (&raw)[N], int v0, int V, 
 #pragma unroll
       for (int e = 0; e < N; ++e) xv[e] = val[e] / tp;
     }
-    random_bits32_n<N>(key, (uint32_t)v0, bits);
+    uint32_t idx[N];
+#pragma unroll
+    for (int e = 0; e < N; ++e) idx[e] = (uint32_t)(v0 + e);
+    random_bits32_n<N>(key, idx, bits);
     // NaN only from a NaN logit (the draw is finite); selecting on the sum
     // keeps the draws unconditional, so the N chains stay one straight block
 #pragma unroll

@@ -50,8 +50,8 @@ __device__ __forceinline__ void threefry2x32(const TfKey& k, uint32_t c0, uint32
 }
 #undef NVJSEL_TF_ROUND
 
-// random_bits32 for the N consecutive indices i0 .. i0+N-1, written round by
-// round across the N counters so the independent chains interleave (one
+// random_bits32 at the N indices idx[], written round by round across the N
+// counters so the independent chains interleave (one
 // chain alone is a serial dependence of ~80 VALU operations).
 // For N == 4 each round is one asm block that issues the four chains'
 // add / rotate / xor interleaved (the compiler's scheduler otherwise emits the
@@ -69,10 +69,10 @@ __device__ __forceinline__ void threefry2x32(const TfKey& k, uint32_t c0, uint32
         "+v"(x1[2]), "+v"(x1[3])                                                        \
       : "n"(32 - (r)))
 template <int N>
-__device__ __forceinline__ void random_bits32_n(const TfKey& k, uint32_t i0, uint32_t (&out)[N]) {
+__device__ __forceinline__ void random_bits32_n(const TfKey& k, const uint32_t (&idx)[N], uint32_t (&out)[N]) {
   uint32_t x0[N], x1[N];
 #pragma unroll
-  for (int e = 0; e < N; ++e) { x0[e] = k.k0; x1[e] = i0 + (uint32_t)e + k.k1; }
+  for (int e = 0; e < N; ++e) { x0[e] = k.k0; x1[e] = idx[e] + k.k1; }
 #define NVJSEL_TF_ROUND_N(r)                                                                      \
   if constexpr (N == 4) {                                                                         \
     NVJSEL_TF4_ROUND(r);                                                                          \

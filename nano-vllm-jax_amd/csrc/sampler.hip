@@ -49,6 +49,11 @@
 namespace nvjsel {
 
 enum { ROW_GREEDY = 0, ROW_FULL = 1, ROW_FILTER = 2 };
+// Per-row words hit by same-address atomics from many blocks (best key,
+// finished-item counter) each get a 256-byte line of their own.
+static constexpr int kRowPad = 64;   // uint32 words
+static constexpr int kRowPad8 = 32;  // uint64 words
+
 enum { STATE_DONE = 1, STATE_HEAVY = 2, STATE_NEEDS_GUMBEL = 3, STATE_TOPP = 4 };
 
 static constexpr int kThreads = 256;
@@ -74,7 +79,7 @@ struct SampleArgs {
   const float* top_p;
   const uint32_t* keys;
   const float* noise;  // optional [B, V] Gumbel override
-  unsigned long long* row_key;     // [B]   zero at rest
+  unsigned long long* row_key;     // [B * kRowPad8] best key per row
   uint32_t* row_tau;               // [B]
   int32_t* row_state;              // [B]
   unsigned long long* chunk_max;   // [B, nchunks]
@@ -85,8 +90,9 @@ struct SampleArgs {
   unsigned long long* topp_cand;   // [B, kToppCap]
   uint32_t* topp_n;                // [B]
   uint32_t* list_n;                // [2]   rows queued for gumbel, for top-p
-  uint32_t* list_gumbel;           // [B]
-  uint32_t* row_done;              // [B]   gumbel items finished per row
+  uint32_t* list_gumbel;           // [B * nchunks] gumbel items: row << 16 | chunk
+  uint32_t* row_done;              // [B * kRowPad] gumbel items finished per row
+  uint32_t* row_items;             // [B * kRowPad] gumbel items queued per row
   uint32_t* list_topp;             // [B]
   int32_t* out_ids;
 };
@@ -252,29 +258,47 @@ struct GumbelShared {
   float s_cur;
 };
 
-// Gumbel-max over this thread's elements x[j] (index base + j*256 + tid) whose
-// bit in `act` is set.  Returns the block's exact best key (all threads).  The
+// Gumbel-max over this thread's elements x[j] (index elem_index(base, j)) whose
+// bit in `act` is set; s_cur is a score already reached by some element.  Returns the block's exact best key (all threads).  The
 // few near-maximal elements are queued in LDS and rescored exactly by the
 // whole block, so the fp64 path is not unrolled per element.
 template <int EPT, int VEC>
 __device__ __forceinline__ unsigned long long block_gumbel(const SampleArgs& a, int b, const TfKey& key,
                                                            const float (&x)[EPT], int base, uint32_t act,
                                                            float s_cur, GumbelShared& sh) {
+#pragma unroll
+  for (int j = 0; j < EPT; ++j)
+    if (x[j] + NVJSEL_GUMBEL_MAX < s_cur) act &= ~(1u << j);  // cannot beat a score found; NaN stays
+  // fast draws in groups of four elements: four interleaved Threefry chains,
+  // skipped when no lane of the wave needs any of the group
   float st[EPT];
   uint32_t tmax = 0;  // ord of the approximate maximum
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    st[j] = -INFINITY;
-    if (!((act >> j) & 1u)) continue;
-    const float xv = x[j];
-    if (xv + NVJSEL_GUMBEL_MAX < s_cur) {  // cannot beat an exact score already found
-      act &= ~(1u << j);
-      continue;
+  for (int g = 0; g < EPT / 4; ++g) {
+    const uint32_t gm = (act >> (4 * g)) & 0xFu;
+    float t[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    if (__any(gm != 0u)) {
+      uint32_t idx[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) idx[e] = (uint32_t)elem_index<VEC>(base, 4 * g + e);
+      if (a.noise) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = x[4 * g + e] + a.noise[(size_t)b * a.V + idx[e]];
+      } else {
+        uint32_t bits[4];
+        random_bits32_n<4>(key, idx, bits);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = x[4 * g + e] + gumbel_fast_from_bits(bits[e]);
+      }
     }
-    const int i = elem_index<VEC>(base, j);
-    st[j] = (xv != xv) ? INFINITY : xv + fast_noise(a, b, key, i);
-    const uint32_t o = ord_f32(st[j]);
-    tmax = o > tmax ? o : tmax;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool on = (gm >> e) & 1u;
+      const float v = (t[e] != t[e]) ? INFINITY : t[e];  // NaN only from a NaN logit
+      st[4 * g + e] = on ? v : -INFINITY;
+      const uint32_t o = on ? ord_f32(v) : 0u;
+      tmax = o > tmax ? o : tmax;
+    }
   }
   const unsigned long long any = block_max_u64(((unsigned long long)tmax << 32) | (act ? 1u : 0u), sh.red);
   if ((any & 1ull) == 0 && (any >> 32) == 0) return 0;  // nothing active in the block
@@ -381,7 +405,7 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   const unsigned long long cbest = block_max_u64(tkey, sh.g.red);
   if (threadIdx.x == 0) {
     a.chunk_max[(size_t)b * a.nchunks + c] = cbest;
-    if (c == 0) a.row_done[b] = 0;
+    if (c == 0) a.row_done[(size_t)b * kRowPad] = 0;
     if (b == 0 && c == 0) { a.list_n[0] = 0; a.list_n[1] = 0; }  // this call's work lists
   }
   if (rp.mode != ROW_FILTER || rp.k == 0 || rp.k > kFastK) return;
@@ -504,6 +528,55 @@ __device__ __forceinline__ unsigned long long topp_target(float p, unsigned long
   return P + 1;
 }
 
+// ------------------------------------------------------------------ gumbel work items
+// A gumbel block covers a quarter chunk (2048 elements): four times the blocks
+// of the scan, for the VALU-heavy noise.
+static constexpr int kGumbelEPT = 8;
+static constexpr int kGumbelSplit = kEPT / kGumbelEPT;
+
+// Scratch of queue_chunks.
+struct QueueShared {
+  uint32_t wsum[kThreads / 64];
+  uint32_t base;
+};
+
+// Whole block, after the row's seed `best` (an exact score some kept element
+// reaches) is known: appends a gumbel item (b << 16 | c) for every chunk c that
+// can hold the row's maximum -- it has a kept element (chunk max >= tau) whose
+// best possible score, chunk max + the largest Gumbel draw, is not below the
+// seed -- and records the row's item count for the gumbel kernel's last-item
+// test.  A row left with no item (it cannot happen: the seed's own chunk
+// qualifies) is answered with the seed.
+__device__ __forceinline__ void queue_chunks(const SampleArgs& a, int b, const RowParams& rp, uint32_t tau,
+                                             unsigned long long best, QueueShared& q) {
+  const int NC = a.nchunks;
+  const float s_seed = prune_level(best);
+  auto keep = [&](int c) {
+    if (c >= NC) return false;
+    const float xv = chunk_max_x(rp, a.chunk_max[(size_t)b * NC + c]);
+    return radix_key(xv) >= tau && !(xv + NVJSEL_GUMBEL_MAX < s_seed);
+  };
+  uint32_t mine = 0;
+  for (int c = threadIdx.x; c < NC; c += kThreads) mine += keep(c) ? 1u : 0u;
+  uint32_t total;
+  (void)block_exclusive_scan<uint32_t>(mine, q.wsum, total);
+  if (threadIdx.x == 0) {
+    q.base = total ? atomicAdd(&a.list_n[0], total) : 0u;
+    a.row_items[(size_t)b * kRowPad] = total * (uint32_t)kGumbelSplit;
+    if (total == 0) a.out_ids[b] = (int32_t)(~(uint32_t)best);
+  }
+  __syncthreads();
+  uint32_t pos = q.base;
+  for (int c0 = 0; c0 < NC; c0 += kThreads) {
+    const int c = c0 + (int)threadIdx.x;
+    const bool k = keep(c);
+    uint32_t n;
+    const uint32_t off = block_exclusive_scan<uint32_t>(k ? 1u : 0u, q.wsum, n);
+    if (k) a.list_gumbel[pos + off] = ((uint32_t)b << 16) | (uint32_t)c;
+    pos += n;
+  }
+}
+
 struct SelectShared {
   unsigned long long cand[kSelCap];
   unsigned long long kept[kKeptCap];
@@ -515,6 +588,7 @@ struct SelectShared {
   uint32_t n, nk;
   uint32_t prefix, rem;
   int flag;
+  QueueShared q;
 };
 
 __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
@@ -534,10 +608,8 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
       best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
     }
     best = block_max_u64(best, s.red);
-    if (threadIdx.x == 0) {
-      a.row_key[b] = best;
-      queue_row(&a.list_n[0], a.list_gumbel, b);
-    }
+    if (threadIdx.x == 0) a.row_key[(size_t)b * kRowPad8] = best;
+    queue_chunks(a, b, rp, 0u, best, s.q);
     return;
   }
   unsigned long long mk = 0;
@@ -830,9 +902,12 @@ struct ToppFinalShared {
   unsigned long long v[kToppCap];
 };
 
-union FinalizeShared {
-  ToppFinalShared tf;
-  HeavyShared hv;
+struct FinalizeShared {
+  union {
+    ToppFinalShared tf;
+    HeavyShared hv;
+  };
+  QueueShared q;
 };
 
 // Rows left by select: top-p-only rows (crossing bin of the histogram ->
@@ -880,72 +955,69 @@ __global__ void __launch_bounds__(kThreads) sample_finalize_kernel(SampleArgs a)
   __syncthreads();
   best = block_max_u64(best, sh.tf.t.wsum);
   if (threadIdx.x == 0) {
-    a.row_key[b] = best;
+    a.row_key[(size_t)b * kRowPad8] = best;
     a.row_tau[b] = tau;
     a.row_state[b] = STATE_NEEDS_GUMBEL;
-    queue_row(&a.list_n[0], a.list_gumbel, b);
   }
+  queue_chunks(a, b, rp, tau, best, sh.q);
 }
 
 // ------------------------------------------------------------------ 4. gumbel over kept (heavy rows)
-// A block covers a quarter chunk (2048 elements): four times the blocks of
-// the scan, for rows that need the VALU-heavy noise.
-static constexpr int kGumbelEPT = 8;
-static constexpr int kGumbelSplit = kEPT / kGumbelEPT;
-
+// Block = quarter `sub` of the chunk of item (b, c).  Every load the item needs
+// depends only on (b, c), so they are issued together; the chunk already
+// passed the prune test against the row's seed when it was queued.
 template <int DT, int VEC>
-__device__ __forceinline__ void gumbel_item(const SampleArgs& a, int b, int sub, GumbelShared& sh) {
-  const int c = sub / kGumbelSplit;
+__device__ __forceinline__ void gumbel_item(const SampleArgs& a, uint32_t item, int sub, GumbelShared& sh) {
+  const int b = (int)(item >> 16), c = (int)(item & 0xFFFFu);
   const RowParams rp = row_params(a, b);
-  const float s_cur = block_prune_level(&a.row_key[b], &sh.s_cur);
-  const float cmax = chunk_max_x(rp, a.chunk_max[(size_t)b * a.nchunks + c]);
-  unsigned long long best = 0;
-  if (!(cmax + NVJSEL_GUMBEL_MAX < s_cur)) {  // else the whole chunk is out of reach
-    const uint32_t tau = rp.mode == ROW_FILTER ? a.row_tau[b] : 0u;
-    const char* row = row_ptr(a, b);
-    const int base = sub * (kThreads * kGumbelEPT);
-    float x[kGumbelEPT];
-    uint32_t valid;
-    load_chunk_elems<DT, VEC, kGumbelEPT>(row, base, a.V, false, rp.tp, x, valid);
-    uint32_t act = 0;
+  const char* row = row_ptr(a, b);
+  const int base = (c * kGumbelSplit + sub) * (kThreads * kGumbelEPT);
+  float x[kGumbelEPT];
+  uint32_t valid;
+  load_chunk_elems<DT, VEC, kGumbelEPT>(row, base, a.V, true, 1.0f, x, valid);
+  const uint32_t tau = rp.mode == ROW_FILTER ? a.row_tau[b] : 0u;
+  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+  // the row's current best (other blocks keep raising it); read per wave
+  unsigned long long* rk = &a.row_key[(size_t)b * kRowPad8];
+  const unsigned long long seen = load_row_best(rk);
+  const float s_cur = prune_level(seen);
+  uint32_t act = 0;
 #pragma unroll
-    for (int j = 0; j < kGumbelEPT; ++j) act |= (((valid >> j) & 1u) && radix_key(x[j]) >= tau ? 1u : 0u) << j;
-    const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
-    best = block_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, act, s_cur, sh);
+  for (int j = 0; j < kGumbelEPT; ++j) {
+    x[j] = x[j] / rp.tp;
+    act |= (((valid >> j) & 1u) && radix_key(x[j]) >= tau ? 1u : 0u) << j;
   }
-  // the row's last item writes its id; counters are per row, so rows do not
-  // contend on one address
+  const unsigned long long best = block_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, act, s_cur, sh);
+  // The row's last item writes its id.  A block whose best does not exceed
+  // the value it read skips the max (the row's best only grows), halving the
+  // same-address atomics; each row's counters sit on their own cache lines.
   if (threadIdx.x == 0) {
-    const unsigned long long prev = best ? atomicMax(&a.row_key[b], best) : 0ull;
-    const uint32_t nsub = (uint32_t)(a.nchunks * kGumbelSplit);
-    if (atomicAdd(&a.row_done[b] + after(prev), 1u) == nsub - 1)
-      a.out_ids[b] = (int32_t)(~(uint32_t)load_row_best(&a.row_key[b]));
+    const unsigned long long prev = best > seen ? atomicMax(rk, best) : 0ull;
+    uint32_t* done = &a.row_done[(size_t)b * kRowPad];
+    if (atomicAdd(done + after(prev), 1u) == a.row_items[(size_t)b * kRowPad] - 1u)
+      a.out_ids[b] = (int32_t)(~(uint32_t)load_row_best(rk));
   }
 }
 
-// Grid over (queued row, quarter chunk) items: rows that need no noise cost
-// nothing here.
+// One block per possible item quarter; blocks past the queued items exit at once.
 template <int DT, int VEC>
 __global__ void __launch_bounds__(kThreads) sample_gumbel_kernel(SampleArgs a) {
   __shared__ GumbelShared sh;
-  const long long nsub = (long long)a.nchunks * kGumbelSplit;
-  const long long items = (long long)a.list_n[0] * nsub;
-  for (long long it = blockIdx.x; it < items; it += gridDim.x)
-    gumbel_item<DT, VEC>(a, (int)a.list_gumbel[it / nsub], (int)(it % nsub), sh);
+  const uint32_t it = blockIdx.x / kGumbelSplit;
+  if (it >= a.list_n[0]) return;
+  gumbel_item<DT, VEC>(a, a.list_gumbel[it], (int)(blockIdx.x % kGumbelSplit), sh);
 }
-// (launched with one block per possible item: queued items take the lowest
-// block indices, the rest exit at once, and the hardware balances the load)
 
 struct WsLayout {
   size_t row_key, row_tau, row_state, chunk_max, cand_count, cand, row_m, topp_hist, topp_cand, topp_n;
-  size_t list_n, list_gumbel, list_topp, row_done, total;
+  size_t list_n, list_gumbel, list_topp, row_done, row_items, total;
 };
 
 static WsLayout ws_layout(int B, int V) {
   const size_t nc = (size_t)((V + kChunk - 1) / kChunk);
   WsLayout w;
   size_t o = 0;
-  w.row_key = o;    o += align_up((size_t)B * 8, 256);
+  w.row_key = o;    o += (size_t)B * kRowPad8 * 8;
   w.row_tau = o;    o += align_up((size_t)B * 4, 256);
   w.row_state = o;  o += align_up((size_t)B * 4, 256);
   w.chunk_max = o;  o += align_up((size_t)B * nc * 8, 256);
@@ -956,9 +1028,10 @@ static WsLayout ws_layout(int B, int V) {
   w.topp_cand = o;  o += align_up((size_t)B * kToppCap * 8, 256);
   w.topp_n = o;     o += align_up((size_t)B * 4, 256);
   w.list_n = o;     o += 256;
-  w.list_gumbel = o; o += align_up((size_t)B * 4, 256);
+  w.list_gumbel = o; o += align_up((size_t)B * nc * 4, 256);
   w.list_topp = o;  o += align_up((size_t)B * 4, 256);
-  w.row_done = o;   o += align_up((size_t)B * 4, 256);
+  w.row_done = o;   o += (size_t)B * kRowPad * 4;
+  w.row_items = o;  o += (size_t)B * kRowPad * 4;
   w.total = o;
   return w;
 }
@@ -992,6 +1065,7 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
     return NVJSEL_EWORKSPACE;
   }
   if (batch > 65535) return fail(NVJSEL_EUNSUPPORTED, "sample: batch > 65535");
+  if ((vocab + kChunk - 1) / kChunk > 65536) return fail(NVJSEL_EUNSUPPORTED, "sample: vocab > 2^29");
   const WsLayout w = ws_layout(batch, vocab);
   char* ws = (char*)workspace;
   SampleArgs a;
@@ -1020,6 +1094,7 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   a.list_gumbel = (uint32_t*)(ws + w.list_gumbel);
   a.list_topp = (uint32_t*)(ws + w.list_topp);
   a.row_done = (uint32_t*)(ws + w.row_done);
+  a.row_items = (uint32_t*)(ws + w.row_items);
   a.out_ids = out_ids;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid_chunks(a.nchunks, batch);
