@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define NVJSEL_ABI_VERSION 1
+#define NVJSEL_ABI_VERSION 2
 
 typedef enum {
   NVJSEL_F32 = 0,
@@ -100,6 +100,43 @@ int nvjsel_lm_head_sample(const void* hidden, int hidden_dtype,
                           const float* temperature, const uint32_t* keys,
                           int32_t* out_ids,
                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Final-RMSNorm prologue variants: the same as nvjsel_lm_head_top1 /
+ * nvjsel_lm_head_sample, but `hidden` is the pre-norm hidden state and the
+ * library first forms, per row, the LM-head input of
+ * _lm_head_normed_hidden_and_weight(hidden_is_normed=False)
+ * (nanovllm_jax/model.py:734-762) with rms_norm (nanovllm_jax/layers.py:11-29):
+ *   y = x * (1 / sqrt(mean(x^2) + eps)) * (1 + norm_weight)   in fp32,
+ * rounded to hidden_dtype (rms_norm's astype(input_dtype)) and then to
+ * act_dtype (lm_head_decode_act_dtype: f32 by default, bf16 when promoted).
+ * reduce_cast applies to the act_dtype x weight_dtype dot as above.  On the
+ * streaming and bf16 tile paths the prologue runs inside the LM-head launch;
+ * otherwise a prologue kernel writes the normalised rows into the workspace.
+ * norm_weight [hidden_dim] of norm_dtype.
+ */
+size_t nvjsel_lm_head_prenorm_workspace_size(int batch, int hidden_dim);
+
+/* The prologue alone: out [batch, hidden_dim] of act_dtype receives the
+ * LM-head input described above (for callers that form dense logits). */
+int nvjsel_rms_norm(const void* hidden, int hidden_dtype, const void* norm_weight, int norm_dtype,
+                    float eps, int act_dtype, int batch, int hidden_dim, void* out, void* stream);
+
+int nvjsel_lm_head_top1_prenorm(const void* hidden, int hidden_dtype,
+                                const void* norm_weight, int norm_dtype, float eps, int act_dtype,
+                                const void* weight, int weight_dtype, int weight_layout,
+                                int batch, int hidden_dim, int vocab, int reduce_cast,
+                                int32_t* out_ids, float* out_best,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+int nvjsel_lm_head_sample_prenorm(const void* hidden, int hidden_dtype,
+                                  const void* norm_weight, int norm_dtype, float eps, int act_dtype,
+                                  const void* weight, int weight_dtype, int weight_layout,
+                                  int batch, int hidden_dim, int vocab, int reduce_cast,
+                                  const float* temperature, const uint32_t* keys,
+                                  int32_t* out_ids, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 
 /* Workspace bytes for nvjsel_sample at (batch, vocab). */
 size_t nvjsel_sample_workspace_size(int batch, int vocab);

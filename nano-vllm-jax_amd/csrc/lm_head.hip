@@ -139,7 +139,14 @@ enum { MODE_GREEDY = 0, MODE_SAMPLE = 1 };
 struct LmArgs {
   const void* W;
   const void* hidden;
-  int hidden_dtype;
+  int hidden_dtype;    // element type of `hidden` as stored
+  // final RMSNorm prologue (prenorm != 0): the kernel multiplies against
+  // act(in(rms_norm(hidden) * (1 + norm_w))) instead of `hidden`
+  int prenorm;
+  const void* norm_w;
+  int norm_dtype;
+  float eps;
+  int act_dtype;
   int weight_dtype;
   int layout;
   int B;  // rows handled by this launch
@@ -175,6 +182,23 @@ __device__ __forceinline__ uint32_t bf16_bits_rne(float v) {
   uint32_t u = __float_as_uint(v);
   if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// rounds v to element type dt (f32: unchanged)
+__device__ __forceinline__ float round_to_dtype(float v, int dt) {
+  return apply_cast(v, dt == DT_BF16 ? 1 : dt == DT_F16 ? 2 : 0);
+}
+
+// Final RMSNorm of the LM-head prologue, as layers.py:22-29 followed by the
+// activation cast of model.py:758-760: with ss = sum of x^2 over the row (fp32),
+//   y = x * (1 / sqrt(ss / H + eps)) * (1 + w), rounded to the hidden's own type
+// (rms_norm's output.astype(input_dtype)) and then to the activation type.
+__device__ __forceinline__ float prenorm_inv(const LmArgs& a, float ss) {
+  return 1.0f / sqrtf(ss / (float)a.H + a.eps);
+}
+__device__ __forceinline__ float prenorm_apply(const LmArgs& a, float x, float inv, int k) {
+  const float y = (x * inv) * (1.0f + load_as_f32(a.norm_w, a.norm_dtype, (size_t)k));
+  return round_to_dtype(round_to_dtype(y, a.hidden_dtype), a.act_dtype);
 }
 
 __device__ __forceinline__ uint32_t f16_bits(float v) {
@@ -466,6 +490,25 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         hv[b][j][e] = (b < B) ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * H + j * 512 + lane * 8 + e) : 0.0f;
+  if (a.prenorm) {
+    // the wave holds whole rows: per-lane sum of squares, then the butterfly
+    // leaves the same total in every lane (and every wave)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(hv[b][j][e], hv[b][j][e], ss);
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+      const float inv = prenorm_inv(a, ss);
+#pragma unroll
+      for (int j = 0; j < KJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) hv[b][j][e] = prenorm_apply(a, hv[b][j][e], inv, j * 512 + lane * 8 + e);
+    }
+  }
 
   float tp[NB];
   bool greedy_row[NB];
@@ -717,13 +760,31 @@ __global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) 
     }
   };
 
+  __shared__ float pre_ss[KSPLIT][ROWS];
   if (gemm) {
     const int brow = nb * 16 + r;
-    const uint16_t* hp = (const uint16_t*)a.hidden + (size_t)(brow < B ? brow : 0) * 1024;
+    if (!a.prenorm) {
+      const uint16_t* hp = (const uint16_t*)a.hidden + (size_t)(brow < B ? brow : 0) * 1024;
 #pragma unroll
-    for (int kk = 0; kk < KPW; ++kk) {
-      const int kb = ks * KPW + kk;
-      hb[kk] = brow < B ? *(const u32x4_t*)(hp + kb * 32 + g * 8) : u32x4_t{0u, 0u, 0u, 0u};
+      for (int kk = 0; kk < KPW; ++kk) {
+        const int kb = ks * KPW + kk;
+        hb[kk] = brow < B ? *(const u32x4_t*)(hp + kb * 32 + g * 8) : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    } else {
+      // RMSNorm prologue, pass 1: this lane's sum of squares; the four lanes
+      // of a row combine by butterfly, the k-split waves through LDS
+      float ss = 0.0f;
+#pragma unroll 4
+      for (int kk = 0; kk < KPW; ++kk)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = brow < B ? load_as_f32(a.hidden, a.hidden_dtype,
+                                                 (size_t)brow * 1024 + (ks * KPW + kk) * 32 + g * 8 + e) : 0.0f;
+          ss = fmaf(x, x, ss);
+        }
+      ss += __shfl_xor(ss, 16, 64);
+      ss += __shfl_xor(ss, 32, 64);
+      if (g == 0) pre_ss[ks][brow] = ss;
     }
   } else {
     if constexpr (MODE == MODE_SAMPLE) {
@@ -734,6 +795,30 @@ __global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) 
       if (erow < B) key = tf_key(a.keys[2 * erow], a.keys[2 * erow + 1]);
       if (lane == 0) qn[ew] = 0;
       qbest[ew][lane] = 0;
+    }
+  }
+
+  if (a.prenorm) {
+    __syncthreads();  // every wave: the row sums are in LDS
+    if (gemm) {
+      // pass 2: normalise, round, pack this lane's fragments
+      const int brow = nb * 16 + r;
+      float tot = 0.0f;
+#pragma unroll
+      for (int s2 = 0; s2 < KSPLIT; ++s2) tot += pre_ss[s2][brow];
+      const float inv = prenorm_inv(a, tot);
+#pragma unroll
+      for (int kk = 0; kk < KPW; ++kk) {
+        uint32_t bits[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int k = (ks * KPW + kk) * 32 + g * 8 + e;
+          const float x = brow < B ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)brow * 1024 + k) : 0.0f;
+          bits[e] = brow < B ? bf16_bits_rne(prenorm_apply(a, x, inv, k)) : 0u;
+        }
+        hb[kk] = u32x4_t{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16), bits[4] | (bits[5] << 16),
+                         bits[6] | (bits[7] << 16)};
+      }
     }
   }
 
@@ -886,6 +971,37 @@ __global__ void __launch_bounds__(256) lm_head_generic_kernel(LmArgs a) {
   finish_rows(a.row_keys, a.counter, a.B, a.out_ids, a.out_best);
 }
 
+// ------------------------------------------------------------------ RMSNorm prologue kernel
+// For the paths without a fused prologue: one block per row writes the
+// activation-typed normalised hidden (same arithmetic as prenorm_apply) into
+// the workspace, and the LM-head kernel reads it as its hidden.
+__global__ void __launch_bounds__(256) lm_prenorm_kernel(LmArgs a, void* out) {
+  __shared__ float wsum[4];
+  const int b = blockIdx.x, H = a.H;
+  float ss = 0.0f;
+  for (int k = threadIdx.x; k < H; k += 256) {
+    const float x = load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * H + k);
+    ss = fmaf(x, x, ss);
+  }
+  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float inv = prenorm_inv(a, (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]));
+  for (int k = threadIdx.x; k < H; k += 256) {
+    const float y = prenorm_apply(a, load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * H + k), inv, k);
+    const size_t i = (size_t)b * H + k;
+    if (a.act_dtype == DT_F32) ((float*)out)[i] = y;
+    else if (a.act_dtype == DT_BF16) ((uint16_t*)out)[i] = (uint16_t)bf16_bits_rne(y);
+    else ((uint16_t*)out)[i] = (uint16_t)f16_bits(y);
+  }
+}
+
+// Re-zeroes n 32-bit words (the prologue rows in the workspace), keeping the
+// workspace zero at rest for the next call whatever its shape.
+__global__ void __launch_bounds__(256) lm_zero_kernel(uint32_t* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0u;
+}
+
 // ------------------------------------------------------------------ host side
 static constexpr int kWaves = NVJSEL_LM_WAVES;
 // LDS reserved for the kernel's static shared variables (finish_rows flag).
@@ -966,12 +1082,25 @@ static int dispatch_nb(const LmArgs& a, hipStream_t s) {
 
 static size_t lm_ws_keys_bytes(int batch) { return align_up((size_t)batch * 8, 256); }
 
+// Final-RMSNorm prologue request (norm_w == nullptr: hidden is already normed).
+struct Prenorm {
+  const void* norm_w = nullptr;
+  int norm_dtype = DT_F32;
+  float eps = 0.0f;
+  int act_dtype = DT_F32;
+};
+
+static size_t lm_prenorm_bytes(int batch, int H) { return align_up((size_t)batch * H * 4, 256); }
+
 static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const void* weight,
                          int weight_dtype, int layout, int batch, int H, int V, int reduce_cast,
                          const float* temperature, const uint32_t* keys, int32_t* out_ids,
-                         float* out_best, void* workspace, size_t ws_bytes, void* stream) {
+                         float* out_best, void* workspace, size_t ws_bytes, void* stream,
+                         const Prenorm& pn = Prenorm()) {
   clear_error();
-  const char* who = mode == MODE_GREEDY ? "lm_head_top1" : "lm_head_sample";
+  const bool prenorm = pn.norm_w != nullptr;
+  const char* who = mode == MODE_GREEDY ? (prenorm ? "lm_head_top1_prenorm" : "lm_head_top1")
+                                        : (prenorm ? "lm_head_sample_prenorm" : "lm_head_sample");
   if (!hidden || !weight || !out_ids) { set_error("%s: null hidden/weight/out_ids", who); return NVJSEL_EINVAL; }
   if (batch <= 0 || H <= 0 || V <= 0) {
     set_error("%s requires non-empty dimensions (batch=%d hidden=%d vocab=%d)", who, batch, H, V);
@@ -985,19 +1114,31 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   if (layout != NVJSEL_W_VH && layout != NVJSEL_W_HV) { set_error("%s: bad weight layout %d", who, layout); return NVJSEL_EINVAL; }
   if (reduce_cast < 0 || reduce_cast > 2) { set_error("%s: reduce_cast must be 0, 1 or 2", who); return NVJSEL_EINVAL; }
   if (mode == MODE_SAMPLE && (!temperature || !keys)) { set_error("%s: null temperature/keys", who); return NVJSEL_EINVAL; }
-  if (!workspace || ws_bytes < nvjsel_lm_head_workspace_size(batch)) {
-    set_error("%s: workspace %zu bytes < required %zu", who, ws_bytes, nvjsel_lm_head_workspace_size(batch));
+  if (prenorm) {
+    if (!valid_dtype(pn.norm_dtype) || !valid_dtype(pn.act_dtype)) {
+      set_error("%s: unsupported dtype (norm=%d act=%d)", who, pn.norm_dtype, pn.act_dtype);
+      return NVJSEL_EINVAL;
+    }
+    if (!(pn.eps >= 0.0f)) { set_error("%s: eps must be >= 0", who); return NVJSEL_EINVAL; }
+  }
+  const size_t need = nvjsel_lm_head_workspace_size(batch) + (prenorm ? lm_prenorm_bytes(batch, H) : 0);
+  if (!workspace || ws_bytes < need) {
+    set_error("%s: workspace %zu bytes < required %zu", who, ws_bytes, need);
     return NVJSEL_EWORKSPACE;
   }
   hipStream_t s = (hipStream_t)stream;
   unsigned long long* row_keys = (unsigned long long*)workspace;
   unsigned int* counter = (unsigned int*)((char*)workspace + lm_ws_keys_bytes(batch));
 
+  // Paths with a fused prologue: the streaming GEMV and the bf16 tile kernel.
+  // Elsewhere the prologue kernel writes the normalised hidden into the
+  // workspace first and the LM head reads it.
+  const int eff_dtype = prenorm ? pn.act_dtype : hidden_dtype;
   const bool aligned = (((uintptr_t)weight) & 15) == 0;
   const bool bf16_mfma = layout == NVJSEL_W_VH && weight_dtype == NVJSEL_BF16 && (H % 32) == 0 && aligned;
   const bool f16_mfma = layout == NVJSEL_W_VH && weight_dtype == NVJSEL_F16 &&
-                        hidden_dtype == NVJSEL_F16 && (H % 32) == 0 && aligned;
-  const int nsplit = (bf16_mfma && hidden_dtype != NVJSEL_BF16) ? 3 : 1;
+                        eff_dtype == NVJSEL_F16 && (H % 32) == 0 && aligned;
+  const int nsplit = (bf16_mfma && eff_dtype != NVJSEL_BF16) ? 3 : 1;
   const bool gemv = layout == NVJSEL_W_VH && weight_dtype == NVJSEL_BF16 && aligned && batch <= 2 &&
                     (H == 512 || H == 1024 || H == 2048);
   // rows per launch: LDS holds H * nsplit * rows bf16 values
@@ -1011,8 +1152,24 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     if (nsplit == 3 && tiles > 1) tiles = 1;
     chunk = tiles * 16;
   }
-  const bool tile = !gemv && bf16_mfma && hidden_dtype == NVJSEL_BF16 && H == 1024 &&
-                    (((uintptr_t)hidden) & 15) == 0 && NVJSEL_USE_TILE;
+  const bool tile = !gemv && bf16_mfma && eff_dtype == NVJSEL_BF16 && H == 1024 &&
+                    (prenorm || (((uintptr_t)hidden) & 15) == 0) && NVJSEL_USE_TILE;
+  const bool fused_prenorm = prenorm && (gemv || tile);
+  if (prenorm && !fused_prenorm) {
+    LmArgs p{};
+    p.hidden = hidden;
+    p.hidden_dtype = hidden_dtype;
+    p.H = H;
+    p.norm_w = pn.norm_w;
+    p.norm_dtype = pn.norm_dtype;
+    p.eps = pn.eps;
+    p.act_dtype = pn.act_dtype;
+    void* normed = (char*)workspace + nvjsel_lm_head_workspace_size(batch);
+    hipLaunchKernelGGL(lm_prenorm_kernel, dim3(batch), dim3(256), 0, s, p, normed);
+    NVJSEL_CHECK_LAUNCH("lm_prenorm_kernel");
+    hidden = normed;
+    hidden_dtype = pn.act_dtype;
+  }
   if (tile) chunk = 64;
   if (gemv) chunk = 0;
   for (int b0 = 0; b0 < batch; b0 += (chunk > 0 ? chunk : batch)) {
@@ -1021,6 +1178,11 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     a.W = weight;
     a.hidden = (const char*)hidden + (size_t)b0 * H * dtype_size(hidden_dtype);
     a.hidden_dtype = hidden_dtype;
+    a.prenorm = fused_prenorm ? 1 : 0;
+    a.norm_w = pn.norm_w;
+    a.norm_dtype = pn.norm_dtype;
+    a.eps = pn.eps;
+    a.act_dtype = fused_prenorm ? pn.act_dtype : hidden_dtype;
     a.weight_dtype = weight_dtype;
     a.layout = layout;
     a.B = nb;
@@ -1057,6 +1219,13 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     }
     if (rc != NVJSEL_OK) return rc;
   }
+  if (prenorm && !fused_prenorm) {
+    const size_t words = lm_prenorm_bytes(batch, H) / 4;
+    const unsigned grid = (unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024);
+    hipLaunchKernelGGL(lm_zero_kernel, dim3(grid), dim3(256), 0, s,
+                       (uint32_t*)((char*)workspace + nvjsel_lm_head_workspace_size(batch)), words);
+    NVJSEL_CHECK_LAUNCH("lm_zero_kernel");
+  }
   return NVJSEL_OK;
 }
 
@@ -1076,6 +1245,65 @@ extern "C" int nvjsel_lm_head_top1(const void* hidden, int hidden_dtype, const v
   return lm_head_entry(MODE_GREEDY, hidden, hidden_dtype, weight, weight_dtype, weight_layout, batch,
                        hidden_dim, vocab, reduce_cast, nullptr, nullptr, out_ids, out_best, workspace,
                        workspace_bytes, stream);
+}
+
+extern "C" size_t nvjsel_lm_head_prenorm_workspace_size(int batch, int hidden_dim) {
+  if (batch <= 0 || hidden_dim <= 0) return 0;
+  return nvjsel_lm_head_workspace_size(batch) + lm_prenorm_bytes(batch, hidden_dim);
+}
+
+extern "C" int nvjsel_rms_norm(const void* hidden, int hidden_dtype, const void* norm_weight, int norm_dtype,
+                               float eps, int act_dtype, int batch, int hidden_dim, void* out, void* stream) {
+  clear_error();
+  if (!hidden || !norm_weight || !out) return fail(NVJSEL_EINVAL, "rms_norm: null pointer");
+  if (batch <= 0 || hidden_dim <= 0) return fail(NVJSEL_EINVAL, "rms_norm: empty dimensions");
+  if (!valid_dtype(hidden_dtype) || !valid_dtype(norm_dtype) || !valid_dtype(act_dtype))
+    return fail(NVJSEL_EINVAL, "rms_norm: unsupported dtype");
+  if (!(eps >= 0.0f)) return fail(NVJSEL_EINVAL, "rms_norm: eps must be >= 0");
+  LmArgs p{};
+  p.hidden = hidden;
+  p.hidden_dtype = hidden_dtype;
+  p.H = hidden_dim;
+  p.norm_w = norm_weight;
+  p.norm_dtype = norm_dtype;
+  p.eps = eps;
+  p.act_dtype = act_dtype;
+  hipLaunchKernelGGL(lm_prenorm_kernel, dim3(batch), dim3(256), 0, (hipStream_t)stream, p, out);
+  NVJSEL_CHECK_LAUNCH("lm_prenorm_kernel");
+  return NVJSEL_OK;
+}
+
+extern "C" int nvjsel_lm_head_top1_prenorm(const void* hidden, int hidden_dtype, const void* norm_weight,
+                                           int norm_dtype, float eps, int act_dtype, const void* weight,
+                                           int weight_dtype, int weight_layout, int batch, int hidden_dim,
+                                           int vocab, int reduce_cast, int32_t* out_ids, float* out_best,
+                                           void* workspace, size_t workspace_bytes, void* stream) {
+  if (!norm_weight) { clear_error(); set_error("lm_head_top1_prenorm: null norm_weight"); return NVJSEL_EINVAL; }
+  Prenorm pn;
+  pn.norm_w = norm_weight;
+  pn.norm_dtype = norm_dtype;
+  pn.eps = eps;
+  pn.act_dtype = act_dtype;
+  return lm_head_entry(MODE_GREEDY, hidden, hidden_dtype, weight, weight_dtype, weight_layout, batch,
+                       hidden_dim, vocab, reduce_cast, nullptr, nullptr, out_ids, out_best, workspace,
+                       workspace_bytes, stream, pn);
+}
+
+extern "C" int nvjsel_lm_head_sample_prenorm(const void* hidden, int hidden_dtype, const void* norm_weight,
+                                             int norm_dtype, float eps, int act_dtype, const void* weight,
+                                             int weight_dtype, int weight_layout, int batch, int hidden_dim,
+                                             int vocab, int reduce_cast, const float* temperature,
+                                             const uint32_t* keys, int32_t* out_ids, void* workspace,
+                                             size_t workspace_bytes, void* stream) {
+  if (!norm_weight) { clear_error(); set_error("lm_head_sample_prenorm: null norm_weight"); return NVJSEL_EINVAL; }
+  Prenorm pn;
+  pn.norm_w = norm_weight;
+  pn.norm_dtype = norm_dtype;
+  pn.eps = eps;
+  pn.act_dtype = act_dtype;
+  return lm_head_entry(MODE_SAMPLE, hidden, hidden_dtype, weight, weight_dtype, weight_layout, batch,
+                       hidden_dim, vocab, reduce_cast, temperature, keys, out_ids, nullptr, workspace,
+                       workspace_bytes, stream, pn);
 }
 
 extern "C" int nvjsel_lm_head_sample(const void* hidden, int hidden_dtype, const void* weight,

@@ -16,6 +16,7 @@ from .selection import (
     lm_head_greedy_top1_hip,
     lm_head_sample_token_ids,
     reference_reduce_cast,
+    rms_norm_hip,
     sample_token_ids,
 )
 
@@ -30,6 +31,7 @@ __all__ = [
     "lm_head_greedy_top1_impl",
     "lm_head_sample_token_ids",
     "reference_reduce_cast",
+    "rms_norm_hip",
     "sample_token_ids",
     "select_token_selection_backend",
 ]

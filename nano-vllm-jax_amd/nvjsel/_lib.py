@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libnvjsel.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, BF16, F16 = 0, 1, 2
 W_VH, W_HV = 0, 1
@@ -21,13 +21,19 @@ W_VH, W_HV = 0, 1
 STATUS = {0: "OK", -1: "EINVAL", -2: "EUNSUPPORTED", -3: "EWORKSPACE", -4: "EHIP"}
 
 # name -> (restype, argtypes); mirrors include/nvjsel.h
-_vp, _i, _sz, _i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_int64
+_vp, _i, _sz, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_int64, ctypes.c_float
 SIGNATURES = {
     "nvjsel_abi_version": (_i, []),
     "nvjsel_last_error": (ctypes.c_char_p, []),
     "nvjsel_lm_head_workspace_size": (_sz, [_i]),
     "nvjsel_lm_head_top1": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "nvjsel_lm_head_sample": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "nvjsel_lm_head_prenorm_workspace_size": (_sz, [_i, _i]),
+    "nvjsel_rms_norm": (_i, [_vp, _i, _vp, _i, _f, _i, _i, _i, _vp, _vp]),
+    "nvjsel_lm_head_top1_prenorm": (_i, [_vp, _i, _vp, _i, _f, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp,
+                                         _vp, _sz, _vp]),
+    "nvjsel_lm_head_sample_prenorm": (_i, [_vp, _i, _vp, _i, _f, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp,
+                                           _vp, _vp, _sz, _vp]),
     "nvjsel_sample_workspace_size": (_sz, [_i, _i]),
     "nvjsel_sample": (_i, [_vp, _i, _i, _i, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "nvjsel_derive_keys": (_i, [_vp, _vp, _i, _vp, _vp, _vp]),

@@ -132,13 +132,26 @@ def _flatten_hidden(hidden_norm: torch.Tensor, require_3d: bool) -> torch.Tensor
     raise ValueError("LM-head top1 requires hidden shape [B, 1, H]")
 
 
+def _prenorm_operands(norm_weight, act_dtype, hidden_dim: int, dev):
+    """The final-RMSNorm prologue's weight (on ``dev``, contiguous) and codes."""
+    if norm_weight.ndim != 1 or int(norm_weight.shape[0]) != hidden_dim:
+        raise ValueError("norm_weight must be [H]")
+    nw = norm_weight.to(dev).contiguous()
+    return nw, _dtype_code(nw, "norm_weight"), _TORCH_DTYPES.get(act_dtype)
+
+
 def lm_head_greedy_top1_hip(hidden_norm: torch.Tensor, output_weight: torch.Tensor, *,
                             weight_layout: str | None = None, reduce_cast: int | None = None,
-                            return_best: bool = False):
+                            return_best: bool = False, norm_weight: torch.Tensor | None = None,
+                            rms_norm_eps: float = 1e-6, act_dtype: torch.dtype = torch.float32):
     """Greedy token ids for ``[B, 1, H] x [H, V]`` without materialising logits.
 
     Returns int32 ``[B, 1]`` (and the winning logits ``f32[B]`` with
-    ``return_best``)."""
+    ``return_best``).  With ``norm_weight`` the input is the pre-norm hidden
+    (``hidden_is_normed=False``, model.py:734-762): the library applies the
+    final RMSNorm ``rms_norm(x, norm_weight, rms_norm_eps)`` (layers.py:11-29),
+    casts to ``act_dtype`` (``lm_head_decode_act_dtype``) and multiplies, in
+    one launch on the streaming and bf16 tile paths."""
     x = _flatten_hidden(hidden_norm, require_3d=False)
     batch, hidden_dim = int(x.shape[0]), int(x.shape[1])
     if batch <= 0 or hidden_dim <= 0 or output_weight.numel() == 0:
@@ -148,16 +161,25 @@ def lm_head_greedy_top1_hip(hidden_norm: torch.Tensor, output_weight: torch.Tens
     w, layout, vocab = _weight_operand(output_weight, weight_layout, hidden_dim)
     dev = _require_cuda(x, w)
     x = x.contiguous()
-    rc = reference_reduce_cast(x.dtype, w.dtype) if reduce_cast is None else int(reduce_cast)
+    act = x.dtype if norm_weight is None else act_dtype
+    if act not in _TORCH_DTYPES:
+        raise ValueError(f"unsupported act dtype: {act}")
+    rc = reference_reduce_cast(act, w.dtype) if reduce_cast is None else int(reduce_cast)
     out = torch.empty((batch,), dtype=torch.int32, device=dev)
     best = torch.empty((batch,), dtype=torch.float32, device=dev) if return_best else None
     stream = _stream_handle(dev)
     lib = _lib.load()
-    nbytes = lib.nvjsel_lm_head_workspace_size(batch)
-    ws = _WS.get(dev, stream, "lm_head", nbytes)
-    _lib.call("nvjsel_lm_head_top1", x.data_ptr(), hd, w.data_ptr(), wd, layout, batch, hidden_dim,
-              vocab, rc, out.data_ptr(), best.data_ptr() if best is not None else None,
-              ws.data_ptr(), ws.numel(), stream)
+    best_ptr = best.data_ptr() if best is not None else None
+    if norm_weight is None:
+        ws = _WS.get(dev, stream, "lm_head", lib.nvjsel_lm_head_workspace_size(batch))
+        _lib.call("nvjsel_lm_head_top1", x.data_ptr(), hd, w.data_ptr(), wd, layout, batch, hidden_dim,
+                  vocab, rc, out.data_ptr(), best_ptr, ws.data_ptr(), ws.numel(), stream)
+    else:
+        nw, nd, ad = _prenorm_operands(norm_weight, act, hidden_dim, dev)
+        ws = _WS.get(dev, stream, "lm_head", lib.nvjsel_lm_head_prenorm_workspace_size(batch, hidden_dim))
+        _lib.call("nvjsel_lm_head_top1_prenorm", x.data_ptr(), hd, nw.data_ptr(), nd, float(rms_norm_eps), ad,
+                  w.data_ptr(), wd, layout, batch, hidden_dim, vocab, rc, out.data_ptr(), best_ptr,
+                  ws.data_ptr(), ws.numel(), stream)
     ids = out[:, None]
     return (ids, best) if return_best else ids
 
@@ -215,12 +237,15 @@ def lm_head_sample_token_ids(hidden_norm: torch.Tensor, output_weight: torch.Ten
                              temperatures: torch.Tensor, rng_keys: torch.Tensor,
                              top_k: torch.Tensor | None = None, top_p: torch.Tensor | None = None,
                              weight_layout: str | None = None,
-                             reduce_cast: int | None = None) -> torch.Tensor:
+                             reduce_cast: int | None = None, norm_weight: torch.Tensor | None = None,
+                             rms_norm_eps: float = 1e-6,
+                             act_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """Sample token ids from the LM head (model.py:901-938).
 
     Without top-k/top-p the projection and the Gumbel-max are fused and no
     logits are written.  With them, the logits are formed once (a library
-    GEMM, rounded as the reference's dot) and handed to the sampler."""
+    GEMM, rounded as the reference's dot) and handed to the sampler.
+    ``norm_weight`` selects the pre-norm input as in lm_head_greedy_top1_hip."""
     x = _flatten_hidden(hidden_norm, require_3d=False)
     batch, hidden_dim = int(x.shape[0]), int(x.shape[1])
     if batch <= 0 or hidden_dim <= 0:
@@ -230,7 +255,13 @@ def lm_head_sample_token_ids(hidden_norm: torch.Tensor, output_weight: torch.Ten
     w, layout, vocab = _weight_operand(output_weight, weight_layout, hidden_dim)
     dev = _require_cuda(x, w)
     x = x.contiguous()
-    rc = reference_reduce_cast(x.dtype, w.dtype) if reduce_cast is None else int(reduce_cast)
+    act = x.dtype if norm_weight is None else act_dtype
+    if act not in _TORCH_DTYPES:
+        raise ValueError(f"unsupported act dtype: {act}")
+    rc = reference_reduce_cast(act, w.dtype) if reduce_cast is None else int(reduce_cast)
+    if norm_weight is not None and (top_k is not None or top_p is not None):
+        x = rms_norm_hip(x, norm_weight, rms_norm_eps, act)
+        norm_weight = None
     if top_k is not None or top_p is not None:
         wt = w.T if layout == _lib.W_VH else w
         if rc:
@@ -245,10 +276,38 @@ def lm_head_sample_token_ids(hidden_norm: torch.Tensor, output_weight: torch.Ten
     out = torch.empty((batch,), dtype=torch.int32, device=dev)
     stream = _stream_handle(dev)
     lib = _lib.load()
-    ws = _WS.get(dev, stream, "lm_head", lib.nvjsel_lm_head_workspace_size(batch))
-    _lib.call("nvjsel_lm_head_sample", x.data_ptr(), hd, w.data_ptr(), wd, layout, batch, hidden_dim,
-              vocab, rc, temps.data_ptr(), keys.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
-              stream)
+    if norm_weight is None:
+        ws = _WS.get(dev, stream, "lm_head", lib.nvjsel_lm_head_workspace_size(batch))
+        _lib.call("nvjsel_lm_head_sample", x.data_ptr(), hd, w.data_ptr(), wd, layout, batch, hidden_dim,
+                  vocab, rc, temps.data_ptr(), keys.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
+                  stream)
+    else:
+        nw, nd, ad = _prenorm_operands(norm_weight, act, hidden_dim, dev)
+        ws = _WS.get(dev, stream, "lm_head", lib.nvjsel_lm_head_prenorm_workspace_size(batch, hidden_dim))
+        _lib.call("nvjsel_lm_head_sample_prenorm", x.data_ptr(), hd, nw.data_ptr(), nd, float(rms_norm_eps), ad,
+                  w.data_ptr(), wd, layout, batch, hidden_dim, vocab, rc, temps.data_ptr(), keys.data_ptr(),
+                  out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    return out
+
+
+def rms_norm_hip(hidden: torch.Tensor, norm_weight: torch.Tensor, eps: float = 1e-6,
+                 act_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """The LM-head input of the pre-norm route as a tensor ``[B, H]`` of
+    ``act_dtype`` (rms_norm, layers.py:11-29, then the activation cast,
+    model.py:758-760), for callers that need dense logits."""
+    x = _flatten_hidden(hidden, require_3d=False)
+    batch, hidden_dim = int(x.shape[0]), int(x.shape[1])
+    if batch <= 0 or hidden_dim <= 0:
+        raise ValueError("rms_norm requires non-empty dimensions")
+    hd = _dtype_code(x, "hidden")
+    dev = _require_cuda(x)
+    x = x.contiguous()
+    nw, nd, ad = _prenorm_operands(norm_weight, act_dtype, hidden_dim, dev)
+    if ad is None:
+        raise ValueError(f"unsupported act dtype: {act_dtype}")
+    out = torch.empty((batch, hidden_dim), dtype=act_dtype, device=dev)
+    _lib.call("nvjsel_rms_norm", x.data_ptr(), hd, nw.data_ptr(), nd, float(eps), ad, batch, hidden_dim,
+              out.data_ptr(), _stream_handle(dev))
     return out
 
 

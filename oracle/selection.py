@@ -78,6 +78,21 @@ def rms_norm(x: np.ndarray, weight: np.ndarray, eps: float = 1e-6) -> np.ndarray
     return (xn * (np.float32(1.0) + np.asarray(weight, np.float32))).astype(np.float32)
 
 
+def lm_head_input(hidden: np.ndarray, norm_weight: np.ndarray | None, eps: float = 1e-6, *,
+                  hidden_dtype: str = "f32", act_dtype: str = "f32") -> np.ndarray:
+    """The LM-head operand of _lm_head_normed_hidden_and_weight (model.py:734-762).
+
+    ``norm_weight`` None: hidden is already normed (``hidden_is_normed=True``).
+    Otherwise rms_norm (layers.py:11-29) in float32 steps, its
+    ``astype(input_dtype)`` (``hidden_dtype``: "f32" / "bf16" / "f16"), then
+    the activation cast (model.py:758-760, ``act_dtype``).  Returns float32."""
+    rnd = {"f32": lambda v: np.asarray(v, np.float32), "bf16": round_bf16, "f16": round_f16}
+    x = np.asarray(hidden, np.float32)
+    if norm_weight is not None:
+        x = rnd[hidden_dtype](rms_norm(x, norm_weight, eps))
+    return rnd[act_dtype](x)
+
+
 def lm_head_logits(hidden: np.ndarray, weight: np.ndarray, *, weight_layout: str = "vh") -> np.ndarray:
     """Exact (float64) logits of ``hidden[B,H] . W``.
 

@@ -202,3 +202,31 @@ def test_rms_norm_formula():
     out = sel.rms_norm(x, w, eps=0.0)
     rms = math.sqrt((9 + 16) / 2)
     assert np.allclose(out, [[3 / rms, 2 * 4 / rms]], rtol=1e-6)
+
+
+def test_lm_head_input_pins():
+    """The pre-norm LM-head operand: closed forms, torch's RMSNorm, rounding order."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(7)
+    # constant rows normalise to +-1 whatever their scale (eps = 0, w = 0)
+    x = np.array([[3.0] * 8, [-0.25] * 8], np.float32)
+    out = sel.lm_head_input(x, np.zeros(8, np.float32), 0.0)
+    assert np.array_equal(out, np.array([[1.0] * 8, [-1.0] * 8], np.float32))
+    # against torch.nn.functional.rms_norm (fp32) times (1 + w)
+    x = rng.normal(0, 2.0, (4, 1024)).astype(np.float32)
+    w = rng.normal(0, 0.1, 1024).astype(np.float32)
+    ref = (torch.nn.functional.rms_norm(torch.from_numpy(x), (1024,), eps=1e-6)
+           * (1.0 + torch.from_numpy(w))).numpy()
+    got = sel.lm_head_input(x, w, 1e-6)
+    assert np.allclose(got, ref, rtol=4e-7 * 4, atol=0)
+    # unit mean square after the norm (w = 0)
+    got0 = sel.lm_head_input(x, np.zeros(1024, np.float32), 1e-6).astype(np.float64)
+    assert np.allclose(np.mean(got0 ** 2, axis=1), 1.0, rtol=1e-5)
+    # rounding: to the hidden's own type first, then to the activation type
+    xb = sel.round_bf16(x)
+    two = sel.lm_head_input(xb, w, 1e-6, hidden_dtype="bf16", act_dtype="f32")
+    assert np.array_equal(two, sel.round_bf16(sel.rms_norm(xb, w, 1e-6)))
+    act = sel.lm_head_input(x, w, 1e-6, hidden_dtype="f32", act_dtype="bf16")
+    assert np.array_equal(act, sel.round_bf16(got))
+    # hidden already normed: only the activation cast
+    assert np.array_equal(sel.lm_head_input(x, None, act_dtype="bf16"), sel.round_bf16(x))
