@@ -171,6 +171,26 @@ int nvjsel_sample(const void* logits, int dtype, int batch, int vocab, int64_t r
                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Top-k values and indices of logits, for the verifier / diagnostic route of
+ * lm_head_token_ids_and_topk(top_k > 0) (nanovllm_jax/model.py:893-898:
+ * jax.lax.top_k(logits.astype(float32), k); the FlashInfer radix_topk route,
+ * model.py:874-892, returns the same set).
+ *
+ * logits [batch, vocab] of dtype, rows row_stride elements apart.  For each
+ * row: out_values[b, j] (f32, the row's own elements, bitwise) and
+ * out_indices[b, j], j < k, sorted by value descending and, among equal
+ * values, by index ascending; NaN orders above every number (the first NaN
+ * first) and -0.0 equals +0.0, the argmax conventions of this library.
+ * out_indices[b, 0] is the greedy token.  1 <= k <= min(256, vocab).
+ * Workspace: nvjsel_topk_workspace_size(batch, vocab) bytes of scratch.
+ */
+size_t nvjsel_topk_workspace_size(int batch, int vocab);
+
+int nvjsel_topk(const void* logits, int dtype, int batch, int vocab, int64_t row_stride, int k,
+                float* out_values, int32_t* out_indices,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Per-row sampling keys of the executor's sampled route:
  * keys[b] = fold_in(fold_in(PRNGKey(0), uint32(slots[b])), uint32(counters[b]))
  * (nanovllm_jax/engine/model_executor.py:2131, 2214-2219), and

@@ -95,6 +95,7 @@ struct SampleArgs {
   uint32_t* row_items;             // [B * kRowPad] gumbel items queued per row
   uint32_t* list_topp;             // [B]
   int32_t* out_ids;
+  int topk;  // > 0: top-k selection (nvjsel_topk): every row FILTER with this k on raw logits
 };
 
 
@@ -112,6 +113,13 @@ struct RowParams {
 
 __device__ __forceinline__ RowParams row_params(const SampleArgs& a, int b) {
   RowParams rp;
+  if (a.topk > 0) {  // raw logits: x = l / 1 == l
+    rp.mode = ROW_FILTER;
+    rp.tp = 1.0f;
+    rp.k = a.topk;
+    rp.p = 1.0f;
+    return rp;
+  }
   const float t = a.temperature[b];
   rp.tp = temp_floor(t);
   const int k = a.top_k ? a.top_k[b] : 0;
@@ -526,6 +534,182 @@ __device__ __forceinline__ unsigned long long topp_target(float p, unsigned long
   unsigned long long P = (unsigned long long)pz;
   if (Z > 0 && P > Z - 1) P = Z - 1;
   return P + 1;
+}
+
+// ------------------------------------------------------------------ top-k values and indices
+// nvjsel_topk: the k largest logits of each row, sorted by value descending
+// and, among equal values, by index ascending (jax.lax.top_k's order; the
+// ordering is that of the argmax keys: NaN above everything, -0 == +0).
+// Values are the row's own elements read back (bitwise equal, as f32).
+// Fast path: the scan kernel's per-chunk candidates (every element at or above
+// the chunk's k-th largest per-thread maximum) meet in LDS, an exact radix
+// descent finds the k-th largest key, and a bitonic sort orders the survivors.
+// Rows holding a NaN, or whose candidates or threshold ties overflow LDS,
+// take an exact full-row path: four 8-bit radix passes over the row, then an
+// index-ordered collection.
+static constexpr int kTopkMax = 256;
+static constexpr int kTopkSort = 2048;
+
+struct TopkShared {
+  unsigned long long cand[kSelCap];
+  unsigned long long sel[kTopkSort];
+  DescShared d;
+  uint32_t off[1025];
+  uint32_t wsum32[kThreads / 64];
+  unsigned long long red[kThreads / 64];
+  uint32_t hist[256];
+  uint32_t n, prefix, rem;
+};
+
+// sort key: (ord(value) << 32) | ~index -- larger is earlier
+__device__ __forceinline__ unsigned long long topk_key(float v, uint32_t i) { return argmax_key(v, i); }
+
+// Bitonic sort of s[0..P) (P a power of two) into descending order.
+__device__ __forceinline__ void bitonic_desc(unsigned long long* s, int P) {
+  for (int size = 2; size <= P; size <<= 1)
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      __syncthreads();
+      for (int t = threadIdx.x; t < P / 2; t += blockDim.x) {
+        const int lo = (t / stride) * stride * 2 + (t % stride), hi = lo + stride;
+        const bool desc = ((lo & size) == 0);
+        const unsigned long long x = s[lo], y = s[hi];
+        if ((x < y) == desc) { s[lo] = y; s[hi] = x; }
+      }
+    }
+  __syncthreads();
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t topk_ord(const char* row, int i) {
+  return ord_f32(load_logit_t<DT>(row, i));
+}
+
+// Exact full-row path: the k-th largest ord key by four 8-bit radix passes,
+// then the elements above it and the lowest-index ties at it, in index order.
+template <int DT>
+__device__ void topk_full_row(const SampleArgs& a, const char* row, int K, TopkShared& s) {
+  const int V = a.V;
+  uint32_t prefix = 0, rem = (uint32_t)K;
+  for (int sh = 24; sh >= 0; sh -= 8) {
+    s.hist[threadIdx.x] = 0;
+    __syncthreads();
+    const uint32_t hi_mask = sh == 24 ? 0u : (0xFFFFFFFFu << (sh + 8));
+    for (int i = threadIdx.x; i < V; i += blockDim.x) {
+      const uint32_t k = topk_ord<DT>(row, i);
+      if ((k & hi_mask) == prefix) atomicAdd(&s.hist[(k >> sh) & 255u], 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t above = 0;
+      int d = 255;
+      for (; d > 0; --d) {
+        if (above + s.hist[d] >= rem) break;
+        above += s.hist[d];
+      }
+      s.prefix = prefix | ((uint32_t)d << sh);
+      s.rem = rem - above;
+    }
+    __syncthreads();
+    prefix = s.prefix;
+    rem = s.rem;
+  }
+  // prefix: the k-th largest key; rem of the elements equal to it are kept
+  // (K - rem above it).  Each thread owns a contiguous index range.
+  const int per = (V + (int)blockDim.x - 1) / (int)blockDim.x;
+  const int i0 = threadIdx.x * per, i1 = min(V, i0 + per);
+  uint32_t gt = 0, eq = 0;
+  for (int i = i0; i < i1; ++i) {
+    const uint32_t k = topk_ord<DT>(row, i);
+    gt += k > prefix;
+    eq += k == prefix;
+  }
+  uint32_t tot;
+  uint32_t pg = block_exclusive_scan<uint32_t>(gt, s.wsum32, tot);
+  uint32_t pe = block_exclusive_scan<uint32_t>(eq, s.wsum32, tot);
+  const uint32_t n_gt = (uint32_t)K - rem;
+  for (int i = i0; i < i1; ++i) {
+    const float v = load_logit_t<DT>(row, i);
+    const uint32_t k = ord_f32(v);
+    if (k > prefix) s.sel[pg++] = topk_key(v, (uint32_t)i);
+    else if (k == prefix) {
+      if (pe < rem) s.sel[n_gt + pe] = topk_key(v, (uint32_t)i);
+      ++pe;
+    }
+  }
+  __syncthreads();
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) topk_select_kernel(SampleArgs a, float* out_values, int32_t* out_indices) {
+  __shared__ TopkShared s;
+  const int b = blockIdx.x, K = a.topk, NC = a.nchunks;
+  const char* row = row_ptr(a, b);
+  // the row's maximum key tells whether it holds a NaN
+  unsigned long long mk = 0;
+  for (int c = threadIdx.x; c < NC; c += blockDim.x) mk = max_u64(mk, a.chunk_max[(size_t)b * NC + c]);
+  mk = block_max_u64(mk, s.red);
+  bool fast = (uint32_t)(mk >> 32) != 0xFFFFFFFFu;
+  int n = 0;
+  if (fast) {
+    uint32_t cnt[4], local = 0;
+    int bad = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = threadIdx.x * 4 + q;
+      cnt[q] = c < NC ? a.cand_count[(size_t)b * NC + c] : 0u;
+      bad |= cnt[q] > (uint32_t)kCandCap;
+      local += cnt[q];
+    }
+    uint32_t tot;
+    uint32_t o = block_exclusive_scan<uint32_t>(local, s.wsum32, tot);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = threadIdx.x * 4 + q;
+      if (c <= NC) s.off[c] = o;
+      o += cnt[q];
+    }
+    fast = !__syncthreads_or(bad) && tot <= (uint32_t)kSelCap;
+    n = (int)tot;
+  }
+  int m = K;  // entries of s.sel to sort
+  if (fast) {
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+      int lo = 0, hi = NC;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if ((int)s.off[mid] <= e) lo = mid; else hi = mid;
+      }
+      s.cand[e] = a.cand[((size_t)b * NC + lo) * kCandCap + (e - (int)s.off[lo])];
+    }
+    __syncthreads();
+    const uint32_t tk = lds_desc<false>(s.d, s.cand, n, (unsigned long long)K, 0.0f);
+    if (threadIdx.x == 0) s.n = 0;
+    __syncthreads();
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+      const unsigned long long c = s.cand[e];
+      if ((uint32_t)(c >> 32) >= tk) {
+        const uint32_t slot = atomicAdd(&s.n, 1u);
+        const uint32_t i = (uint32_t)c;
+        if (slot < (uint32_t)kTopkSort) s.sel[slot] = topk_key(load_logit_t<DT>(row, (int)i), i);
+      }
+    }
+    __syncthreads();
+    m = (int)s.n;
+    fast = m <= kTopkSort;
+  }
+  if (!fast) {
+    topk_full_row<DT>(a, row, K, s);
+    m = K;
+  }
+  int P = 1;
+  while (P < m) P <<= 1;
+  for (int e = m + (int)threadIdx.x; e < P; e += blockDim.x) s.sel[e] = 0ull;
+  bitonic_desc(s.sel, P);
+  for (int j = threadIdx.x; j < K; j += blockDim.x) {
+    const uint32_t i = ~(uint32_t)s.sel[j];
+    out_indices[(size_t)b * K + j] = (int32_t)i;
+    out_values[(size_t)b * K + j] = load_logit_t<DT>(row, (int)i);
+  }
 }
 
 // ------------------------------------------------------------------ gumbel work items
@@ -1040,6 +1224,35 @@ static WsLayout ws_layout(int B, int V) {
 
 using namespace nvjsel;
 
+static SampleArgs make_args(const void* logits, int dtype, int batch, int vocab, int64_t row_stride,
+                            void* workspace) {
+  const WsLayout w = ws_layout(batch, vocab);
+  char* ws = (char*)workspace;
+  SampleArgs a{};
+  a.logits = logits;
+  a.dtype = dtype;
+  a.B = batch;
+  a.V = vocab;
+  a.nchunks = (vocab + kChunk - 1) / kChunk;
+  a.stride = row_stride;
+  a.row_key = (unsigned long long*)(ws + w.row_key);
+  a.row_tau = (uint32_t*)(ws + w.row_tau);
+  a.row_state = (int32_t*)(ws + w.row_state);
+  a.chunk_max = (unsigned long long*)(ws + w.chunk_max);
+  a.cand_count = (uint32_t*)(ws + w.cand_count);
+  a.cand = (unsigned long long*)(ws + w.cand);
+  a.row_m = (float*)(ws + w.row_m);
+  a.topp_hist = (unsigned long long*)(ws + w.topp_hist);
+  a.topp_cand = (unsigned long long*)(ws + w.topp_cand);
+  a.topp_n = (uint32_t*)(ws + w.topp_n);
+  a.list_n = (uint32_t*)(ws + w.list_n);
+  a.list_gumbel = (uint32_t*)(ws + w.list_gumbel);
+  a.list_topp = (uint32_t*)(ws + w.list_topp);
+  a.row_done = (uint32_t*)(ws + w.row_done);
+  a.row_items = (uint32_t*)(ws + w.row_items);
+  return a;
+}
+
 extern "C" size_t nvjsel_sample_workspace_size(int batch, int vocab) {
   if (batch <= 0 || vocab <= 0) return 0;
   return ws_layout(batch, vocab).total;
@@ -1065,36 +1278,14 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
     return NVJSEL_EWORKSPACE;
   }
   if (batch > 65535) return fail(NVJSEL_EUNSUPPORTED, "sample: batch > 65535");
-  if ((vocab + kChunk - 1) / kChunk > 65536) return fail(NVJSEL_EUNSUPPORTED, "sample: vocab > 2^29");
-  const WsLayout w = ws_layout(batch, vocab);
-  char* ws = (char*)workspace;
-  SampleArgs a;
-  a.logits = logits;
-  a.dtype = dtype;
-  a.B = batch;
-  a.V = vocab;
-  a.nchunks = (vocab + kChunk - 1) / kChunk;
-  a.stride = row_stride;
+  // the select kernel reads up to 1024 chunk counts per row
+  if ((vocab + kChunk - 1) / kChunk > 1024) return fail(NVJSEL_EUNSUPPORTED, "sample: vocab > 2^23");
+  SampleArgs a = make_args(logits, dtype, batch, vocab, row_stride, workspace);
   a.temperature = temperature;
   a.top_k = top_k;
   a.top_p = top_p;
   a.keys = keys;
   a.noise = noise;
-  a.row_key = (unsigned long long*)(ws + w.row_key);
-  a.row_tau = (uint32_t*)(ws + w.row_tau);
-  a.row_state = (int32_t*)(ws + w.row_state);
-  a.chunk_max = (unsigned long long*)(ws + w.chunk_max);
-  a.cand_count = (uint32_t*)(ws + w.cand_count);
-  a.cand = (unsigned long long*)(ws + w.cand);
-  a.row_m = (float*)(ws + w.row_m);
-  a.topp_hist = (unsigned long long*)(ws + w.topp_hist);
-  a.topp_cand = (unsigned long long*)(ws + w.topp_cand);
-  a.topp_n = (uint32_t*)(ws + w.topp_n);
-  a.list_n = (uint32_t*)(ws + w.list_n);
-  a.list_gumbel = (uint32_t*)(ws + w.list_gumbel);
-  a.list_topp = (uint32_t*)(ws + w.list_topp);
-  a.row_done = (uint32_t*)(ws + w.row_done);
-  a.row_items = (uint32_t*)(ws + w.row_items);
   a.out_ids = out_ids;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid_chunks(a.nchunks, batch);
@@ -1130,5 +1321,51 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   }
   NVJSEL_LAUNCH_CHUNK(sample_gumbel_kernel, grid_items);
 #undef NVJSEL_LAUNCH_CHUNK
+  return NVJSEL_OK;
+}
+
+extern "C" size_t nvjsel_topk_workspace_size(int batch, int vocab) {
+  return nvjsel_sample_workspace_size(batch, vocab);
+}
+
+extern "C" int nvjsel_topk(const void* logits, int dtype, int batch, int vocab, int64_t row_stride, int k,
+                           float* out_values, int32_t* out_indices, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  clear_error();
+  if (!logits || !out_values || !out_indices) return fail(NVJSEL_EINVAL, "topk: null logits/outputs");
+  if (batch <= 0 || vocab <= 0) return fail(NVJSEL_EINVAL, "topk requires non-empty dimensions");
+  if (vocab >= 0x7FFFFFFF) return fail(NVJSEL_EINVAL, "topk: vocab too large");
+  if (!valid_dtype(dtype)) return fail(NVJSEL_EINVAL, "topk: unsupported dtype");
+  if (row_stride < vocab) return fail(NVJSEL_EINVAL, "topk: row_stride < vocab");
+  if (k < 1 || k > vocab) return fail(NVJSEL_EINVAL, "topk: k must be in [1, vocab]");
+  if (k > kTopkMax || k > kFastK) return fail(NVJSEL_EUNSUPPORTED, "topk: k > 256");
+  if (!workspace || workspace_bytes < nvjsel_topk_workspace_size(batch, vocab))
+    return fail(NVJSEL_EWORKSPACE, "topk: workspace smaller than nvjsel_topk_workspace_size");
+  if (batch > 65535) return fail(NVJSEL_EUNSUPPORTED, "topk: batch > 65535");
+  if ((vocab + kChunk - 1) / kChunk > 1024) return fail(NVJSEL_EUNSUPPORTED, "topk: vocab > 2^23");
+  SampleArgs a = make_args(logits, dtype, batch, vocab, row_stride, workspace);
+  a.topk = k;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid_chunks(a.nchunks, batch);
+  const size_t esz = dtype_size(dtype);
+  const int vec = (int)(16 / esz);
+  const bool vec_ok = (vocab % vec) == 0 && (row_stride % vec) == 0 && (((uintptr_t)logits) & 15) == 0;
+  if (dtype == NVJSEL_F32) {
+    if (vec_ok) hipLaunchKernelGGL((sample_scan_kernel<DT_F32, 4>), grid_chunks, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((sample_scan_kernel<DT_F32, 1>), grid_chunks, dim3(kThreads), 0, s, a);
+    NVJSEL_CHECK_LAUNCH("sample_scan_kernel");
+    hipLaunchKernelGGL((topk_select_kernel<DT_F32>), dim3(batch), dim3(kThreads), 0, s, a, out_values, out_indices);
+  } else if (dtype == NVJSEL_BF16) {
+    if (vec_ok) hipLaunchKernelGGL((sample_scan_kernel<DT_BF16, 8>), grid_chunks, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((sample_scan_kernel<DT_BF16, 1>), grid_chunks, dim3(kThreads), 0, s, a);
+    NVJSEL_CHECK_LAUNCH("sample_scan_kernel");
+    hipLaunchKernelGGL((topk_select_kernel<DT_BF16>), dim3(batch), dim3(kThreads), 0, s, a, out_values, out_indices);
+  } else {
+    if (vec_ok) hipLaunchKernelGGL((sample_scan_kernel<DT_F16, 8>), grid_chunks, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((sample_scan_kernel<DT_F16, 1>), grid_chunks, dim3(kThreads), 0, s, a);
+    NVJSEL_CHECK_LAUNCH("sample_scan_kernel");
+    hipLaunchKernelGGL((topk_select_kernel<DT_F16>), dim3(batch), dim3(kThreads), 0, s, a, out_values, out_indices);
+  }
+  NVJSEL_CHECK_LAUNCH("topk_select_kernel");
   return NVJSEL_OK;
 }

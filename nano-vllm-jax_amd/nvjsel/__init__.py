@@ -15,9 +15,11 @@ from .selection import (
     derive_rng_keys,
     lm_head_greedy_top1_hip,
     lm_head_sample_token_ids,
+    lm_head_token_ids_and_topk,
     reference_reduce_cast,
     rms_norm_hip,
     sample_token_ids,
+    topk_hip,
 )
 
 __all__ = [
@@ -30,8 +32,10 @@ __all__ = [
     "lm_head_greedy_top1_hip",
     "lm_head_greedy_top1_impl",
     "lm_head_sample_token_ids",
+    "lm_head_token_ids_and_topk",
     "reference_reduce_cast",
     "rms_norm_hip",
     "sample_token_ids",
     "select_token_selection_backend",
+    "topk_hip",
 ]

@@ -325,3 +325,72 @@ def derive_rng_keys(slots: torch.Tensor, counters: torch.Tensor):
     _lib.call("nvjsel_derive_keys", s.data_ptr(), c.data_ptr(), s.numel(), keys.data_ptr(),
               nxt.data_ptr(), _stream_handle(dev))
     return keys, nxt
+
+
+def topk_hip(logits: torch.Tensor, k: int):
+    """``jax.lax.top_k(logits.astype(float32), k)`` over the last axis of
+    ``logits [B, V]`` (or ``[B, 1, V]``): values f32 ``[B, k]`` (the logits'
+    own values) and indices int32 ``[B, k]``, by value descending then index
+    ascending (NaN first, -0.0 == +0.0)."""
+    squeeze = logits.ndim == 3
+    if squeeze:
+        if int(logits.shape[1]) != 1:
+            raise ValueError("topk takes logits [B, V] or [B, 1, V]")
+        logits = logits[:, 0, :]
+    if logits.ndim != 2:
+        raise ValueError("topk takes logits [B, V] or [B, 1, V]")
+    batch, vocab = int(logits.shape[0]), int(logits.shape[1])
+    k = int(k)
+    if batch <= 0 or vocab <= 0:
+        raise ValueError("topk requires non-empty dimensions")
+    if not 1 <= k <= vocab:
+        raise ValueError("top_k must be in [1, vocab]")
+    dt = _dtype_code(logits, "logits")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    dev = _require_cuda(logits)
+    values = torch.empty((batch, k), dtype=torch.float32, device=dev)
+    indices = torch.empty((batch, k), dtype=torch.int32, device=dev)
+    stream = _stream_handle(dev)
+    lib = _lib.load()
+    ws = _WS.get(dev, stream, "sample", lib.nvjsel_topk_workspace_size(batch, vocab))
+    _lib.call("nvjsel_topk", logits.data_ptr(), dt, batch, vocab, int(logits.stride(0)), k, values.data_ptr(),
+              indices.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    if squeeze:
+        return values[:, None, :], indices[:, None, :]
+    return values, indices
+
+
+def lm_head_token_ids_and_topk(hidden: torch.Tensor, output_weight: torch.Tensor, *, top_k: int = 0,
+                               norm_weight: torch.Tensor | None = None, rms_norm_eps: float = 1e-6,
+                               act_dtype: torch.dtype = torch.float32, weight_layout: str | None = None,
+                               reduce_cast: int | None = None):
+    """Greedy token ids and optional top-k of the LM head (model.py:833-898).
+
+    ``hidden [B, W, H]`` (W > 1: MTP / verifier width, flattened to B*W rows as
+    model.py:862-865) or ``[B, H]``; ``norm_weight`` given: pre-norm input.
+    ``top_k == 0``: the fused greedy route, returns ``(ids int32[B, W], None,
+    None)``.  ``top_k > 0``: dense logits (the reference's dot: bf16 x bf16
+    rounds to bf16) and ``topk_hip``; returns ``(ids, values f32[B, W, k],
+    indices int32[B, W, k])`` with ``ids = indices[..., 0]``, the argmax."""
+    if hidden.ndim == 2:
+        hidden = hidden[:, None, :]
+    if hidden.ndim != 3:
+        raise ValueError("hidden must be [B, W, H] or [B, H]")
+    batch, width, hidden_dim = (int(d) for d in hidden.shape)
+    flat = hidden.reshape(batch * width, hidden_dim)
+    if int(top_k) == 0:
+        ids = lm_head_greedy_top1_hip(flat, output_weight, weight_layout=weight_layout, reduce_cast=reduce_cast,
+                                      norm_weight=norm_weight, rms_norm_eps=rms_norm_eps, act_dtype=act_dtype)
+        return ids.reshape(batch, width), None, None
+    w, layout, vocab = _weight_operand(output_weight, weight_layout, hidden_dim)
+    x = flat if norm_weight is None else rms_norm_hip(flat, norm_weight, rms_norm_eps, act_dtype)
+    rc = reference_reduce_cast(x.dtype, w.dtype) if reduce_cast is None else int(reduce_cast)
+    wt = w.T if layout == _lib.W_VH else w
+    if rc:
+        logits = torch.matmul(x.contiguous(), wt)
+    else:
+        logits = torch.matmul(x.float(), wt.float())
+    values, indices = topk_hip(logits, int(top_k))
+    ids = indices[:, 0].reshape(batch, width)
+    return ids, values.reshape(batch, width, -1), indices.reshape(batch, width, -1)

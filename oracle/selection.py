@@ -250,3 +250,28 @@ def sample_rows(logits: np.ndarray, temperature, top_k, top_p, keys, noise=None)
         out[b] = r["id"]
         info.append(r)
     return out, info
+
+
+def order_key(x: np.ndarray) -> np.ndarray:
+    """Total-order key of float32 values as used by the library's argmax and
+    top-k: larger value -> larger key; every NaN above +inf; -0.0 == +0.0."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).copy()
+    u[np.isnan(np.asarray(x, np.float32))] = 0x7FFFFFFF
+    u[u == 0x80000000] = 0
+    neg = (u & 0x80000000) != 0
+    return np.where(neg, ~u, u | np.uint32(0x80000000)).astype(np.uint64)
+
+
+def topk(logits: np.ndarray, k: int):
+    """jax.lax.top_k(logits.astype(float32), k) (model.py:896) per row: values
+    (the elements themselves) and int32 indices by value descending, then
+    index ascending, with order_key's NaN / signed-zero conventions."""
+    x = np.atleast_2d(np.asarray(logits, np.float32))
+    vals = np.empty((x.shape[0], k), np.float32)
+    idx = np.empty((x.shape[0], k), np.int32)
+    for b in range(x.shape[0]):
+        key = order_key(x[b])
+        order = np.lexsort((np.arange(x.shape[1]), -key.astype(np.int64)))[:k]
+        idx[b] = order
+        vals[b] = x[b][order]
+    return vals, idx

@@ -230,3 +230,33 @@ def test_lm_head_input_pins():
     assert np.array_equal(act, sel.round_bf16(got))
     # hidden already normed: only the activation cast
     assert np.array_equal(sel.lm_head_input(x, None, act_dtype="bf16"), sel.round_bf16(x))
+
+
+def test_topk_oracle_pins():
+    """Top-k order: textbook stable sort for finite data, torch.topk values,
+    argmax agreement (first NaN, -0 == +0), brute force on tiny rows."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(3)
+    x = rng.normal(0, 1, (3, 1000)).astype(np.float32)
+    x[:, 10] = x[:, 20] = x[:, 900] = 7.0  # ties at the top keep index order
+    v, i = sel.topk(x, 17)
+    for b in range(3):
+        assert np.array_equal(i[b], np.argsort(-x[b], kind="stable")[:17])
+    tv, _ = torch.topk(torch.from_numpy(x), 17, sorted=True)
+    assert np.array_equal(v, tv.numpy())
+    assert np.array_equal(i[:, :3], np.array([[10, 20, 900]] * 3))
+    # NaN orders first (the first NaN first), then +inf; signed zeros tie
+    y = np.array([1.0, np.nan, -0.0, np.inf, 0.0, np.nan, -np.inf], np.float32)
+    v, i = sel.topk(y, 7)
+    assert i[0].tolist() == [1, 5, 3, 0, 2, 4, 6]
+    assert np.array_equal(v[0].view(np.uint32), y[i[0]].view(np.uint32))
+    assert sel.topk(y, 1)[1][0, 0] == jr.argmax_first(y[None])[0]
+    assert sel.topk(np.array([[-0.0, 0.0]], np.float32), 1)[1][0, 0] == 0
+    # brute force over all permutations of a tiny row with ties
+    import itertools
+    base = np.array([2.0, -1.0, 2.0, 0.5, -1.0], np.float32)
+    for perm in itertools.permutations(range(5)):
+        row = base[list(perm)]
+        got = sel.topk(row, 3)[1][0].tolist()
+        exp = sorted(range(5), key=lambda j: (-row[j], j))[:3]
+        assert got == exp
