@@ -200,6 +200,18 @@ int nvjsel_topk(const void* logits, int dtype, int batch, int vocab, int64_t row
 int nvjsel_derive_keys(const int32_t* slots, const int32_t* counters, int batch,
                        uint32_t* keys, int32_t* counters_out, void* stream);
 
+/*
+ * The same keys from a device-resident counter table, with the table bumped
+ * in the same launch (nanovllm_jax/engine/model_executor.py:3593-3619:
+ * counters = table[slot_ids]; keys = fold_in(fold_in(PRNGKey(0), slot),
+ * counter); table.at[slot_ids].set(counters + 1)).  Negative slots read slot 0
+ * (model_runner.py:4785); slots >= num_slots read the last entry and are not
+ * written (jnp gather clamps, scatter drops).  Rows sharing a slot read the
+ * same counter.  counter_table [num_slots] int32, updated in place.
+ */
+int nvjsel_derive_keys_table(const int32_t* slots, int batch, int32_t* counter_table, int num_slots,
+                             uint32_t* keys, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

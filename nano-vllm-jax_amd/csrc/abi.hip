@@ -66,6 +66,32 @@ __global__ void derive_keys_kernel(const int32_t* __restrict__ slots,
   if (counters_out) counters_out[b] = ctr + 1;
 }
 
+// Device-resident counter table (model_executor.py:3593-3619): one block
+// reads every row's counter, derives the keys, and after a barrier writes
+// counter + 1 back -- `.at[slot_ids].set(counters + 1)`, so duplicate slots in
+// a batch read the same counter and store the same successor.
+__global__ void __launch_bounds__(256) derive_keys_table_kernel(const int32_t* __restrict__ slots, int batch,
+                                                                int32_t* table, int num_slots,
+                                                                uint32_t* __restrict__ keys) {
+  for (int b0 = 0; b0 < batch; b0 += 256) {
+    const int b = b0 + (int)threadIdx.x;
+    int32_t slot = 0, ctr = 0;
+    if (b < batch) {
+      slot = slots[b];
+      if (slot < 0) slot = 0;  // the executor's max(0, slot) for padding rows
+      ctr = table[slot < num_slots ? slot : num_slots - 1];  // a gather clamps (jnp indexing)
+      uint32_t a0, a1, c0, c1;
+      threefry2x32(tf_key(0u, 0u), 0u, (uint32_t)slot, a0, a1);
+      threefry2x32(tf_key(a0, a1), 0u, (uint32_t)ctr, c0, c1);
+      keys[2 * b] = c0;
+      keys[2 * b + 1] = c1;
+    }
+    __syncthreads();  // every read of this round before any write
+    if (b < batch && slot < num_slots) table[slot] = ctr + 1;  // a scatter drops out-of-range rows
+    __syncthreads();
+  }
+}
+
 }  // namespace nvjsel
 
 using namespace nvjsel;
@@ -84,5 +110,16 @@ extern "C" int nvjsel_derive_keys(const int32_t* slots, const int32_t* counters,
   hipLaunchKernelGGL(derive_keys_kernel, dim3(blocks), dim3(threads), 0, (hipStream_t)stream,
                      slots, counters, batch, keys, counters_out);
   NVJSEL_CHECK_LAUNCH("derive_keys_kernel");
+  return NVJSEL_OK;
+}
+
+extern "C" int nvjsel_derive_keys_table(const int32_t* slots, int batch, int32_t* counter_table, int num_slots,
+                                        uint32_t* keys, void* stream) {
+  clear_error();
+  if (!slots || !counter_table || !keys) return fail(NVJSEL_EINVAL, "derive_keys_table: null pointer");
+  if (batch <= 0 || num_slots <= 0) return fail(NVJSEL_EINVAL, "derive_keys_table: empty batch or table");
+  hipLaunchKernelGGL(derive_keys_table_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, slots, batch,
+                     counter_table, num_slots, keys);
+  NVJSEL_CHECK_LAUNCH("derive_keys_table_kernel");
   return NVJSEL_OK;
 }

@@ -9,14 +9,18 @@ from .registry import (
     KernelBackendUnavailable,
     available_backends,
     lm_head_greedy_top1_impl,
+    mtp_lm_head_greedy_top1_impl,
     select_token_selection_backend,
 )
 from .selection import (
     derive_rng_keys,
+    derive_rng_keys_from_table,
     lm_head_greedy_top1_hip,
     lm_head_sample_token_ids,
     lm_head_token_ids_and_topk,
+    mtp_greedy_top1_token_ids,
     reference_reduce_cast,
+    reset_rng_counters,
     rms_norm_hip,
     sample_token_ids,
     topk_hip,
@@ -28,12 +32,16 @@ __all__ = [
     "KernelBackendUnavailable",
     "available_backends",
     "derive_rng_keys",
+    "derive_rng_keys_from_table",
     "load",
     "lm_head_greedy_top1_hip",
     "lm_head_greedy_top1_impl",
     "lm_head_sample_token_ids",
     "lm_head_token_ids_and_topk",
+    "mtp_greedy_top1_token_ids",
+    "mtp_lm_head_greedy_top1_impl",
     "reference_reduce_cast",
+    "reset_rng_counters",
     "rms_norm_hip",
     "sample_token_ids",
     "select_token_selection_backend",

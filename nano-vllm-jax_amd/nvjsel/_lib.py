@@ -37,6 +37,7 @@ SIGNATURES = {
     "nvjsel_sample_workspace_size": (_sz, [_i, _i]),
     "nvjsel_sample": (_i, [_vp, _i, _i, _i, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "nvjsel_derive_keys": (_i, [_vp, _vp, _i, _vp, _vp, _vp]),
+    "nvjsel_derive_keys_table": (_i, [_vp, _i, _vp, _i, _vp, _vp]),
     "nvjsel_topk_workspace_size": (_sz, [_i, _i]),
     "nvjsel_topk": (_i, [_vp, _i, _i, _i, _i64, _i, _vp, _vp, _vp, _sz, _vp]),
 }

@@ -50,7 +50,10 @@ _SPECS = {
         aliases=("hip", "rocm", "nvjsel", "mi355x", "gfx950", "auto"),
         provided_kernels=(
             "lm_head_greedy_top1",
+            "lm_head_greedy_top1_prenorm",
             "lm_head_sample",
+            "lm_head_topk",
+            "mtp_greedy_top1",
             "sample_topk_topp",
             "derive_rng_keys",
         ),
@@ -74,6 +77,20 @@ def lm_head_greedy_top1_impl(value: str | None) -> str:
     raise ValueError(
         "lm_head_greedy_top1_impl must be jax, triton, cutlass, or hip, "
         f"got {value!r}")
+
+
+def mtp_lm_head_greedy_top1_impl(value: str | None) -> str:
+    """Normalise ``mtp_lm_head_greedy_top1_impl`` (mtp/mtp_layer.py:225-247 plus "hip")."""
+    v = str(value or "jax").strip().lower()
+    if v in {"jax", "", "none"}:
+        return "jax"
+    if v in {"triton", "triton_tensorcore", "triton_top1"}:
+        return "triton"
+    if v in {"cutlass", "cutlass_top1", "cutlass_fused_gemm", "fused_gemm"}:
+        return "cutlass"
+    if v in {"hip", "hip_mfma", "rocm", "nvjsel"}:
+        return "hip"
+    raise ValueError(f"unsupported MTP greedy top1 implementation: {value!r}")
 
 
 def _normalize(name: str | None) -> str:

@@ -394,3 +394,45 @@ def lm_head_token_ids_and_topk(hidden: torch.Tensor, output_weight: torch.Tensor
     values, indices = topk_hip(logits, int(top_k))
     ids = indices[:, 0].reshape(batch, width)
     return ids, values.reshape(batch, width, -1), indices.reshape(batch, width, -1)
+
+
+def mtp_greedy_top1_token_ids(x_normed: torch.Tensor, output_weight: torch.Tensor, *,
+                              weight_layout: str | None = None) -> torch.Tensor:
+    """MTP draft seeding with the HIP top-1 (_mtp_greedy_top1_token_ids,
+    mtp/mtp_layer.py:220-248, its Triton branch): ``x_normed [B, T, H]`` is
+    cast to the weight's dtype (the contract of
+    tests/test_mtp_layer_contract.py:155-178), T > 1 is flattened to B*T rows
+    and reshaped back.  Returns int32 ``[B, T]``."""
+    if x_normed.ndim != 3:
+        raise ValueError("HIP MTP greedy top1 expects hidden shape [B, T, H]")
+    batch, seq_len, hidden_dim = (int(d) for d in x_normed.shape)
+    flat = x_normed.reshape(batch * seq_len, 1, hidden_dim).to(output_weight.dtype)
+    ids = lm_head_greedy_top1_hip(flat, output_weight, weight_layout=weight_layout)
+    return ids.reshape(batch, seq_len)
+
+
+def derive_rng_keys_from_table(slots: torch.Tensor, counter_table: torch.Tensor) -> torch.Tensor:
+    """Keys for the rows' slots from the device-resident counter table, which
+    is advanced in place (model_executor.py:3593-3619).  ``counter_table`` is
+    int32 ``[num_slots]`` on the device; returns keys int32 ``[B, 2]`` (uint32
+    bit patterns) for the samplers' ``rng_keys``."""
+    dev = _require_cuda(slots, counter_table)
+    if counter_table.dtype != torch.int32 or counter_table.ndim != 1 or not counter_table.is_contiguous():
+        raise ValueError("counter_table must be a contiguous int32 [num_slots] tensor")
+    s = slots.to(dtype=torch.int32).reshape(-1).contiguous()
+    if s.numel() == 0 or counter_table.numel() == 0:
+        raise ValueError("slots and counter_table must be non-empty")
+    keys = torch.empty((s.numel(), 2), dtype=torch.int32, device=dev)
+    _lib.call("nvjsel_derive_keys_table", s.data_ptr(), s.numel(), counter_table.data_ptr(),
+              counter_table.numel(), keys.data_ptr(), _stream_handle(dev))
+    return keys
+
+
+def reset_rng_counters(counter_table: torch.Tensor, slots) -> None:
+    """Zero the counters of released / reused slots
+    (_flush_resident_rng_counter_resets, model_runner.py:4801-4815)."""
+    idx = torch.as_tensor(list(slots) if not torch.is_tensor(slots) else slots, dtype=torch.long,
+                          device=counter_table.device).reshape(-1)
+    idx = idx[idx >= 0]
+    if idx.numel():
+        counter_table.index_fill_(0, idx, 0)

@@ -122,3 +122,16 @@ def test_product_code_never_imports_the_oracle():
         assert "oracle" not in f.read_text(), f
     bench = (root / "bench.py").read_text()
     assert "import oracle" not in bench and "from oracle" not in bench
+
+
+def test_mtp_registry_and_shape_contract():
+    assert registry.mtp_lm_head_greedy_top1_impl(None) == "jax"
+    assert registry.mtp_lm_head_greedy_top1_impl("triton_top1") == "triton"
+    assert registry.mtp_lm_head_greedy_top1_impl("fused_gemm") == "cutlass"
+    assert registry.mtp_lm_head_greedy_top1_impl("HIP") == "hip"
+    with pytest.raises(ValueError):
+        registry.mtp_lm_head_greedy_top1_impl("bogus")
+    torch = pytest.importorskip("torch")
+    import nvjsel
+    with pytest.raises(ValueError, match=r"\[B, T, H\]"):
+        nvjsel.mtp_greedy_top1_token_ids(torch.zeros(2, 8), torch.zeros(16, 8, dtype=torch.bfloat16))

@@ -176,3 +176,18 @@ def test_fused_lm_head_sample_full_vocab_c4():
     z = sel.lm_head_logits(h.float().numpy(), W.float().numpy())
     namb = check_fused_sampled(ids.cpu().numpy(), z, [1.0] * B, keys, 1, "C4")
     assert namb <= 4
+
+
+@pytest.mark.parametrize("seq_len", [1, 3])
+def test_mtp_draft_top1_casts_and_flattens(seq_len):
+    """mtp/mtp_layer.py:220-248: fp32 x_normed [B, T, H] cast to the weight's
+    bf16, T > 1 flattened to B*T rows and reshaped to [B, T]."""
+    rng = np.random.default_rng(40 + seq_len)
+    B, H, V = 2, 1024, 4099
+    x = rng.standard_normal((B, seq_len, H)).astype(np.float32)
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.02)
+    ids = nvjsel.mtp_greedy_top1_token_ids(torch.from_numpy(x).cuda(), W, weight_layout="vh")
+    torch.cuda.synchronize()
+    assert tuple(ids.shape) == (B, seq_len) and ids.dtype == torch.int32
+    xb = sel.round_bf16(x.reshape(-1, H))  # the cast the contract requires
+    check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(xb, as_f32(W)), 1, f"mtp T={seq_len}")

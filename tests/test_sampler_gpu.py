@@ -162,6 +162,33 @@ def test_derive_keys_matches_fold_in_chain():
     assert np.array_equal(nxt.cpu().numpy(), (counters.astype(np.int64) + 1).astype(np.int32))
 
 
+def test_counter_table_keys_and_bump():
+    """Device-resident counters (model_executor.py:3593-3619): gather, fold_in
+    chain, table.at[slots].set(counter + 1); negative slots use slot 0, slots
+    past the table read its last entry and are not written."""
+    table = torch.zeros(16, dtype=torch.int32).cuda()
+    table[15] = 9
+    slots = np.array([3, 5, -1, 3, 20, 15], np.int32)
+    st = torch.from_numpy(slots).cuda()
+    for step in range(3):
+        before = table.cpu().numpy().copy()
+        keys = nvjsel.derive_rng_keys_from_table(st, table)
+        torch.cuda.synchronize()
+        got = keys.cpu().numpy().view(np.uint32)
+        for b, slot in enumerate(slots):
+            s_eff = max(0, int(slot))
+            ctr = int(before[min(s_eff, 15)])
+            exp = jr.engine_key(s_eff, ctr)
+            assert tuple(int(x) for x in got[b]) == (int(exp[0]), int(exp[1])), (step, b)
+        after = table.cpu().numpy()
+        exp_after = before.copy()
+        for slot in (3, 5, 0, 15):
+            exp_after[slot] = before[slot] + 1
+        assert np.array_equal(after, exp_after), (step, after, exp_after)
+    nvjsel.reset_rng_counters(table, [3, -1])
+    assert int(table[3]) == 0 and int(table[5]) == 3
+
+
 def test_repeated_calls_leave_workspace_clean():
     rng = np.random.default_rng(9)
     for trial in range(3):
