@@ -34,7 +34,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,x1,x2")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -217,6 +217,39 @@ def build_configs(torch, which):
 
         cfgs.append(Cfg("c5_mixed_b256_bf16", B, B * V_FULL * 2, launch, "sample_gumbel_kernel",
                         "mixed per-row T/top-k/top-p, bf16 logits [256,248320]"))
+    if "x1" in which:  # the final-RMSNorm prologue fused into the C1 launch
+        Ws = weights()
+        h = (torch.randn(1, H_FULL, device=dev, generator=gen) * 4).to(torch.bfloat16)
+        nw = (torch.randn(H_FULL, device=dev, generator=gen) * 0.1).float()
+        out = torch.empty(1, dtype=torch.int32, device=dev)
+        w = ws(lib.nvjsel_lm_head_prenorm_workspace_size(1, H_FULL))
+        state = {"i": 0}
+
+        def launch(Ws=Ws, h=h, nw=nw, out=out, w=w, state=state):
+            Wi = Ws[state["i"] & 1]
+            state["i"] += 1
+            rc = lib.nvjsel_lm_head_top1_prenorm(h.data_ptr(), 1, nw.data_ptr(), 0, 1e-6, 1, Wi.data_ptr(), 1, 0,
+                                                 1, H_FULL, V_FULL, 1, out.data_ptr(), None, w.data_ptr(),
+                                                 w.numel(), stream())
+            assert rc == 0, lib.nvjsel_last_error()
+
+        cfgs.append(Cfg("x1_prenorm_greedy_lm_head_b1", 1, V_FULL * H_FULL * 2 + H_FULL * 2, launch,
+                        "lm_head_gemv_kernel", "C1 with the final RMSNorm applied in the launch (bf16 act)"))
+
+    if "x2" in which:  # top-k values/indices of the verifier route on the C3 logits shape
+        B, K = 64, 50
+        l = _zipf_rows(torch, gen, B, V_FULL, 1.1, 1.1, 0.5, dev).float().contiguous()
+        vals = torch.empty(B, K, dtype=torch.float32, device=dev)
+        idx = torch.empty(B, K, dtype=torch.int32, device=dev)
+        w = ws(lib.nvjsel_topk_workspace_size(B, V_FULL))
+
+        def launch(l=l, vals=vals, idx=idx, w=w, B=B, K=K):
+            rc = lib.nvjsel_topk(l.data_ptr(), 0, B, V_FULL, V_FULL, K, vals.data_ptr(), idx.data_ptr(),
+                                 w.data_ptr(), w.numel(), stream())
+            assert rc == 0, lib.nvjsel_last_error()
+
+        cfgs.append(Cfg("x2_topk50_b64", B, B * V_FULL * 4, launch, "topk_select_kernel",
+                        "top-k values+indices k=50, f32 logits [64,248320] Zipf(1.1)"))
     torch.cuda.synchronize()
     return cfgs
 

@@ -106,12 +106,18 @@ __device__ __forceinline__ void static_for(F&& f) {
 // constant and no register holding an in-flight load is ever copied (a copy
 // would wait for the load, collapsing the ring to one item in flight).  The
 // main loop issues its loads unconditionally, so the compiler's wait counts
-// keep DEPTH - 1 items in flight; only the tail tests bounds.
-template <int DEPTH, typename Load, typename Body>
-__device__ __forceinline__ void ring_pipeline(int n, Load&& load, Body&& body) {
+// keep DEPTH - 1 items in flight; only the tail tests bounds.  pre() runs
+// once the first loads are issued, so set-up work overlaps them.
+struct NoPrologue {
+  __device__ void operator()() const {}
+};
+
+template <int DEPTH, typename Load, typename Body, typename Pre = NoPrologue>
+__device__ __forceinline__ void ring_pipeline(int n, Load&& load, Body&& body, Pre&& pre = Pre()) {
   static_for<DEPTH - 1>([&](auto D) NVJSEL_INLINE {
     if (decltype(D)::value < n) load(D, (int)decltype(D)::value);
   });
+  pre();  // work that can overlap the first loads
   int i = 0;
   for (; i + 2 * DEPTH - 2 < n; i += DEPTH)
     static_for<DEPTH>([&](auto D) NVJSEL_INLINE {
@@ -196,9 +202,12 @@ __device__ __forceinline__ float round_to_dtype(float v, int dt) {
 __device__ __forceinline__ float prenorm_inv(const LmArgs& a, float ss) {
   return 1.0f / sqrtf(ss / (float)a.H + a.eps);
 }
-__device__ __forceinline__ float prenorm_apply(const LmArgs& a, float x, float inv, int k) {
-  const float y = (x * inv) * (1.0f + load_as_f32(a.norm_w, a.norm_dtype, (size_t)k));
+__device__ __forceinline__ float prenorm_apply_w(const LmArgs& a, float x, float inv, float w) {
+  const float y = (x * inv) * (1.0f + w);
   return round_to_dtype(round_to_dtype(y, a.hidden_dtype), a.act_dtype);
+}
+__device__ __forceinline__ float prenorm_apply(const LmArgs& a, float x, float inv, int k) {
+  return prenorm_apply_w(a, x, inv, load_as_f32(a.norm_w, a.norm_dtype, (size_t)k));
 }
 
 __device__ __forceinline__ uint32_t f16_bits(float v) {
@@ -490,7 +499,17 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         hv[b][j][e] = (b < B) ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * H + j * 512 + lane * 8 + e) : 0.0f;
+  // RMSNorm prologue: its operands are requested with the hidden, and it runs
+  // once the first weight groups are in flight (finish_prenorm below)
+  float nwv[KJ][8] = {};
   if (a.prenorm) {
+#pragma unroll
+    for (int j = 0; j < KJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) nwv[j][e] = load_as_f32(a.norm_w, a.norm_dtype, j * 512 + lane * 8 + e);
+  }
+  auto finish_prenorm = [&]() NVJSEL_INLINE {
+    if (!a.prenorm) return;
     // the wave holds whole rows: per-lane sum of squares, then the butterfly
     // leaves the same total in every lane (and every wave)
 #pragma unroll
@@ -506,9 +525,9 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
 #pragma unroll
       for (int j = 0; j < KJ; ++j)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) hv[b][j][e] = prenorm_apply(a, hv[b][j][e], inv, j * 512 + lane * 8 + e);
+        for (int e = 0; e < 8; ++e) hv[b][j][e] = prenorm_apply_w(a, hv[b][j][e], inv, nwv[j][e]);
     }
-  }
+  };
 
   float tp[NB];
   bool greedy_row[NB];
@@ -641,7 +660,7 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
   if constexpr (MODE == MODE_SAMPLE) {
     ring_pipeline<DEPTH>(
         n_mine, [&](auto S, int j) NVJSEL_INLINE { load_grp(ring[decltype(S)::value], gid(j)); },
-        [&](auto S, int i) NVJSEL_INLINE { proc_grp(ring[decltype(S)::value], gid(i)); });
+        [&](auto S, int i) NVJSEL_INLINE { proc_grp(ring[decltype(S)::value], gid(i)); }, finish_prenorm);
   } else {
     // Greedy streams fastest (measured) with the shifting ring: the register
     // copies wait for every outstanding load at the top of each step, so one
@@ -649,6 +668,7 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
 #pragma unroll
     for (int d = 0; d < DEPTH - 1; ++d)
       if (d < n_mine) load_grp(ring[d], gid(d));
+    finish_prenorm();
     for (int i = 0; i < n_mine; ++i) {
       if (i + DEPTH - 1 < n_mine) load_grp(ring[DEPTH - 1], gid(i + DEPTH - 1));
       proc_grp(ring[0], gid(i));
@@ -798,34 +818,35 @@ __global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) 
     }
   }
 
-  if (a.prenorm) {
-    __syncthreads();  // every wave: the row sums are in LDS
-    if (gemm) {
-      // pass 2: normalise, round, pack this lane's fragments
-      const int brow = nb * 16 + r;
-      float tot = 0.0f;
-#pragma unroll
-      for (int s2 = 0; s2 < KSPLIT; ++s2) tot += pre_ss[s2][brow];
-      const float inv = prenorm_inv(a, tot);
-#pragma unroll
-      for (int kk = 0; kk < KPW; ++kk) {
-        uint32_t bits[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int k = (ks * KPW + kk) * 32 + g * 8 + e;
-          const float x = brow < B ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)brow * 1024 + k) : 0.0f;
-          bits[e] = brow < B ? bf16_bits_rne(prenorm_apply(a, x, inv, k)) : 0u;
-        }
-        hb[kk] = u32x4_t{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16), bits[4] | (bits[5] << 16),
-                         bits[6] | (bits[7] << 16)};
-      }
-    }
-  }
-
   // The two roles run separate loops with one barrier per iteration each
   // (my_tiles + 1 of them), so neither keeps the other's registers live.  The
   // barrier orders: W(i) stores before its fragment reads; partials of tile i-1
   // before the epilogue reads them; every read of a slot before it is rewritten.
+  // pass 2 of the RMSNorm prologue (GEMM waves), run once the first W tiles
+  // are in flight; its barrier pairs with the epilogue waves' first one
+  auto finish_prenorm = [&]() NVJSEL_INLINE {
+    if (!a.prenorm) return;
+    __syncthreads();  // the row sums are in LDS
+    // pass 2: normalise, round, pack this lane's fragments
+    const int brow = nb * 16 + r;
+    float tot = 0.0f;
+#pragma unroll
+    for (int s2 = 0; s2 < KSPLIT; ++s2) tot += pre_ss[s2][brow];
+    const float inv = prenorm_inv(a, tot);
+#pragma unroll
+    for (int kk = 0; kk < KPW; ++kk) {
+      uint32_t bits[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int k = (ks * KPW + kk) * 32 + g * 8 + e;
+        const float x = brow < B ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)brow * 1024 + k) : 0.0f;
+        bits[e] = brow < B ? bf16_bits_rne(prenorm_apply(a, x, inv, k)) : 0u;
+      }
+      hb[kk] = u32x4_t{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16), bits[4] | (bits[5] << 16),
+                       bits[6] | (bits[7] << 16)};
+    }
+  };
+
   if (gemm) {
     ring_pipeline<DEPTH>(my_tiles, [&](auto S, int j) NVJSEL_INLINE { load_tile(ring[decltype(S)::value], j); },
                          [&](auto S, int i) NVJSEL_INLINE {
@@ -844,9 +865,10 @@ __global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) 
         acc = mfma16x16x32<DT_BF16>(buf[q * 16 + (r ^ (q & 15))], hb[kk], acc);
       }
       part[i & 1][(ks * NB + nb) * 64 + lane] = acc;
-    });
+    }, finish_prenorm);
     __syncthreads();  // the epilogue waves' last iteration
   } else {
+    if (a.prenorm) __syncthreads();  // pairs with the GEMM waves' prologue barrier
     for (int i = 0; i <= my_tiles; ++i) {
       __syncthreads();
       if (i == 0) continue;
