@@ -84,6 +84,7 @@ struct SampleArgs {
   int32_t* row_state;              // [B]
   unsigned long long* chunk_max;   // [B, nchunks]
   uint32_t* cand_count;            // [B, nchunks]
+  float* cand_floor;               // [B, nchunks] logit floor of each chunk's candidates
   unsigned long long* cand;        // [B, nchunks, kCandCap]
   float* row_m;                    // [B]   max of x (top-p rows)
   unsigned long long* topp_hist;   // [B, kToppBins] zero at rest
@@ -442,7 +443,10 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   const uint32_t theta = prefix > 8u ? prefix - 8u : 0u;
   // keys below ord(-inf) = 0x007FFFFF are NaN patterns: clamp to -inf
   const float theta_v = theta > 0x007FFFFFu ? radix_value(theta) : -INFINITY;
-  if (threadIdx.x == 0) sh.cnt = 0;
+  if (threadIdx.x == 0) {
+    sh.cnt = 0;
+    a.cand_floor[(size_t)b * a.nchunks + c] = theta_v;
+  }
   __syncthreads();
   unsigned long long* out = a.cand + ((size_t)b * a.nchunks + c) * kCandCap;
 #pragma unroll
@@ -534,6 +538,60 @@ __device__ __forceinline__ unsigned long long topp_target(float p, unsigned long
   unsigned long long P = (unsigned long long)pz;
   if (Z > 0 && P > Z - 1) P = Z - 1;
   return P + 1;
+}
+
+// Loads the row's candidates into LDS, keeping only those at or above the
+// row's floor: every chunk's floor is at most that chunk's k-th largest
+// logit, which is at most the row's, so the largest floor bounds the row's
+// k-th largest from below and the row's top-k (ties included) all pass.  The
+// floor is compared in score space (x = l / T', monotone in l, so
+// l >= floor implies x >= fl(floor / T')).  off[c] are the chunks' exclusive
+// offsets, tot their sum.  Returns the number kept (may exceed cap: then the
+// list is incomplete and the caller takes its exact path).
+__device__ __forceinline__ int load_candidates(const SampleArgs& a, int b, const RowParams& rp, const uint32_t* off,
+                                               int tot, unsigned long long* dst, int cap, uint32_t* s_n,
+                                               unsigned long long* red) {
+  const int NC = a.nchunks;
+  unsigned long long fk = 0;
+  for (int c = threadIdx.x; c < NC; c += blockDim.x)
+    fk = max_u64(fk, ord_f32(a.cand_floor[(size_t)b * NC + c]));
+  fk = block_max_u64(fk, red);
+  const uint32_t kfloor = radix_key(unord_f32((uint32_t)fk) / rp.tp);
+  if (threadIdx.x == 0) *s_n = 0;
+  __syncthreads();
+  // wave w reads chunks w, w+4, ...: each chunk's list with 64-wide coalesced
+  // loads, all of a chunk's loads issued before any is used
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  // the wave's 64-entry pieces (chunk c, piece j), eight loads in flight at a time
+  constexpr int kBatch = 8;
+  int c = wave, j = 0;
+  while (c < NC) {
+    unsigned long long v[kBatch];
+    int rem[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      while (c < NC && j * 64 >= (int)(off[c + 1] - off[c])) { c += nw; j = 0; }  // wave-uniform
+      rem[q] = c < NC ? (int)(off[c + 1] - off[c]) - j * 64 : 0;
+      v[q] = lane < rem[q] ? a.cand[((size_t)b * NC + c) * kCandCap + j * 64 + lane] : 0ull;
+      ++j;
+    }
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      // wave-level compaction: one LDS atomic per piece
+      const bool keep = lane < rem[q] && (uint32_t)(v[q] >> 32) >= kfloor;
+      const unsigned long long mask = __ballot(keep);
+      if (mask == 0ull) continue;
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(s_n, (uint32_t)__popcll(mask));
+      base = (uint32_t)__shfl((int)base, 0, 64);
+      const uint32_t slot = base + (uint32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+      if (keep && slot < (uint32_t)cap) dst[slot] = v[q];
+    }
+  }
+  __syncthreads();
+  (void)tot;
+  return (int)*s_n;
 }
 
 // ------------------------------------------------------------------ top-k values and indices
@@ -668,20 +726,14 @@ __global__ void __launch_bounds__(kThreads) topk_select_kernel(SampleArgs a, flo
       if (c <= NC) s.off[c] = o;
       o += cnt[q];
     }
-    fast = !__syncthreads_or(bad) && tot <= (uint32_t)kSelCap;
-    n = (int)tot;
+    fast = !__syncthreads_or(bad);
+    if (fast) {
+      n = load_candidates(a, b, row_params(a, b), s.off, (int)tot, s.cand, kSelCap, &s.n, s.red);
+      fast = n <= kSelCap;
+    }
   }
   int m = K;  // entries of s.sel to sort
   if (fast) {
-    for (int e = threadIdx.x; e < n; e += blockDim.x) {
-      int lo = 0, hi = NC;
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if ((int)s.off[mid] <= e) lo = mid; else hi = mid;
-      }
-      s.cand[e] = a.cand[((size_t)b * NC + lo) * kCandCap + (e - (int)s.off[lo])];
-    }
-    __syncthreads();
     const uint32_t tk = lds_desc<false>(s.d, s.cand, n, (unsigned long long)K, 0.0f);
     if (threadIdx.x == 0) s.n = 0;
     __syncthreads();
@@ -840,7 +892,8 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
       o += cnt[q];
     }
     const int anybad = __syncthreads_or(bad);
-    fast = !anybad && tot <= (uint32_t)kSelCap;
+    fast = !anybad;
+    if (fast) fast = load_candidates(a, b, rp, s.off, (int)tot, s.cand, kSelCap, &s.n, s.red) <= kSelCap;
   }
   if (!fast) {
     const bool topp_only = rp.k == 0 && rp.p < 1.0f;
@@ -855,16 +908,7 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     }
     return;
   }
-  const int n = (int)s.off[NC];
-  for (int e = threadIdx.x; e < n; e += blockDim.x) {
-    int lo = 0, hi = NC;  // chunk c with off[c] <= e < off[c + 1]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if ((int)s.off[mid] <= e) lo = mid; else hi = mid;
-    }
-    s.cand[e] = a.cand[((size_t)b * NC + lo) * kCandCap + (e - (int)s.off[lo])];
-  }
-  __syncthreads();
+  const int n = (int)s.n;
   // exact top-k threshold
   const uint32_t tk = lds_desc<false>(s.d, s.cand, n, (unsigned long long)rp.k, 0.0f);
   if (threadIdx.x == 0) s.nk = 0;
@@ -1193,7 +1237,7 @@ __global__ void __launch_bounds__(kThreads) sample_gumbel_kernel(SampleArgs a) {
 }
 
 struct WsLayout {
-  size_t row_key, row_tau, row_state, chunk_max, cand_count, cand, row_m, topp_hist, topp_cand, topp_n;
+  size_t row_key, row_tau, row_state, chunk_max, cand_count, cand_floor, cand, row_m, topp_hist, topp_cand, topp_n;
   size_t list_n, list_gumbel, list_topp, row_done, row_items, total;
 };
 
@@ -1206,6 +1250,7 @@ static WsLayout ws_layout(int B, int V) {
   w.row_state = o;  o += align_up((size_t)B * 4, 256);
   w.chunk_max = o;  o += align_up((size_t)B * nc * 8, 256);
   w.cand_count = o; o += align_up((size_t)B * nc * 4, 256);
+  w.cand_floor = o; o += align_up((size_t)B * nc * 4, 256);
   w.cand = o;       o += align_up((size_t)B * nc * kCandCap * 8, 256);
   w.row_m = o;      o += align_up((size_t)B * 4, 256);
   w.topp_hist = o;  o += align_up((size_t)B * kToppBins * 8, 256);
@@ -1240,6 +1285,7 @@ static SampleArgs make_args(const void* logits, int dtype, int batch, int vocab,
   a.row_state = (int32_t*)(ws + w.row_state);
   a.chunk_max = (unsigned long long*)(ws + w.chunk_max);
   a.cand_count = (uint32_t*)(ws + w.cand_count);
+  a.cand_floor = (float*)(ws + w.cand_floor);
   a.cand = (unsigned long long*)(ws + w.cand);
   a.row_m = (float*)(ws + w.row_m);
   a.topp_hist = (unsigned long long*)(ws + w.topp_hist);
