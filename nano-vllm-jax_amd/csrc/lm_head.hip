@@ -270,9 +270,18 @@ template <int MODE, int N, typename Push>
 __device__ __forceinline__ void score_run(const float (&raw)[N], int v0, int V, int reduce_cast, bool greedy_row,
                                           bool unit_tp, float tp, const TfKey& key, float& amax,
                                           unsigned long long& best, Push&& push) {
+  // one branch per run, not per element: the cast and the bounds are uniform
   float val[N];
+  if (reduce_cast == 1) {
 #pragma unroll
-  for (int e = 0; e < N; ++e) val[e] = apply_cast(raw[e], reduce_cast);
+    for (int e = 0; e < N; ++e) val[e] = round_bf16(raw[e]);
+  } else if (reduce_cast == 2) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) val[e] = round_f16(raw[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; ++e) val[e] = raw[e];
+  }
   if (MODE == MODE_SAMPLE && !greedy_row) {
     float xv[N], ap[N];
     uint32_t bits[N];
@@ -296,17 +305,20 @@ __device__ __forceinline__ void score_run(const float (&raw)[N], int v0, int V, 
     // every draw feeds an unconditional select, so none is sunk into a branch
     const float am = amax;
     const float sam = fminf(fabsf(am), 1e30f);
-    bool q[N];
+    bool q[N], anyq = false;
 #pragma unroll
     for (int e = 0; e < N; ++e) {
       const bool ok = v0 + e < V;
       const float slack = 2e-4f + 4.8e-7f * (fminf(fabsf(ap[e]), 1e30f) + sam);
       q[e] = ok && !(ap[e] + slack < am);
+      anyq |= q[e];
       amax = fmaxf(amax, ok ? ap[e] : -INFINITY);
     }
+    if (anyq) {  // rare once the row's maximum is established
 #pragma unroll
-    for (int e = 0; e < N; ++e)
-      if (q[e]) push(xv[e], v0 + e);
+      for (int e = 0; e < N; ++e)
+        if (q[e]) push(xv[e], v0 + e);
+    }
   } else {
 #pragma unroll
     for (int e = 0; e < N; ++e)
