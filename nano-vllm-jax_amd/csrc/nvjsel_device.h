@@ -68,11 +68,28 @@ __device__ __forceinline__ void threefry2x32(const TfKey& k, uint32_t c0, uint32
       : "+v"(x0[0]), "+v"(x0[1]), "+v"(x0[2]), "+v"(x0[3]), "+v"(x1[0]), "+v"(x1[1]), \
         "+v"(x1[2]), "+v"(x1[3])                                                        \
       : "n"(32 - (r)))
+// The 20 rounds and 5 key injections of four Threefry-2x32 chains in one asm
+// block (interleaved chain by chain; one block so the compiler adds no hazard
+// padding between rounds).  Vector instructions only.
+__device__ __forceinline__ void threefry4_rounds(uint32_t (&x0)[4], uint32_t (&x1)[4], uint32_t k0, uint32_t k1,
+                                                 uint32_t k2) {
+  asm volatile(
+      "v_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 19\n\tv_alignbit_b32 %5, %5, %5, 19\n\tv_alignbit_b32 %6, %6, %6, 19\n\tv_alignbit_b32 %7, %7, %7, 19\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 17\n\tv_alignbit_b32 %5, %5, %5, 17\n\tv_alignbit_b32 %6, %6, %6, 17\n\tv_alignbit_b32 %7, %7, %7, 17\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 6\n\tv_alignbit_b32 %5, %5, %5, 6\n\tv_alignbit_b32 %6, %6, %6, 6\n\tv_alignbit_b32 %7, %7, %7, 6\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 26\n\tv_alignbit_b32 %5, %5, %5, 26\n\tv_alignbit_b32 %6, %6, %6, 26\n\tv_alignbit_b32 %7, %7, %7, 26\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %9\n\tv_add_u32 %1, %1, %9\n\tv_add_u32 %2, %2, %9\n\tv_add_u32 %3, %3, %9\n\tv_add3_u32 %4, %4, %10, 1\n\tv_add3_u32 %5, %5, %10, 1\n\tv_add3_u32 %6, %6, %10, 1\n\tv_add3_u32 %7, %7, %10, 1\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 15\n\tv_alignbit_b32 %5, %5, %5, 15\n\tv_alignbit_b32 %6, %6, %6, 15\n\tv_alignbit_b32 %7, %7, %7, 15\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 3\n\tv_alignbit_b32 %5, %5, %5, 3\n\tv_alignbit_b32 %6, %6, %6, 3\n\tv_alignbit_b32 %7, %7, %7, 3\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 16\n\tv_alignbit_b32 %5, %5, %5, 16\n\tv_alignbit_b32 %6, %6, %6, 16\n\tv_alignbit_b32 %7, %7, %7, 16\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 8\n\tv_alignbit_b32 %5, %5, %5, 8\n\tv_alignbit_b32 %6, %6, %6, 8\n\tv_alignbit_b32 %7, %7, %7, 8\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %10\n\tv_add_u32 %1, %1, %10\n\tv_add_u32 %2, %2, %10\n\tv_add_u32 %3, %3, %10\n\tv_add3_u32 %4, %4, %8, 2\n\tv_add3_u32 %5, %5, %8, 2\n\tv_add3_u32 %6, %6, %8, 2\n\tv_add3_u32 %7, %7, %8, 2\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 19\n\tv_alignbit_b32 %5, %5, %5, 19\n\tv_alignbit_b32 %6, %6, %6, 19\n\tv_alignbit_b32 %7, %7, %7, 19\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 17\n\tv_alignbit_b32 %5, %5, %5, 17\n\tv_alignbit_b32 %6, %6, %6, 17\n\tv_alignbit_b32 %7, %7, %7, 17\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 6\n\tv_alignbit_b32 %5, %5, %5, 6\n\tv_alignbit_b32 %6, %6, %6, 6\n\tv_alignbit_b32 %7, %7, %7, 6\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 26\n\tv_alignbit_b32 %5, %5, %5, 26\n\tv_alignbit_b32 %6, %6, %6, 26\n\tv_alignbit_b32 %7, %7, %7, 26\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %8\n\tv_add_u32 %1, %1, %8\n\tv_add_u32 %2, %2, %8\n\tv_add_u32 %3, %3, %8\n\tv_add3_u32 %4, %4, %9, 3\n\tv_add3_u32 %5, %5, %9, 3\n\tv_add3_u32 %6, %6, %9, 3\n\tv_add3_u32 %7, %7, %9, 3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 15\n\tv_alignbit_b32 %5, %5, %5, 15\n\tv_alignbit_b32 %6, %6, %6, 15\n\tv_alignbit_b32 %7, %7, %7, 15\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 3\n\tv_alignbit_b32 %5, %5, %5, 3\n\tv_alignbit_b32 %6, %6, %6, 3\n\tv_alignbit_b32 %7, %7, %7, 3\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 16\n\tv_alignbit_b32 %5, %5, %5, 16\n\tv_alignbit_b32 %6, %6, %6, 16\n\tv_alignbit_b32 %7, %7, %7, 16\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 8\n\tv_alignbit_b32 %5, %5, %5, 8\n\tv_alignbit_b32 %6, %6, %6, 8\n\tv_alignbit_b32 %7, %7, %7, 8\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %9\n\tv_add_u32 %1, %1, %9\n\tv_add_u32 %2, %2, %9\n\tv_add_u32 %3, %3, %9\n\tv_add3_u32 %4, %4, %10, 4\n\tv_add3_u32 %5, %5, %10, 4\n\tv_add3_u32 %6, %6, %10, 4\n\tv_add3_u32 %7, %7, %10, 4\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 19\n\tv_alignbit_b32 %5, %5, %5, 19\n\tv_alignbit_b32 %6, %6, %6, 19\n\tv_alignbit_b32 %7, %7, %7, 19\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 17\n\tv_alignbit_b32 %5, %5, %5, 17\n\tv_alignbit_b32 %6, %6, %6, 17\n\tv_alignbit_b32 %7, %7, %7, 17\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 6\n\tv_alignbit_b32 %5, %5, %5, 6\n\tv_alignbit_b32 %6, %6, %6, 6\n\tv_alignbit_b32 %7, %7, %7, 6\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 26\n\tv_alignbit_b32 %5, %5, %5, 26\n\tv_alignbit_b32 %6, %6, %6, 26\n\tv_alignbit_b32 %7, %7, %7, 26\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %10\n\tv_add_u32 %1, %1, %10\n\tv_add_u32 %2, %2, %10\n\tv_add_u32 %3, %3, %10\n\tv_add3_u32 %4, %4, %8, 5\n\tv_add3_u32 %5, %5, %8, 5\n\tv_add3_u32 %6, %6, %8, 5\n\tv_add3_u32 %7, %7, %8, 5"
+      : "+v"(x0[0]), "+v"(x0[1]), "+v"(x0[2]), "+v"(x0[3]), "+v"(x1[0]), "+v"(x1[1]), "+v"(x1[2]), "+v"(x1[3]),
+        "+v"(k0), "+v"(k1), "+v"(k2));  // in-out: the key words never share a register with x0 (== k0 on entry)
+}
+
 template <int N>
 __device__ __forceinline__ void random_bits32_n(const TfKey& k, const uint32_t (&idx)[N], uint32_t (&out)[N]) {
   uint32_t x0[N], x1[N];
 #pragma unroll
   for (int e = 0; e < N; ++e) { x0[e] = k.k0; x1[e] = idx[e] + k.k1; }
+  if constexpr (N == 4) {
+    threefry4_rounds(x0, x1, k.k0, k.k1, k.k2);
+#pragma unroll
+    for (int e = 0; e < N; ++e) out[e] = x0[e] ^ x1[e];
+    return;
+  }
 #define NVJSEL_TF_ROUND_N(r)                                                                      \
   if constexpr (N == 4) {                                                                         \
     NVJSEL_TF4_ROUND(r);                                                                          \
