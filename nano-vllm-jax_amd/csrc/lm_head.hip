@@ -719,9 +719,12 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
 // One barrier per tile orders both rings, so a tile costs max(GEMM, epilogue)
 // rather than their sum, and the epilogue's VALU work (Threefry + logs) runs
 // beside the GEMM waves' LDS, MFMA and memory waits on the same SIMDs.
-template <int NB, int GW, int MODE, int DEPTH>
-__global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) {
-  constexpr int NT = (GW + NB) * 64;
+template <int NB, int GW, int MODE, int DEPTH, int EPM>
+__global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmArgs a) {
+  constexpr int EW = NB * EPM;     // epilogue waves
+  constexpr int EPL = 4 / EPM;     // vocabulary rows per epilogue lane per tile
+  static_assert(EPM == 1 || EPM == 2, "one or two epilogue waves per batch tile");
+  constexpr int NT = (GW + EW) * 64;
   constexpr int NTG = GW * 64;
   constexpr int KSPLIT = GW / NB;
   static_assert(KSPLIT >= 1 && GW % NB == 0, "GEMM waves split k evenly");
@@ -734,11 +737,11 @@ __global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) 
   constexpr int QCAP = 64 * 4 + 64;
   __shared__ u32x4_t wt[2][16 * 128];
   __shared__ f32x4_t part[2][KSPLIT * NB * 64];
-  __shared__ float qx[MODE == MODE_SAMPLE ? NB : 1][QCAP];
-  __shared__ uint32_t qv[MODE == MODE_SAMPLE ? NB : 1][QCAP];
-  __shared__ uint32_t qn[NB];
-  __shared__ unsigned long long qbest[MODE == MODE_SAMPLE ? NB : 1][64];
-  __shared__ unsigned long long red[NB * 64];
+  __shared__ float qx[MODE == MODE_SAMPLE ? EW : 1][QCAP];
+  __shared__ uint32_t qv[MODE == MODE_SAMPLE ? EW : 1][QCAP];
+  __shared__ uint32_t qn[EW];
+  __shared__ unsigned long long qbest[MODE == MODE_SAMPLE ? EW : 1][64];
+  __shared__ unsigned long long red[EW * 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool gemm = wave < GW;
   const int B = a.B, V = a.V;
@@ -755,7 +758,7 @@ __global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) 
   // ---- epilogue-wave state
   const int ew = wave - GW;                      // epilogue wave index
   const int el = (ew < 0 ? 0 : ew) * 64 + lane;  // epilogue lane id
-  const int erow = el % ROWS, evq = el / ROWS;   // batch row, vocab quad
+  const int erow = el % ROWS, evq = el / ROWS;   // batch row, vocab run (EPL rows)
   float tp = 1.0f;
   bool greedy_row = true, unit_tp = true;
   TfKey key = tf_key(0u, 0u);
@@ -884,8 +887,10 @@ __global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) 
     for (int i = 0; i <= my_tiles; ++i) {
       __syncthreads();
       if (i == 0) continue;
-      // tile i-1: sum the k-split partials of (row erow, vocab rows 4 evq + e)
-      const int pnb = erow >> 4, pl = evq * 16 + (erow & 15);
+      // tile i-1: sum the k-split partials of (row erow, vocab rows EPL evq + e);
+      // GEMM lane (g, r) holds vocab rows 4 g .. 4 g + 3 of batch row r
+      const int vr = EPL * evq;
+      const int pnb = erow >> 4, pl = (vr >> 2) * 16 + (erow & 15), c0 = vr & 3;
       f32x4_t s = part[(i - 1) & 1][pnb * 64 + pl];
 #pragma unroll
       for (int s2 = 1; s2 < KSPLIT; ++s2) {
@@ -893,7 +898,7 @@ __global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) 
 #pragma unroll
         for (int e = 0; e < 4; ++e) s[e] += p[e];
       }
-      const int v0 = (blockIdx.x + (i - 1) * grid) * 16 + 4 * evq;
+      const int v0 = (blockIdx.x + (i - 1) * grid) * 16 + vr;
       if constexpr (MODE == MODE_SAMPLE) {
         if constexpr (ROWS < 64) {
           // lanes holding the same batch row share their approximate maximum
@@ -903,8 +908,10 @@ __global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) 
         if (qn[ew] >= 64u) flush();  // full waves of exact work; room for this tile
       }
       if (erow < B) {
-        const float raw[4] = {s[0], s[1], s[2], s[3]};
-        score_run<MODE, 4>(raw, v0, V, a.reduce_cast, greedy_row, unit_tp, tp, key, amax, best,
+        float raw[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) raw[e] = EPL == 4 ? s[e] : (c0 == 0 ? s[e] : s[e + 2]);
+        score_run<MODE, EPL>(raw, v0, V, a.reduce_cast, greedy_row, unit_tp, tp, key, amax, best,
                            [&](float x, int v) {
                              const uint32_t slot = atomicAdd(&qn[ew], 1u);
                              qx[ew][slot] = x;
@@ -924,7 +931,7 @@ __global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) 
   for (int b = tid; b < B && b < ROWS; b += NT) {
     unsigned long long m = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) m = max_u64(m, red[q * ROWS + b]);
+    for (int q = 0; q < 4 * EPM; ++q) m = max_u64(m, red[q * ROWS + b]);
     if (m) (void)after(atomicMax(&a.row_keys[b], m));
   }
   finish_rows(a.row_keys, a.counter, B, a.out_ids, a.out_best);
@@ -948,11 +955,14 @@ __global__ void __launch_bounds__((GW + NB) * 64) lm_head_tile_kernel(LmArgs a) 
 
 template <int NB, int GW, int MODE>
 static int launch_tile(const LmArgs& a, hipStream_t stream) {
-  auto kern = lm_head_tile_kernel<NB, GW, MODE, NVJSEL_TILE_DEPTH>;
+  // a second epilogue wave per batch tile pays off where the register budget
+  // allows it (measured, sample mode: B=32 91 -> 81 us; B=64 would spill)
+  constexpr int EPM = (MODE == MODE_SAMPLE && NB == 2) ? 2 : 1;
+  auto kern = lm_head_tile_kernel<NB, GW, MODE, NVJSEL_TILE_DEPTH, EPM>;
   int grid = NVJSEL_TILE_BPC * device_cu_count();
   const int ntiles = (a.V + 15) / 16;
   if (grid > ntiles) grid = ntiles;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3((GW + NB) * 64), 0, stream, a);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3((GW + NB * EPM) * 64), 0, stream, a);
   NVJSEL_CHECK_LAUNCH("lm_head_tile_kernel");
   return NVJSEL_OK;
 }

@@ -142,7 +142,7 @@ def test_streaming_gemv_shapes(H, batch):
     check_greedy(ids.cpu().numpy(), z, 1, f"gemv H={H} B={batch}")
 
 
-@pytest.mark.parametrize("batch", [1, 2, 5, 16, 33, 64, 70])
+@pytest.mark.parametrize("batch", [1, 2, 5, 16, 20, 32, 33, 64, 70])
 def test_fused_lm_head_sample(batch):
     """nvjsel_lm_head_sample vs the oracle: greedy rows, temperature rows (JAX keys)."""
     from tests.gpu_helpers import check_fused_sampled, engine_keys, keys_tensor

@@ -53,7 +53,7 @@ def test_prenorm_greedy(batch, H, hidden_dtype, act_dtype):
                  f"prenorm B={batch} H={H} {hidden_dtype}->{act_dtype}")
 
 
-@pytest.mark.parametrize("batch,act_dtype", [(1, "bf16"), (2, "f32"), (16, "bf16"), (64, "bf16"), (9, "f32")])
+@pytest.mark.parametrize("batch,act_dtype", [(1, "bf16"), (2, "f32"), (16, "bf16"), (24, "bf16"), (64, "bf16"), (9, "f32")])
 def test_prenorm_fused_sample(batch, act_dtype):
     rng = np.random.default_rng(300 + batch)
     H, V = 1024, 8191
