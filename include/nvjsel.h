@@ -182,7 +182,9 @@ int nvjsel_sample(const void* logits, int dtype, int batch, int vocab, int64_t r
  * values, by index ascending; NaN orders above every number (the first NaN
  * first) and -0.0 equals +0.0, the argmax conventions of this library.
  * out_indices[b, 0] is the greedy token.  1 <= k <= min(256, vocab).
- * Workspace: nvjsel_topk_workspace_size(batch, vocab) bytes of scratch.
+ * Workspace: nvjsel_topk_workspace_size(batch, vocab) bytes of scratch; any
+ * contents on entry.  It writes none of the zero-at-rest accumulators of
+ * nvjsel_sample, so a sampler workspace at least this large can be shared.
  */
 size_t nvjsel_topk_workspace_size(int batch, int vocab);
 

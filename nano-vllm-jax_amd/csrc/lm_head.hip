@@ -57,16 +57,6 @@
 #ifndef NVJSEL_GEMV_WAVES
 #define NVJSEL_GEMV_WAVES 4  // waves per block of the streaming GEMV
 #endif
-#ifndef NVJSEL_GEMV_CONTIG
-#define NVJSEL_GEMV_CONTIG 0  // 0 grid-stride groups, 1 slice per wave, 2 per block, 3 rotated slice
-#endif
-#ifndef NVJSEL_GEMV_GRID_NUM
-#define NVJSEL_GEMV_GRID_NUM 1  // grid = CUs * blocks-per-CU * NUM / DEN
-#define NVJSEL_GEMV_GRID_DEN 1
-#endif
-#ifndef NVJSEL_GEMV_NOCOMPUTE
-#define NVJSEL_GEMV_NOCOMPUTE 0
-#endif
 #ifndef NVJSEL_GEMV_DEPTH
 #define NVJSEL_GEMV_DEPTH 4  // row groups in flight per wave
 #endif
@@ -561,21 +551,9 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
   const int ngroups = (V + R - 1) / R;
   const int nwaves = gridDim.x * WAVES;
   const int gw = blockIdx.x * WAVES + wave;
-#if NVJSEL_GEMV_CONTIG == 1 || NVJSEL_GEMV_CONTIG == 3
-  // each wave streams one contiguous slice of the vocabulary
-  const int per = (ngroups + nwaves - 1) / nwaves;
-  const int g_begin = gw * per;
-  const int g_end = min(g_begin + per, ngroups);
-  const int g_step = 1;
-#elif NVJSEL_GEMV_CONTIG == 2
-  // each block streams one contiguous slice; its waves take adjacent groups
-  const int per = (ngroups + gridDim.x - 1) / gridDim.x;
-  const int g_begin = blockIdx.x * per + wave;
-  const int g_end = min(blockIdx.x * per + per, ngroups);
-  const int g_step = WAVES;
-#else
+  // round-robin groups: wave gw takes gw, gw + nwaves, ...  (measured faster
+  // than contiguous slices per wave or per block)
   const int g_begin = gw, g_end = ngroups, g_step = nwaves;
-#endif
 
   auto load_grp = [&](u32x4_t(&w)[R][KJ], int grp) NVJSEL_INLINE {
     const int v0 = grp * R;
@@ -592,16 +570,6 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
 
   auto proc_grp = [&](const u32x4_t(&w)[R][KJ], int grp) NVJSEL_INLINE {
     const int v0 = grp * R;
-#if NVJSEL_GEMV_NOCOMPUTE
-    // timing probe only: consume the loads without the dot products
-    uint32_t xx = 0;
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int j = 0; j < KJ; ++j) xx ^= w[r][j].x ^ w[r][j].y ^ w[r][j].z ^ w[r][j].w;
-    best[0] = max_u64(best[0], (unsigned long long)(xx & 1u) << 32 | (uint32_t)~v0);
-    return;
-#endif
     float p[NB][R];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
@@ -660,14 +628,7 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
   // ring of DEPTH * R * KJ 16-byte loads per lane
   constexpr int DEPTH = MODE == MODE_SAMPLE ? (KJ >= 4 ? 2 : 3) : NVJSEL_GEMV_DEPTH;
   const int n_mine = g_end > g_begin ? (g_end - g_begin + g_step - 1) / g_step : 0;
-#if NVJSEL_GEMV_CONTIG == 3
-  // waves advance in lockstep; starting each slice at a different point keeps
-  // simultaneous requests from landing on the same memory channels
-  const int rot = n_mine > 0 ? (gw * 7) % n_mine : 0;
-#else
-  const int rot = 0;
-#endif
-  auto gid = [&](int i) { int k = i + rot; k = k >= n_mine ? k - n_mine : k; return g_begin + k * g_step; };
+  auto gid = [&](int i) { return g_begin + i * g_step; };
   u32x4_t ring[DEPTH][R][KJ];
   if constexpr (MODE == MODE_SAMPLE) {
     ring_pipeline<DEPTH>(
@@ -1092,7 +1053,7 @@ static int launch_gemv(const LmArgs& a, hipStream_t stream) {
   if (per_cu < 1) per_cu = 1;
   if (NVJSEL_GEMV_BPC > 0 && per_cu > NVJSEL_GEMV_BPC) per_cu = NVJSEL_GEMV_BPC;
   const int need = (a.V + R * WAVES - 1) / (R * WAVES);
-  int grid = per_cu * device_cu_count() * NVJSEL_GEMV_GRID_NUM / NVJSEL_GEMV_GRID_DEN;
+  int grid = per_cu * device_cu_count();
   if (grid < 1) grid = 1;
   if (grid > need) grid = need;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(WAVES * 64), 0, stream, a);

@@ -51,33 +51,43 @@ __device__ __forceinline__ void threefry2x32(const TfKey& k, uint32_t c0, uint32
 #undef NVJSEL_TF_ROUND
 
 // random_bits32 at the N indices idx[], written round by round across the N
-// counters so the independent chains interleave (one
-// chain alone is a serial dependence of ~80 VALU operations).
-// For N == 4 each round is one asm block that issues the four chains'
-// add / rotate / xor interleaved (the compiler's scheduler otherwise emits the
-// chains one after another to save registers, and a lone dependent chain
-// issues at a fraction of the VALU rate).  Only vector instructions.
-#define NVJSEL_TF4_ROUND(r)                                                             \
-  asm volatile(                                                                         \
-      "v_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\t"                                \
-      "v_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\t"                                \
-      "v_alignbit_b32 %4, %4, %4, %8\n\tv_alignbit_b32 %5, %5, %5, %8\n\t"              \
-      "v_alignbit_b32 %6, %6, %6, %8\n\tv_alignbit_b32 %7, %7, %7, %8\n\t"              \
-      "v_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\t"                                \
-      "v_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3"                                     \
-      : "+v"(x0[0]), "+v"(x0[1]), "+v"(x0[2]), "+v"(x0[3]), "+v"(x1[0]), "+v"(x1[1]), \
-        "+v"(x1[2]), "+v"(x1[3])                                                        \
-      : "n"(32 - (r)))
-// The 20 rounds and 5 key injections of four Threefry-2x32 chains in one asm
-// block (interleaved chain by chain; one block so the compiler adds no hazard
-// padding between rounds).  Vector instructions only.
+// counters so the independent chains interleave (one chain alone is a serial
+// dependence of ~80 VALU operations).  N == 4 runs as a single asm block:
+// the compiler's scheduler otherwise emits the chains one after another to
+// save registers, and pads every separate asm block with a wait state.
+// Only vector instructions.  Rotations are written as right-rotations by
+// 32 - r (v_alignbit_b32 x, x, x, s == rotr(x, s)).
+#define NVJSEL_TF4_ROUND(s)                                                              \
+  "v_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\t"            \
+  "v_add_u32 %3, %3, %7\n\t"                                                            \
+  "v_alignbit_b32 %4, %4, %4, " #s "\n\tv_alignbit_b32 %5, %5, %5, " #s "\n\t"         \
+  "v_alignbit_b32 %6, %6, %6, " #s "\n\tv_alignbit_b32 %7, %7, %7, " #s "\n\t"         \
+  "v_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\t"            \
+  "v_xor_b32 %7, %7, %3\n\t"
+// key injection: x0 += ka; x1 += kb + c   (operands %8, %9, %10 = k0, k1, k2)
+#define NVJSEL_TF4_INJECT(ka, kb, c)                                                     \
+  "v_add_u32 %0, %0, " ka "\n\tv_add_u32 %1, %1, " ka "\n\tv_add_u32 %2, %2, " ka        \
+  "\n\tv_add_u32 %3, %3, " ka "\n\t"                                                     \
+  "v_add3_u32 %4, %4, " kb ", " #c "\n\tv_add3_u32 %5, %5, " kb ", " #c "\n\t"           \
+  "v_add3_u32 %6, %6, " kb ", " #c "\n\tv_add3_u32 %7, %7, " kb ", " #c "\n\t"
+// rotations {13, 15, 26, 6} and {17, 29, 16, 24} as right-rotations
+#define NVJSEL_TF4_ROUNDS_A NVJSEL_TF4_ROUND(19) NVJSEL_TF4_ROUND(17) NVJSEL_TF4_ROUND(6) NVJSEL_TF4_ROUND(26)
+#define NVJSEL_TF4_ROUNDS_B NVJSEL_TF4_ROUND(15) NVJSEL_TF4_ROUND(3) NVJSEL_TF4_ROUND(16) NVJSEL_TF4_ROUND(8)
+
 __device__ __forceinline__ void threefry4_rounds(uint32_t (&x0)[4], uint32_t (&x1)[4], uint32_t k0, uint32_t k1,
                                                  uint32_t k2) {
-  asm volatile(
-      "v_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 19\n\tv_alignbit_b32 %5, %5, %5, 19\n\tv_alignbit_b32 %6, %6, %6, 19\n\tv_alignbit_b32 %7, %7, %7, 19\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 17\n\tv_alignbit_b32 %5, %5, %5, 17\n\tv_alignbit_b32 %6, %6, %6, 17\n\tv_alignbit_b32 %7, %7, %7, 17\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 6\n\tv_alignbit_b32 %5, %5, %5, 6\n\tv_alignbit_b32 %6, %6, %6, 6\n\tv_alignbit_b32 %7, %7, %7, 6\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 26\n\tv_alignbit_b32 %5, %5, %5, 26\n\tv_alignbit_b32 %6, %6, %6, 26\n\tv_alignbit_b32 %7, %7, %7, 26\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %9\n\tv_add_u32 %1, %1, %9\n\tv_add_u32 %2, %2, %9\n\tv_add_u32 %3, %3, %9\n\tv_add3_u32 %4, %4, %10, 1\n\tv_add3_u32 %5, %5, %10, 1\n\tv_add3_u32 %6, %6, %10, 1\n\tv_add3_u32 %7, %7, %10, 1\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 15\n\tv_alignbit_b32 %5, %5, %5, 15\n\tv_alignbit_b32 %6, %6, %6, 15\n\tv_alignbit_b32 %7, %7, %7, 15\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 3\n\tv_alignbit_b32 %5, %5, %5, 3\n\tv_alignbit_b32 %6, %6, %6, 3\n\tv_alignbit_b32 %7, %7, %7, 3\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 16\n\tv_alignbit_b32 %5, %5, %5, 16\n\tv_alignbit_b32 %6, %6, %6, 16\n\tv_alignbit_b32 %7, %7, %7, 16\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 8\n\tv_alignbit_b32 %5, %5, %5, 8\n\tv_alignbit_b32 %6, %6, %6, 8\n\tv_alignbit_b32 %7, %7, %7, 8\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %10\n\tv_add_u32 %1, %1, %10\n\tv_add_u32 %2, %2, %10\n\tv_add_u32 %3, %3, %10\n\tv_add3_u32 %4, %4, %8, 2\n\tv_add3_u32 %5, %5, %8, 2\n\tv_add3_u32 %6, %6, %8, 2\n\tv_add3_u32 %7, %7, %8, 2\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 19\n\tv_alignbit_b32 %5, %5, %5, 19\n\tv_alignbit_b32 %6, %6, %6, 19\n\tv_alignbit_b32 %7, %7, %7, 19\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 17\n\tv_alignbit_b32 %5, %5, %5, 17\n\tv_alignbit_b32 %6, %6, %6, 17\n\tv_alignbit_b32 %7, %7, %7, 17\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 6\n\tv_alignbit_b32 %5, %5, %5, 6\n\tv_alignbit_b32 %6, %6, %6, 6\n\tv_alignbit_b32 %7, %7, %7, 6\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 26\n\tv_alignbit_b32 %5, %5, %5, 26\n\tv_alignbit_b32 %6, %6, %6, 26\n\tv_alignbit_b32 %7, %7, %7, 26\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %8\n\tv_add_u32 %1, %1, %8\n\tv_add_u32 %2, %2, %8\n\tv_add_u32 %3, %3, %8\n\tv_add3_u32 %4, %4, %9, 3\n\tv_add3_u32 %5, %5, %9, 3\n\tv_add3_u32 %6, %6, %9, 3\n\tv_add3_u32 %7, %7, %9, 3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 15\n\tv_alignbit_b32 %5, %5, %5, 15\n\tv_alignbit_b32 %6, %6, %6, 15\n\tv_alignbit_b32 %7, %7, %7, 15\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 3\n\tv_alignbit_b32 %5, %5, %5, 3\n\tv_alignbit_b32 %6, %6, %6, 3\n\tv_alignbit_b32 %7, %7, %7, 3\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 16\n\tv_alignbit_b32 %5, %5, %5, 16\n\tv_alignbit_b32 %6, %6, %6, 16\n\tv_alignbit_b32 %7, %7, %7, 16\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 8\n\tv_alignbit_b32 %5, %5, %5, 8\n\tv_alignbit_b32 %6, %6, %6, 8\n\tv_alignbit_b32 %7, %7, %7, 8\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %9\n\tv_add_u32 %1, %1, %9\n\tv_add_u32 %2, %2, %9\n\tv_add_u32 %3, %3, %9\n\tv_add3_u32 %4, %4, %10, 4\n\tv_add3_u32 %5, %5, %10, 4\n\tv_add3_u32 %6, %6, %10, 4\n\tv_add3_u32 %7, %7, %10, 4\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 19\n\tv_alignbit_b32 %5, %5, %5, 19\n\tv_alignbit_b32 %6, %6, %6, 19\n\tv_alignbit_b32 %7, %7, %7, 19\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 17\n\tv_alignbit_b32 %5, %5, %5, 17\n\tv_alignbit_b32 %6, %6, %6, 17\n\tv_alignbit_b32 %7, %7, %7, 17\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 6\n\tv_alignbit_b32 %5, %5, %5, 6\n\tv_alignbit_b32 %6, %6, %6, 6\n\tv_alignbit_b32 %7, %7, %7, 6\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\tv_add_u32 %3, %3, %7\n\tv_alignbit_b32 %4, %4, %4, 26\n\tv_alignbit_b32 %5, %5, %5, 26\n\tv_alignbit_b32 %6, %6, %6, 26\n\tv_alignbit_b32 %7, %7, %7, 26\n\tv_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\tv_xor_b32 %7, %7, %3\n\tv_add_u32 %0, %0, %10\n\tv_add_u32 %1, %1, %10\n\tv_add_u32 %2, %2, %10\n\tv_add_u32 %3, %3, %10\n\tv_add3_u32 %4, %4, %8, 5\n\tv_add3_u32 %5, %5, %8, 5\n\tv_add3_u32 %6, %6, %8, 5\n\tv_add3_u32 %7, %7, %8, 5"
-      : "+v"(x0[0]), "+v"(x0[1]), "+v"(x0[2]), "+v"(x0[3]), "+v"(x1[0]), "+v"(x1[1]), "+v"(x1[2]), "+v"(x1[3]),
-        "+v"(k0), "+v"(k1), "+v"(k2));  // in-out: the key words never share a register with x0 (== k0 on entry)
+  asm volatile(NVJSEL_TF4_ROUNDS_A NVJSEL_TF4_INJECT("%9", "%10", 1)
+               NVJSEL_TF4_ROUNDS_B NVJSEL_TF4_INJECT("%10", "%8", 2)
+               NVJSEL_TF4_ROUNDS_A NVJSEL_TF4_INJECT("%8", "%9", 3)
+               NVJSEL_TF4_ROUNDS_B NVJSEL_TF4_INJECT("%9", "%10", 4)
+               NVJSEL_TF4_ROUNDS_A NVJSEL_TF4_INJECT("%10", "%8", 5)
+               : "+v"(x0[0]), "+v"(x0[1]), "+v"(x0[2]), "+v"(x0[3]), "+v"(x1[0]), "+v"(x1[1]), "+v"(x1[2]),
+                 "+v"(x1[3]), "+v"(k0), "+v"(k1), "+v"(k2));  // in-out: no key word shares x0's register
 }
+#undef NVJSEL_TF4_ROUNDS_A
+#undef NVJSEL_TF4_ROUNDS_B
+#undef NVJSEL_TF4_INJECT
+#undef NVJSEL_TF4_ROUND
 
 template <int N>
 __device__ __forceinline__ void random_bits32_n(const TfKey& k, const uint32_t (&idx)[N], uint32_t (&out)[N]) {
@@ -90,12 +100,8 @@ __device__ __forceinline__ void random_bits32_n(const TfKey& k, const uint32_t (
     for (int e = 0; e < N; ++e) out[e] = x0[e] ^ x1[e];
     return;
   }
-#define NVJSEL_TF_ROUND_N(r)                                                                      \
-  if constexpr (N == 4) {                                                                         \
-    NVJSEL_TF4_ROUND(r);                                                                          \
-  } else {                                                                                        \
-    _Pragma("unroll") for (int e = 0; e < N; ++e) { x0[e] += x1[e]; x1[e] = rotl32(x1[e], r); x1[e] ^= x0[e]; } \
-  }
+#define NVJSEL_TF_ROUND_N(r) \
+  _Pragma("unroll") for (int e = 0; e < N; ++e) { x0[e] += x1[e]; x1[e] = rotl32(x1[e], r); x1[e] ^= x0[e]; }
 #define NVJSEL_TF_INJECT_N(a, b, c) \
   _Pragma("unroll") for (int e = 0; e < N; ++e) { x0[e] += (a); x1[e] += (b) + (uint32_t)(c); }
   NVJSEL_TF_ROUND_N(13) NVJSEL_TF_ROUND_N(15) NVJSEL_TF_ROUND_N(26) NVJSEL_TF_ROUND_N(6)
@@ -109,7 +115,6 @@ __device__ __forceinline__ void random_bits32_n(const TfKey& k, const uint32_t (
   NVJSEL_TF_ROUND_N(13) NVJSEL_TF_ROUND_N(15) NVJSEL_TF_ROUND_N(26) NVJSEL_TF_ROUND_N(6)
   NVJSEL_TF_INJECT_N(k.k2, k.k0, 5)
 #undef NVJSEL_TF_ROUND_N
-#undef NVJSEL_TF4_ROUND
 #undef NVJSEL_TF_INJECT_N
 #pragma unroll
   for (int e = 0; e < N; ++e) out[e] = x0[e] ^ x1[e];
