@@ -377,88 +377,251 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* ws, T& total) {
 }
 
 // ------------------------------------------------------------------ 1. scan
+// One block per (chunk, row); thread t holds Q = EPT / VEC vectors of VEC
+// elements (elem_index).  Work per element is kept to a few VALU operations
+// (the pass runs at the HBM rate only if the block's arithmetic stays well
+// under its load time): a max3 tree per vector and an unordered compare per
+// pair for NaN detection; the first index of the maximum is found per wave
+// with one ballot per vector slot.
 struct ScanShared {
-  GumbelShared g;
-  uint32_t hist[256];
-  uint32_t wsum[kThreads / 64];
-  uint32_t sel, rem, cnt;
+  unsigned long long wkey[kThreads / 64];
+  uint32_t wfloor[kThreads / 64];
+  uint32_t cnt;
 };
+
+typedef short nvjsel_s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short nvjsel_u16x2 __attribute__((ext_vector_type(2)));
+
+// A thread's EPT raw elements as Q vectors, with each vector's maximum.  The
+// maximum of sign-magnitude floats is taken on their bit patterns: the signed
+// integer maximum is right whenever the vector holds a value with the sign bit
+// clear, the unsigned minimum when every value is negative (-0 included); a
+// NaN shows as a signed maximum above +inf or an unsigned maximum above -inf.
+// Three integer max/min per element word (packed 16-bit for bf16/f16, 3-input
+// for f32) instead of decoding every element.
+template <int DT, int VEC>
+struct ChunkRegs {
+  static constexpr int Q = kEPT / VEC;
+  static constexpr int W = VEC == 1 ? 1 : 4;  // dwords per vector
+  uint32_t w[Q][W];
+  float vmax[Q];  // max of each vector (NaN ignored)
+  bool vnan[Q];   // the vector holds a NaN
+  bool vok[Q];    // the vector lies inside the row
+
+  __device__ __forceinline__ float elem(int q, int e) const {
+    if constexpr (DT == DT_F32) return __uint_as_float(w[q][VEC == 1 ? 0 : e]);
+    else {
+      const uint32_t h = VEC == 1 ? w[q][0] : ((e & 1) ? w[q][e >> 1] >> 16 : w[q][e >> 1] & 0xFFFFu);
+      return DT == DT_BF16 ? __uint_as_float(h << 16) : f16_to_f32((uint16_t)h);
+    }
+  }
+};
+
+template <int DT>
+__device__ __forceinline__ float decode16(uint32_t h) {
+  return DT == DT_BF16 ? __uint_as_float(h << 16) : f16_to_f32((uint16_t)h);
+}
+
+template <int DT, int VEC>
+__device__ __forceinline__ void scan_load(const char* row, int base, int V, ChunkRegs<DT, VEC>& r) {
+  constexpr int Q = ChunkRegs<DT, VEC>::Q;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int i0 = base + (q * kThreads + (int)threadIdx.x) * VEC;
+    r.vok[q] = i0 < V;
+    // vectors past the row's end re-read its last vector: duplicates of row
+    // elements, harmless to the maximum and masked everywhere else
+    const int j = r.vok[q] ? i0 : V - VEC;
+    if constexpr (VEC == 1) {
+      r.w[q][0] = DT == DT_F32 ? ((const uint32_t*)row)[j] : (uint32_t)((const uint16_t*)row)[j];
+    } else {
+      const uint4 v = DT == DT_F32 ? *(const uint4*)((const float*)row + j) : *(const uint4*)((const uint16_t*)row + j);
+      r.w[q][0] = v.x; r.w[q][1] = v.y; r.w[q][2] = v.z; r.w[q][3] = v.w;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    if constexpr (VEC == 1) {
+      const float v = r.elem(q, 0);
+      r.vmax[q] = v;
+      r.vnan[q] = v != v;
+    } else if constexpr (DT == DT_F32) {
+      const int32_t* si = (const int32_t*)r.w[q];
+      const int32_t smax = max(max(si[0], si[1]), max(si[2], si[3]));
+      const uint32_t umin = min(min(r.w[q][0], r.w[q][1]), min(r.w[q][2], r.w[q][3]));
+      const uint32_t umax = max(max(r.w[q][0], r.w[q][1]), max(r.w[q][2], r.w[q][3]));
+      r.vmax[q] = __uint_as_float(smax >= 0 ? (uint32_t)smax : umin);
+      r.vnan[q] = smax > 0x7F800000 || umax > 0xFF800000u;
+    } else {
+      nvjsel_s16x2 smax = __builtin_bit_cast(nvjsel_s16x2, r.w[q][0]);
+      nvjsel_u16x2 umin = __builtin_bit_cast(nvjsel_u16x2, r.w[q][0]), umax = umin;
+#pragma unroll
+      for (int d = 1; d < 4; ++d) {
+        smax = __builtin_elementwise_max(smax, __builtin_bit_cast(nvjsel_s16x2, r.w[q][d]));
+        umin = __builtin_elementwise_min(umin, __builtin_bit_cast(nvjsel_u16x2, r.w[q][d]));
+        umax = __builtin_elementwise_max(umax, __builtin_bit_cast(nvjsel_u16x2, r.w[q][d]));
+      }
+      const int s1 = max((int)smax.x, (int)smax.y);
+      const uint32_t u1 = min((uint32_t)umin.x, (uint32_t)umin.y);
+      const uint32_t u3 = max((uint32_t)umax.x, (uint32_t)umax.y);
+      constexpr int kPosInf = DT == DT_BF16 ? 0x7F80 : 0x7C00;
+      constexpr uint32_t kNegInf = DT == DT_BF16 ? 0xFF80u : 0xFC00u;
+      r.vmax[q] = decode16<DT>(s1 >= 0 ? (uint32_t)s1 : u1);
+      r.vnan[q] = s1 > kPosInf || u3 > kNegInf;
+    }
+  }
+}
+
+// The wave's argmax key: its first NaN if it holds one (nan_wave), else the
+// first element equal (as floats: -0 == +0) to its maximum wm.  The first
+// index lies in the lowest vector slot q that holds a match and, within it,
+// in the lowest lane; one lane then scans that vector.
+template <int DT, int VEC>
+__device__ __forceinline__ unsigned long long wave_first_max(const ChunkRegs<DT, VEC>& r, int base, float wm,
+                                                             bool nan_wave) {
+  constexpr int Q = ChunkRegs<DT, VEC>::Q;
+  unsigned long long key = 0;
+  bool found = false;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    if (found) break;
+    const bool hit = r.vok[q] && (nan_wave ? r.vnan[q] : r.vmax[q] == wm);
+    const unsigned long long mask = __ballot(hit);
+    if (mask) {
+      found = true;
+      const int lane = __ffsll((long long)mask) - 1;
+      int e_hit = VEC;
+#pragma unroll
+      for (int e = VEC - 1; e >= 0; --e) {
+        const float v = r.elem(q, e);
+        if (nan_wave ? (v != v) : (v == wm)) e_hit = e;
+      }
+      const int idx = elem_index<VEC>(base, q * VEC + (e_hit < VEC ? e_hit : 0));
+      const int sel = __shfl(idx, lane, 64);
+      key = argmax_key(nan_wave ? __uint_as_float(0x7FFFFFFFu) : wm, (uint32_t)sel);
+    }
+  }
+  return key;
+}
+
+// Largest 16-bit prefix p such that at least kk lanes of the wave have
+// radix_key(v) >> 16 >= p (lanes holding no element of the row pass 0): a
+// bit-by-bit search, one compare and one popcount per step.
+__device__ __forceinline__ uint32_t wave_kth_prefix(float v, bool ok, uint32_t kk) {
+  const uint32_t k16 = ok ? (radix_key(v) >> 16) : 0u;
+  uint32_t p = 0;
+#pragma unroll
+  for (int bit = 15; bit >= 0; --bit) {
+    const uint32_t c = p | (1u << bit);
+    if ((uint32_t)__popcll(__ballot(k16 >= c)) >= kk) p = c;
+  }
+  return p;
+}
 
 template <int DT, int VEC>
 __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
+  constexpr int Q = kEPT / VEC;
   __shared__ ScanShared sh;
   const int b = blockIdx.y, c = blockIdx.x;
   const RowParams rp = row_params(a, b);
   const char* row = row_ptr(a, b);
   const int base = c * kChunk;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // Raw logits: x = l / T' is monotone in l, so maxima and the candidate test
   // run on l and only candidates pay for the division.
-  float l[kEPT];
-  uint32_t valid;
-  load_chunk_elems<DT, VEC, kEPT>(row, base, a.V, true, 1.0f, l, valid);
-  // first maximum with plain float compares: ties keep the earlier index and
-  // -0 == +0; NaN compares false, so the first NaN is tracked on its own
-  float bv = -INFINITY;
-  int bi = -1, ni = -1;
+  ChunkRegs<DT, VEC> r;
+  scan_load<DT, VEC>(row, base, a.V, r);
+  float tm = r.vmax[0];
+  bool tn = r.vnan[0];
 #pragma unroll
-  for (int j = 0; j < kEPT; ++j) {
-    const bool ok = (valid >> j) & 1u;
-    const float v = l[j];
-    const int i = elem_index<VEC>(base, j);
-    if (ok && (v > bv || bi < 0)) { bv = v; bi = i; }
-    if (ok && v != v && ni < 0) ni = i;
+  for (int q = 1; q < Q; ++q) { tm = fmaxf(tm, r.vmax[q]); tn |= r.vnan[q]; }
+  float wm = tm;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) wm = fmaxf(wm, __shfl_xor(wm, o, 64));
+  const bool wnan = __any(tn);
+  const unsigned long long wkey = wave_first_max<DT, VEC>(r, base, wm, wnan);
+  // FILTER rows with small k: the chunk's candidates are its elements at or
+  // above theta = min over waves w of the top 16 bits of the kk_w-th largest
+  // lane maximum of wave w, kk_w = ceil(k * L_w / L) for a wave holding L_w of
+  // the chunk's L lanes that hold elements (ceil(k/4) in a full chunk).  The
+  // waves then hold at least sum kk_w >= k lane maxima >= theta, so theta <=
+  // the chunk's k-th largest logit.  Less a margin of 8 orderable units for
+  // values the division by T' may merge.
+  const bool topk = rp.mode == ROW_FILTER && rp.k > 0 && rp.k <= kFastK;
+  uint32_t wfloor = 0xFFFFFFFFu;
+  if (topk && !wnan) {
+    // lane t holds an element iff its first vector (index t) lies in the row
+    const int nv = (min(a.V - base, kChunk) + VEC - 1) / VEC;
+    const int Lw = max(0, min(64, nv - 64 * wave)), L = min(nv, kThreads);
+    const uint32_t kk = (uint32_t)(((long long)rp.k * Lw + L - 1) / L);
+    float tv = r.vmax[0];  // the lane's maximum over its vectors inside the row
+#pragma unroll
+    for (int q = 1; q < Q; ++q)
+      if (r.vok[q]) tv = fmaxf(tv, r.vmax[q]);
+    wfloor = kk ? wave_kth_prefix(tv, r.vok[0], kk) << 16 : 0xFFFFFFFFu;
   }
-  if (ni >= 0) { bv = __uint_as_float(0x7FFFFFFFu); bi = ni; }
-  // (the first valid element seeds the maximum, so an all -inf chunk keeps index 0)
-  const unsigned long long tkey = bi >= 0 ? argmax_key(bv, (uint32_t)bi) : 0ull;
-  const unsigned long long cbest = block_max_u64(tkey, sh.g.red);
+  if (lane == 0) { sh.wkey[wave] = wkey; sh.wfloor[wave] = wfloor; }
+  if (threadIdx.x == 0) sh.cnt = 0;
+  __syncthreads();
+  unsigned long long cbest = sh.wkey[0];
+  uint32_t prefix = sh.wfloor[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / 64; ++w) {
+    cbest = max_u64(cbest, sh.wkey[w]);
+    prefix = min(prefix, sh.wfloor[w]);
+  }
   if (threadIdx.x == 0) {
     a.chunk_max[(size_t)b * a.nchunks + c] = cbest;
     if (c == 0) a.row_done[(size_t)b * kRowPad] = 0;
     if (b == 0 && c == 0) { a.list_n[0] = 0; a.list_n[1] = 0; }  // this call's work lists
   }
-  if (rp.mode != ROW_FILTER || rp.k == 0 || rp.k > kFastK) return;
-  const uint32_t bo = bi >= 0 ? ord_f32(bv) : 0u;
-
-  // FILTER with small k: theta = top 16 bits of the k-th largest per-thread
-  // maximum (two 8-bit radix passes), less a margin of 8 orderable units for
-  // values the division by T' may merge; every element >= theta is a candidate.
-  uint32_t prefix = 0, rem = (uint32_t)rp.k;
-#pragma unroll 1
-  for (int pass = 0; pass < 2; ++pass) {
-    const int shift = pass == 0 ? 24 : 16;
-    __syncthreads();
-    sh.hist[threadIdx.x] = 0;
-    __syncthreads();
-    if (pass == 0 || (bo >> 24) == (prefix >> 24)) atomicAdd(&sh.hist[(bo >> shift) & 255u], 1u);
-    __syncthreads();
-    const uint32_t h = sh.hist[255 - threadIdx.x];
-    uint32_t tot;
-    const uint32_t above = block_exclusive_scan<uint32_t>(h, sh.wsum, tot);
-    if (above < rem && rem <= above + h) { sh.sel = prefix | ((uint32_t)(255 - threadIdx.x) << shift); sh.rem = rem - above; }
-    __syncthreads();
-    prefix = sh.sel;
-    rem = sh.rem;
-  }
-  const uint32_t theta = prefix > 8u ? prefix - 8u : 0u;
+  if (!topk) return;
+  // a NaN chunk makes the row non-finite: select answers it without candidates
+  const bool nan_chunk = (uint32_t)(cbest >> 32) == 0xFFFFFFFFu;
+  const uint32_t theta = prefix == 0xFFFFFFFFu ? 0u : prefix > 8u ? prefix - 8u : 0u;
   // keys below ord(-inf) = 0x007FFFFF are NaN patterns: clamp to -inf
   const float theta_v = theta > 0x007FFFFFu ? radix_value(theta) : -INFINITY;
-  if (threadIdx.x == 0) {
-    sh.cnt = 0;
-    a.cand_floor[(size_t)b * a.nchunks + c] = theta_v;
+  uint32_t mine = 0;
+  if (!nan_chunk) {
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+      if (r.vok[q] && r.vmax[q] >= theta_v) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) mine += r.elem(q, e) >= theta_v ? 1u : 0u;
+      }
+  }
+  // wave-level reservation: one LDS atomic per wave
+  uint32_t incl = mine;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  const uint32_t wtot = __shfl(incl, 63, 64);
+  uint32_t wbase = 0;
+  if (lane == 0 && wtot) wbase = atomicAdd(&sh.cnt, wtot);
+  uint32_t slot = __shfl(wbase, 0, 64) + incl - mine;
+  unsigned long long* out = a.cand + ((size_t)b * a.nchunks + c) * kCandCap;
+  if (mine) {
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+      if (r.vok[q] && r.vmax[q] >= theta_v) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float l = r.elem(q, e);
+          if (l >= theta_v) {
+            if (slot < (uint32_t)kCandCap)
+              out[slot] = ((unsigned long long)radix_key(l / rp.tp) << 32) | (uint32_t)elem_index<VEC>(base, q * VEC + e);
+            ++slot;
+          }
+        }
+      }
   }
   __syncthreads();
-  unsigned long long* out = a.cand + ((size_t)b * a.nchunks + c) * kCandCap;
-#pragma unroll
-  for (int j = 0; j < kEPT; ++j)
-    if (((valid >> j) & 1u) && l[j] >= theta_v) {
-      const uint32_t slot = atomicAdd(&sh.cnt, 1u);
-      if (slot < (uint32_t)kCandCap)
-        out[slot] = ((unsigned long long)radix_key(l[j] / rp.tp) << 32) | (uint32_t)elem_index<VEC>(base, j);
-    }
-  __syncthreads();
-  if (threadIdx.x == 0)
+  if (threadIdx.x == 0) {
+    a.cand_floor[(size_t)b * a.nchunks + c] = theta_v;
     a.cand_count[(size_t)b * a.nchunks + c] = sh.cnt > (uint32_t)kCandCap ? kCandCap + 1 : sh.cnt;
+  }
 }
 
 // Value of a chunk-max key in the row's x space (the keys hold raw logits).
