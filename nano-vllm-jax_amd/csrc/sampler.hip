@@ -84,6 +84,8 @@ struct SampleArgs {
   int32_t* row_state;              // [B]
   unsigned long long* chunk_max;   // [B, nchunks]
   uint32_t* cand_count;            // [B, nchunks]
+  uint32_t* cand_count_a;          // [B, nchunks] tier A: the list's first entries, those >= cand_floor_a
+  float* cand_floor_a;             // [B, nchunks]
   float* cand_floor;               // [B, nchunks] logit floor of each chunk's candidates
   unsigned long long* cand;        // [B, nchunks, kCandCap]
   float* row_m;                    // [B]   max of x (top-p rows)
@@ -96,6 +98,7 @@ struct SampleArgs {
   uint32_t* row_items;             // [B * kRowPad] gumbel items queued per row
   uint32_t* list_topp;             // [B]
   int32_t* out_ids;
+  float* lane_tops;                // [B, nchunks, 4 waves, kTops] raw-logit lane maxima
   int topk;  // > 0: top-k selection (nvjsel_topk): every row FILTER with this k on raw logits
 };
 
@@ -376,6 +379,165 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* ws, T& total) {
   return before + incl - v;
 }
 
+// Value of a chunk-max key in the row's x space (the keys hold raw logits).
+__device__ __forceinline__ float chunk_max_x(const RowParams& rp, unsigned long long ck) {
+  const float l = unord_f32((uint32_t)(ck >> 32));
+  return rp.mode == ROW_GREEDY ? l : l / rp.tp;
+}
+
+// floor(p * Z) + 1, clamped to [1, Z]: the cumulative mass that must be reached.
+__device__ __forceinline__ unsigned long long topp_target(float p, unsigned long long Z) {
+  double pz = floor((double)p * (double)Z);
+  if (!(pz >= 0.0)) pz = 0.0;
+  unsigned long long P = (unsigned long long)pz;
+  if (Z > 0 && P > Z - 1) P = Z - 1;
+  return P + 1;
+}
+// ------------------------------------------------------------------ top-k rows from candidates
+// A FILTER row with k <= 256: the row floor is the larger of the largest chunk
+// floor and the k-th largest lane maximum the scan published (four per wave);
+// the candidates at or above it (about k of them) are rank-sorted in LDS, and
+// top-k, top-p and the exact Gumbel-max read the sorted prefix.
+static constexpr int kTops = 4;        // lane maxima published per wave
+static constexpr int kTopsChunks = 64; // chunks whose tops bound the row floor
+static constexpr int kFinCap = 512;    // survivors sorted in LDS
+
+struct FinishShared {
+  unsigned long long ent[kFinCap];
+  unsigned long long srt[kFinCap];
+  unsigned long long red[kThreads / 64];
+  unsigned long long wsum64[kThreads / 64];
+  uint32_t wsum32[kThreads / 64];
+  uint32_t cnt[kThreads], cnt_a[kThreads];
+  float fl_a[kThreads];
+  uint32_t n, kf, tau;
+};
+
+// Largest 16-bit prefix p with at least k of the row's published lane maxima
+// at or above p << 16 (0 when fewer than k are published).  Every published
+// value is a distinct element of the row, so (p << 16) <= the row's k-th
+// largest raw logit key.  Run by one wave; `nvals` <= 1024.
+__device__ __forceinline__ uint32_t row_tops_kth(const float* tops, int nvals, int k) {
+  const int lane = threadIdx.x & 63;
+  uint32_t key[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int j = lane + 64 * i;
+    key[i] = j < nvals ? radix_key(tops[j]) >> 16 : 0u;
+  }
+  const int nv = (nvals + 63) >> 6;
+  uint32_t p = 0;
+#pragma unroll 1
+  for (int bit = 15; bit >= 0; --bit) {
+    const uint32_t c = p | (1u << bit);
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (i < nv) cnt += (uint32_t)__popcll(__ballot(key[i] >= c));
+    if (cnt >= (uint32_t)k) p = c;
+  }
+  return p;
+}
+
+// Top-k (then top-p, then exact Gumbel-max) of a FILTER row with k <= 256 from
+// the scan's candidates, with the thresholds of the select kernel's candidate
+// path.  Returns false (nothing written) when a chunk's list overflowed or the
+// survivors do not fit in LDS.
+__device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp, float m, FinishShared& s) {
+  const int NC = a.nchunks, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (NC > kThreads) return false;
+  // round 1: chunk counts and floors, and (wave 0) the published lane maxima
+  float fl = -INFINITY;
+  if ((int)threadIdx.x < NC) {
+    const size_t i = (size_t)b * NC + threadIdx.x;
+    s.cnt[threadIdx.x] = a.cand_count[i];
+    s.cnt_a[threadIdx.x] = a.cand_count_a[i];
+    s.fl_a[threadIdx.x] = a.cand_floor_a[i];
+    fl = a.cand_floor[i];
+  }
+  if (wave == 0) {
+    const int nvals = min(NC, kTopsChunks) * (kThreads / 64) * kTops;
+    const uint32_t p = row_tops_kth(a.lane_tops + (size_t)b * NC * (kThreads / 64) * kTops, nvals, rp.k) << 16;
+    if (lane == 0) s.kf = p;
+  }
+  if (threadIdx.x == 0) s.n = 0;
+  const float flmax = unord_f32((uint32_t)block_max_u64(ord_f32(fl), s.red));  // (barriers)
+  // the row floor (raw logits) and, per chunk, how much of its list can reach it
+  const float F = fmaxf(s.kf > 0x007FFFFFu ? radix_value(s.kf) : -INFINITY, flmax);
+  const uint32_t kf = radix_key(F / rp.tp);
+  // round 2: eight threads per chunk read what they need of its list
+  int bad = 0;
+  for (int c0 = 0; c0 < NC; c0 += kThreads / 8) {
+    const int c = c0 + (int)(threadIdx.x >> 3);
+    int need = 0;
+    if (c < NC) {
+      need = F >= s.fl_a[c] ? (int)s.cnt_a[c] : (int)s.cnt[c];
+      bad |= need > kCandCap;
+      need = min(need, kCandCap);
+    }
+    const unsigned long long* src = a.cand + ((size_t)b * NC + c) * kCandCap;
+    for (int e0 = (int)(threadIdx.x & 7); e0 < need; e0 += 32) {
+      unsigned long long v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = e0 + 8 * q < need ? src[e0 + 8 * q] : 0ull;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (e0 + 8 * q < need && (uint32_t)(v[q] >> 32) >= kf) {
+          const uint32_t slot = atomicAdd(&s.n, 1u);
+          if (slot < (uint32_t)kFinCap) s.ent[slot] = v[q];
+        }
+    }
+  }
+  if (__syncthreads_or(bad)) return false;
+  __syncthreads();
+  const int n = (int)s.n;
+  if (n > kFinCap || n < rp.k) return false;
+  // rank sort, descending (keys are unique: they carry the index)
+  for (int i = threadIdx.x; i < n; i += kThreads) {
+    const unsigned long long e = s.ent[i];
+    int rank = 0;
+    for (int j = 0; j < n; ++j) rank += s.ent[j] > e ? 1 : 0;
+    s.srt[rank] = e;
+  }
+  __syncthreads();
+  // kept: every survivor >= the k-th largest (ties kept) -- a prefix
+  const uint32_t thr = (uint32_t)(s.srt[rp.k - 1] >> 32);
+  uint32_t mine = 0;
+  for (int i = threadIdx.x; i < n; i += kThreads) mine += (uint32_t)(s.srt[i] >> 32) >= thr ? 1u : 0u;
+  uint32_t tot;
+  (void)block_exclusive_scan<uint32_t>(mine, s.wsum32, tot);
+  const int nk = (int)tot;
+  uint32_t tau = thr;
+  if (rp.p < 1.0f) {
+    // top-p over the kept prefix in sorted order: thread t holds entries 2t, 2t + 1;
+    // the threshold is the key of the entry where the cumulative mass first
+    // reaches floor(p * Z) + 1 (the select kernel's weighted descent gives the same)
+    const int i0 = 2 * (int)threadIdx.x;
+    const unsigned long long m0 = i0 < nk ? fixed_mass(radix_value((uint32_t)(s.srt[i0] >> 32)), m) : 0ull;
+    const unsigned long long m1 = i0 + 1 < nk ? fixed_mass(radix_value((uint32_t)(s.srt[i0 + 1] >> 32)), m) : 0ull;
+    unsigned long long Z;
+    const unsigned long long ex = block_exclusive_scan<unsigned long long>(m0 + m1, s.wsum64, Z);
+    const unsigned long long target = topp_target(rp.p, Z);
+    if (i0 < nk && ex < target && target <= ex + m0) s.tau = (uint32_t)(s.srt[i0] >> 32);
+    if (i0 + 1 < nk && ex + m0 < target && target <= ex + m0 + m1) s.tau = (uint32_t)(s.srt[i0 + 1] >> 32);
+    __syncthreads();
+    tau = s.tau;
+  }
+  // exact Gumbel-max over the survivors >= tau
+  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+  unsigned long long best = 0;
+  for (int i = threadIdx.x; i < nk; i += kThreads) {
+    const unsigned long long ce = s.srt[i];
+    const uint32_t kk = (uint32_t)(ce >> 32);
+    if (kk < tau) continue;
+    const uint32_t idx = (uint32_t)ce;
+    best = max_u64(best, argmax_key(radix_value(kk) + exact_noise(a, b, key, (int)idx), idx));
+  }
+  best = block_max_u64(best, s.red);
+  if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)best);
+  return true;
+}
+
 // ------------------------------------------------------------------ 1. scan
 // One block per (chunk, row); thread t holds Q = EPT / VEC vectors of VEC
 // elements (elem_index).  Work per element is kept to a few VALU operations
@@ -386,7 +548,8 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* ws, T& total) {
 struct ScanShared {
   unsigned long long wkey[kThreads / 64];
   uint32_t wfloor[kThreads / 64];
-  uint32_t cnt;
+  float wtop[kThreads / 64];  // each wave's kTops-th largest lane maximum
+  uint32_t cnt, cnt_b;
 };
 
 typedef short nvjsel_s16x2 __attribute__((ext_vector_type(2)));
@@ -559,9 +722,24 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
     for (int q = 1; q < Q; ++q)
       if (r.vok[q]) tv = fmaxf(tv, r.vmax[q]);
     wfloor = kk ? wave_kth_prefix(tv, r.vok[0], kk) << 16 : 0xFFFFFFFFu;
+    // the wave's kTops largest lane maxima (-inf fills), for the row floor
+    float v = r.vok[0] ? tv : -INFINITY;
+    float* tops = a.lane_tops + (((size_t)b * a.nchunks + c) * (kThreads / 64) + wave) * kTops;
+#pragma unroll
+    for (int t = 0; t < kTops; ++t) {
+      float mx = v;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      if (lane == 0) tops[t] = mx;
+      if (lane == 0 && t == kTops - 1) sh.wtop[wave] = mx;
+      const unsigned long long hm = __ballot(v == mx);
+      if (lane == __ffsll((long long)hm) - 1) v = -INFINITY;
+    }
+  } else if (topk && lane < kTops) {
+    a.lane_tops[(((size_t)b * a.nchunks + c) * (kThreads / 64) + wave) * kTops + lane] = -INFINITY;
   }
   if (lane == 0) { sh.wkey[wave] = wkey; sh.wfloor[wave] = wfloor; }
-  if (threadIdx.x == 0) sh.cnt = 0;
+  if (threadIdx.x == 0) { sh.cnt = 0; sh.cnt_b = 0; }
   __syncthreads();
   unsigned long long cbest = sh.wkey[0];
   uint32_t prefix = sh.wfloor[0];
@@ -581,16 +759,26 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   const uint32_t theta = prefix == 0xFFFFFFFFu ? 0u : prefix > 8u ? prefix - 8u : 0u;
   // keys below ord(-inf) = 0x007FFFFF are NaN patterns: clamp to -inf
   const float theta_v = theta > 0x007FFFFFu ? radix_value(theta) : -INFINITY;
-  uint32_t mine = 0;
+  // Tier A, written first: candidates at or above t_a = min over waves of the
+  // wave's kTops-th largest lane maximum (the chunk holds at least
+  // 4 * kTops elements >= t_a).  A row floor >= t_a needs only tier A.
+  float t_a = sh.wtop[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / 64; ++w) t_a = fminf(t_a, sh.wtop[w]);
+  const float th_a = fmaxf(t_a, theta_v);
+  uint32_t mine = 0;  // tier A count | tier B count << 16
   if (!nan_chunk) {
 #pragma unroll
     for (int q = 0; q < Q; ++q)
       if (r.vok[q] && r.vmax[q] >= theta_v) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) mine += r.elem(q, e) >= theta_v ? 1u : 0u;
+        for (int e = 0; e < VEC; ++e) {
+          const float l = r.elem(q, e);
+          mine += l >= th_a ? 1u : (l >= theta_v ? 0x10000u : 0u);
+        }
       }
   }
-  // wave-level reservation: one LDS atomic per wave
+  // wave-level reservations: one LDS atomic per wave and tier
   uint32_t incl = mine;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -599,8 +787,13 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   }
   const uint32_t wtot = __shfl(incl, 63, 64);
   uint32_t wbase = 0;
-  if (lane == 0 && wtot) wbase = atomicAdd(&sh.cnt, wtot);
-  uint32_t slot = __shfl(wbase, 0, 64) + incl - mine;
+  if (lane == 0 && (wtot & 0xFFFFu)) wbase = atomicAdd(&sh.cnt, wtot & 0xFFFFu);
+  uint32_t slot_a = __shfl(wbase, 0, 64) + ((incl - mine) & 0xFFFFu);
+  __syncthreads();
+  const uint32_t n_a = sh.cnt;
+  wbase = 0;
+  if (lane == 0 && (wtot >> 16)) wbase = atomicAdd(&sh.cnt_b, wtot >> 16);
+  uint32_t slot_b = n_a + __shfl(wbase, 0, 64) + ((incl - mine) >> 16);
   unsigned long long* out = a.cand + ((size_t)b * a.nchunks + c) * kCandCap;
   if (mine) {
 #pragma unroll
@@ -610,24 +803,24 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
         for (int e = 0; e < VEC; ++e) {
           const float l = r.elem(q, e);
           if (l >= theta_v) {
+            const bool ta = l >= th_a;
+            const uint32_t slot = ta ? slot_a : slot_b;
             if (slot < (uint32_t)kCandCap)
               out[slot] = ((unsigned long long)radix_key(l / rp.tp) << 32) | (uint32_t)elem_index<VEC>(base, q * VEC + e);
-            ++slot;
+            slot_a += ta ? 1u : 0u;
+            slot_b += ta ? 0u : 1u;
           }
         }
       }
   }
   __syncthreads();
   if (threadIdx.x == 0) {
+    const uint32_t n = n_a + sh.cnt_b;
     a.cand_floor[(size_t)b * a.nchunks + c] = theta_v;
-    a.cand_count[(size_t)b * a.nchunks + c] = sh.cnt > (uint32_t)kCandCap ? kCandCap + 1 : sh.cnt;
+    a.cand_count[(size_t)b * a.nchunks + c] = n > (uint32_t)kCandCap ? kCandCap + 1 : n;
+    a.cand_count_a[(size_t)b * a.nchunks + c] = n_a;
+    a.cand_floor_a[(size_t)b * a.nchunks + c] = th_a;
   }
-}
-
-// Value of a chunk-max key in the row's x space (the keys hold raw logits).
-__device__ __forceinline__ float chunk_max_x(const RowParams& rp, unsigned long long ck) {
-  const float l = unord_f32((uint32_t)(ck >> 32));
-  return rp.mode == ROW_GREEDY ? l : l / rp.tp;
 }
 
 // ------------------------------------------------------------------ 2. select
@@ -694,14 +887,6 @@ __device__ uint32_t lds_desc(DescShared& s, const unsigned long long* v, int n, 
   return prefix;
 }
 
-// floor(p * Z) + 1, clamped to [1, Z]: the cumulative mass that must be reached.
-__device__ __forceinline__ unsigned long long topp_target(float p, unsigned long long Z) {
-  double pz = floor((double)p * (double)Z);
-  if (!(pz >= 0.0)) pz = 0.0;
-  unsigned long long P = (unsigned long long)pz;
-  if (Z > 0 && P > Z - 1) P = Z - 1;
-  return P + 1;
-}
 
 // Loads the row's candidates into LDS, keeping only those at or above the
 // row's floor: every chunk's floor is at most that chunk's k-th largest
@@ -988,6 +1173,7 @@ struct SelectShared {
   uint32_t prefix, rem;
   int flag;
   QueueShared q;
+  FinishShared fin;
 };
 
 __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
@@ -1032,6 +1218,10 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
       ans = block_max_u64(first, s.red);
     }
     if (threadIdx.x == 0) { a.out_ids[b] = (int32_t)(~(uint32_t)ans); a.row_state[b] = STATE_DONE; }
+    return;
+  }
+  if (rp.k > 0 && rp.k <= kFastK && finish_topk_row(a, b, rp, m, s.fin)) {
+    if (threadIdx.x == 0) a.row_state[b] = STATE_DONE;
     return;
   }
   bool fast = rp.k > 0 && rp.k <= kFastK && NC < 1024;
@@ -1400,7 +1590,7 @@ __global__ void __launch_bounds__(kThreads) sample_gumbel_kernel(SampleArgs a) {
 }
 
 struct WsLayout {
-  size_t row_key, row_tau, row_state, chunk_max, cand_count, cand_floor, cand, row_m, topp_hist, topp_cand, topp_n;
+  size_t lane_tops, row_key, row_tau, row_state, chunk_max, cand_count, cand_count_a, cand_floor_a, cand_floor, cand, row_m, topp_hist, topp_cand, topp_n;
   size_t list_n, list_gumbel, list_topp, row_done, row_items, total;
 };
 
@@ -1408,11 +1598,14 @@ static WsLayout ws_layout(int B, int V) {
   const size_t nc = (size_t)((V + kChunk - 1) / kChunk);
   WsLayout w;
   size_t o = 0;
+  w.lane_tops = o;  o += align_up((size_t)B * nc * (kThreads / 64) * kTops * 4, 256);
   w.row_key = o;    o += (size_t)B * kRowPad8 * 8;
   w.row_tau = o;    o += align_up((size_t)B * 4, 256);
   w.row_state = o;  o += align_up((size_t)B * 4, 256);
   w.chunk_max = o;  o += align_up((size_t)B * nc * 8, 256);
   w.cand_count = o; o += align_up((size_t)B * nc * 4, 256);
+  w.cand_count_a = o; o += align_up((size_t)B * nc * 4, 256);
+  w.cand_floor_a = o; o += align_up((size_t)B * nc * 4, 256);
   w.cand_floor = o; o += align_up((size_t)B * nc * 4, 256);
   w.cand = o;       o += align_up((size_t)B * nc * kCandCap * 8, 256);
   w.row_m = o;      o += align_up((size_t)B * 4, 256);
@@ -1443,11 +1636,14 @@ static SampleArgs make_args(const void* logits, int dtype, int batch, int vocab,
   a.V = vocab;
   a.nchunks = (vocab + kChunk - 1) / kChunk;
   a.stride = row_stride;
+  a.lane_tops = (float*)(ws + w.lane_tops);
   a.row_key = (unsigned long long*)(ws + w.row_key);
   a.row_tau = (uint32_t*)(ws + w.row_tau);
   a.row_state = (int32_t*)(ws + w.row_state);
   a.chunk_max = (unsigned long long*)(ws + w.chunk_max);
   a.cand_count = (uint32_t*)(ws + w.cand_count);
+  a.cand_count_a = (uint32_t*)(ws + w.cand_count_a);
+  a.cand_floor_a = (float*)(ws + w.cand_floor_a);
   a.cand_floor = (float*)(ws + w.cand_floor);
   a.cand = (unsigned long long*)(ws + w.cand);
   a.row_m = (float*)(ws + w.row_m);
