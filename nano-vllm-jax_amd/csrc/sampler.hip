@@ -260,91 +260,124 @@ __device__ __forceinline__ void load_chunk_elems(const char* row, int base, int 
   }
 }
 
-// Scratch of the block-level Gumbel-max: exact-rescoring queue.
+// Scratch of the block-level Gumbel-max: the dense list of elements that need
+// a draw and the exact-rescoring queue.
 static constexpr int kExactCap = 256;
+static constexpr int kDenseCap = 2048;  // kThreads * kGumbelEPT
 struct GumbelShared {
   unsigned long long red[kThreads / 64];
+  uint32_t wsum[kThreads / 64];
+  float dx[kDenseCap];
+  uint32_t di[kDenseCap];
   float qx[kExactCap];
   uint32_t qi[kExactCap];
   uint32_t n;
-  float s_cur;
 };
 
+template <typename T>
+__device__ __forceinline__ T block_exclusive_scan(T v, T* ws, T& total);
+
 // Gumbel-max over this thread's elements x[j] (index elem_index(base, j)) whose
-// bit in `act` is set; s_cur is a score already reached by some element.  Returns the block's exact best key (all threads).  The
-// few near-maximal elements are queued in LDS and rescored exactly by the
-// whole block, so the fp64 path is not unrolled per element.
+// bit in `act` is set; s_cur is a score already reached by some element.
+// Returns the block's exact best key (all threads).  Elements that cannot beat
+// s_cur are dropped first and the rest are packed densely in LDS, so the
+// Threefry work (four interleaved chains per thread) follows the elements that
+// need a draw, not the block's width.  The few near-maximal elements are then
+// queued and rescored exactly by the whole block.
 template <int EPT, int VEC>
 __device__ __forceinline__ unsigned long long block_gumbel(const SampleArgs& a, int b, const TfKey& key,
                                                            const float (&x)[EPT], int base, uint32_t act,
                                                            float s_cur, GumbelShared& sh) {
+  static_assert(EPT * kThreads <= kDenseCap, "dense list holds the block's elements");
 #pragma unroll
   for (int j = 0; j < EPT; ++j)
     if (x[j] + NVJSEL_GUMBEL_MAX < s_cur) act &= ~(1u << j);  // cannot beat a score found; NaN stays
-  // fast draws in groups of four elements: four interleaved Threefry chains,
-  // skipped when no lane of the wave needs any of the group
+  uint32_t n;
+  uint32_t pos = block_exclusive_scan<uint32_t>((uint32_t)__popc(act), sh.wsum, n);
+  if (n == 0) return 0;  // nothing active in the block
+#pragma unroll
+  for (int j = 0; j < EPT; ++j)
+    if ((act >> j) & 1u) {
+      sh.dx[pos] = x[j];
+      sh.di[pos] = (uint32_t)elem_index<VEC>(base, j);
+      ++pos;
+    }
+  __syncthreads();
+  // dense entry e = 4 * kThreads * g + 4 * t + j
+  constexpr int G = EPT / 4;
   float st[EPT];
   uint32_t tmax = 0;  // ord of the approximate maximum
 #pragma unroll
-  for (int g = 0; g < EPT / 4; ++g) {
-    const uint32_t gm = (act >> (4 * g)) & 0xFu;
-    float t[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    if (__any(gm != 0u)) {
-      uint32_t idx[4];
+  for (int g = 0; g < G; ++g) {
+    const int e0 = 4 * kThreads * g + 4 * (int)threadIdx.x;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) idx[e] = (uint32_t)elem_index<VEC>(base, 4 * g + e);
+    for (int j = 0; j < 4; ++j) st[4 * g + j] = -INFINITY;
+    if (__any(e0 < (int)n)) {
+      uint32_t idx[4];
+      float xv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool in = e0 + j < (int)n;
+        idx[j] = in ? sh.di[e0 + j] : 0u;
+        xv[j] = in ? sh.dx[e0 + j] : -INFINITY;
+      }
+      float t[4];
       if (a.noise) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] = x[4 * g + e] + a.noise[(size_t)b * a.V + idx[e]];
+        for (int j = 0; j < 4; ++j) t[j] = xv[j] + a.noise[(size_t)b * a.V + idx[j]];
       } else {
         uint32_t bits[4];
         random_bits32_n<4>(key, idx, bits);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] = x[4 * g + e] + gumbel_fast_from_bits(bits[e]);
+        for (int j = 0; j < 4; ++j) t[j] = xv[j] + gumbel_fast_from_bits(bits[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool in = e0 + j < (int)n;
+        const float v = (t[j] != t[j]) ? INFINITY : t[j];  // NaN only from a NaN logit
+        st[4 * g + j] = in ? v : -INFINITY;
+        const uint32_t o = in ? ord_f32(v) : 0u;
+        tmax = o > tmax ? o : tmax;
       }
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bool on = (gm >> e) & 1u;
-      const float v = (t[e] != t[e]) ? INFINITY : t[e];  // NaN only from a NaN logit
-      st[4 * g + e] = on ? v : -INFINITY;
-      const uint32_t o = on ? ord_f32(v) : 0u;
-      tmax = o > tmax ? o : tmax;
-    }
   }
-  const unsigned long long any = block_max_u64(((unsigned long long)tmax << 32) | (act ? 1u : 0u), sh.red);
-  if ((any & 1ull) == 0 && (any >> 32) == 0) return 0;  // nothing active in the block
-  const float m = unord_f32((uint32_t)(any >> 32));
+  const float m = unord_f32((uint32_t)(block_max_u64(tmax, sh.red)));
+#ifdef NVJSEL_PROBE_NOEXACT
+  return m > 1e30f ? 1ull : 2ull;
+#endif
   // |fast - exact| <= ~2e-5 on the draw, plus one ulp of the sum
   const float thr = m - (1e-3f + fabsf(m) * 4.8e-7f);
   uint32_t cm = 0;
 #pragma unroll
-  for (int j = 0; j < EPT; ++j)
-    if (((act >> j) & 1u) && st[j] >= thr) cm |= 1u << j;
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (4 * kThreads * g + 4 * (int)threadIdx.x + j < (int)n && st[4 * g + j] >= thr) cm |= 1u << (4 * g + j);
   unsigned long long best = 0;
   for (;;) {
     __syncthreads();
     if (threadIdx.x == 0) sh.n = 0;
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-      if (!((cm >> j) & 1u)) continue;
+    for (int q = 0; q < EPT; ++q) {
+      if (!((cm >> q) & 1u)) continue;
       const uint32_t slot = atomicAdd(&sh.n, 1u);
       if (slot < (uint32_t)kExactCap) {
-        sh.qx[slot] = x[j];
-        sh.qi[slot] = (uint32_t)elem_index<VEC>(base, j);
-        cm &= ~(1u << j);
+        const int e = 4 * kThreads * (q / 4) + 4 * (int)threadIdx.x + (q % 4);
+        sh.qx[slot] = sh.dx[e];
+        sh.qi[slot] = sh.di[e];
+        cm &= ~(1u << q);
       }
     }
     __syncthreads();
-    const uint32_t n = sh.n;
-    const int lim = n < (uint32_t)kExactCap ? (int)n : kExactCap;
+    const uint32_t nq = sh.n;
+    const int lim = nq < (uint32_t)kExactCap ? (int)nq : kExactCap;
     for (int e = threadIdx.x; e < lim; e += kThreads) {
       const uint32_t i = sh.qi[e];
       const float sc = sh.qx[e] + exact_noise(a, b, key, (int)i);
       best = max_u64(best, argmax_key(sc, i));
     }
-    if (n <= (uint32_t)kExactCap) break;
+    if (nq <= (uint32_t)kExactCap) break;
   }
   return block_max_u64(best, sh.red);
 }
