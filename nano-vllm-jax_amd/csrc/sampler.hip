@@ -342,11 +342,11 @@ __device__ __forceinline__ unsigned long long block_gumbel(const SampleArgs& a, 
     }
   }
   const float m = unord_f32((uint32_t)(block_max_u64(tmax, sh.red)));
-#ifdef NVJSEL_PROBE_NOEXACT
-  return m > 1e30f ? 1ull : 2ull;
-#endif
   // |fast - exact| <= ~2e-5 on the draw, plus one ulp of the sum
-  const float thr = m - (1e-3f + fabsf(m) * 4.8e-7f);
+  const float margin = 1e-3f + fabsf(m) * 4.8e-7f;
+  // nothing here can beat the score already reached: no exact rescoring
+  if (m + margin < s_cur) return 0;
+  const float thr = m - margin;
   uint32_t cm = 0;
 #pragma unroll
   for (int g = 0; g < G; ++g)
