@@ -585,6 +585,32 @@ struct ScanShared {
   uint32_t cnt, cnt_b;
 };
 
+// Wave-wide max and inclusive prefix sum with DPP row shifts and row
+// broadcasts (no LDS round trips): the result of the max is in every lane,
+// the scan is inclusive in lane order.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f32(float v, float old) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = fmaxf(v, dpp_f32<0x111, 0xF>(v, -INFINITY));  // row_shr:1
+  v = fmaxf(v, dpp_f32<0x112, 0xF>(v, -INFINITY));  // row_shr:2
+  v = fmaxf(v, dpp_f32<0x114, 0xF>(v, -INFINITY));  // row_shr:4
+  v = fmaxf(v, dpp_f32<0x118, 0xF>(v, -INFINITY));  // row_shr:8
+  v = fmaxf(v, dpp_f32<0x142, 0xA>(v, -INFINITY));  // row_bcast:15
+  v = fmaxf(v, dpp_f32<0x143, 0xC>(v, -INFINITY));  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);
+  return v;
+}
+
 typedef short nvjsel_s16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short nvjsel_u16x2 __attribute__((ext_vector_type(2)));
 
@@ -732,8 +758,7 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
 #pragma unroll
   for (int q = 1; q < Q; ++q) { tm = fmaxf(tm, r.vmax[q]); tn |= r.vnan[q]; }
   float wm = tm;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) wm = fmaxf(wm, __shfl_xor(wm, o, 64));
+  wm = wave_max_f32(wm);
   const bool wnan = __any(tn);
   const unsigned long long wkey = wave_first_max<DT, VEC>(r, base, wm, wnan);
   // FILTER rows with small k: the chunk's candidates are its elements at or
@@ -743,7 +768,11 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   // waves then hold at least sum kk_w >= k lane maxima >= theta, so theta <=
   // the chunk's k-th largest logit.  Less a margin of 8 orderable units for
   // values the division by T' may merge.
+#ifdef NVJSEL_PROBE_NOTOPK
+  const bool topk = false;
+#else
   const bool topk = rp.mode == ROW_FILTER && rp.k > 0 && rp.k <= kFastK;
+#endif
   uint32_t wfloor = 0xFFFFFFFFu;
   if (topk && !wnan) {
     // lane t holds an element iff its first vector (index t) lies in the row
@@ -760,9 +789,7 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
     float* tops = a.lane_tops + (((size_t)b * a.nchunks + c) * (kThreads / 64) + wave) * kTops;
 #pragma unroll
     for (int t = 0; t < kTops; ++t) {
-      float mx = v;
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      const float mx = wave_max_f32(v);
       if (lane == 0) tops[t] = mx;
       if (lane == 0 && t == kTops - 1) sh.wtop[wave] = mx;
       const unsigned long long hm = __ballot(v == mx);
@@ -812,13 +839,8 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
       }
   }
   // wave-level reservations: one LDS atomic per wave and tier
-  uint32_t incl = mine;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t o = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += o;
-  }
-  const uint32_t wtot = __shfl(incl, 63, 64);
+  const uint32_t incl = wave_incl_sum(mine);
+  const uint32_t wtot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
   uint32_t wbase = 0;
   if (lane == 0 && (wtot & 0xFFFFu)) wbase = atomicAdd(&sh.cnt, wtot & 0xFFFFu);
   uint32_t slot_a = __shfl(wbase, 0, 64) + ((incl - mine) & 0xFFFFu);
