@@ -62,7 +62,6 @@ static constexpr int kChunk = kThreads * kEPT;     // 8192 elements per block
 static constexpr int kFastK = 256;                 // top-k resolved from candidates
 static constexpr int kCandCap = 512;               // candidates kept per chunk
 static constexpr int kSelCap = 8192;               // candidates per row held in LDS
-static constexpr int kKeptCap = 2048;              // survivors of top-k sorted for top-p
 static constexpr int kToppBins = 1024;             // 1/32-nat mass bins below the row max
 static constexpr float kToppBinScale = 32.0f;
 static constexpr int kToppCap = 8192;              // elements of the crossing bin
@@ -98,7 +97,7 @@ struct SampleArgs {
   uint32_t* row_items;             // [B * kRowPad] gumbel items queued per row
   uint32_t* list_topp;             // [B]
   int32_t* out_ids;
-  float* lane_tops;                // [B, nchunks, 4 waves, kTops] raw-logit lane maxima
+  float* lane_tops;                // [B, nchunks, 4 waves, kTopsPub] largest raw-logit lane maxima
   int topk;  // > 0: top-k selection (nvjsel_topk): every row FILTER with this k on raw logits
 };
 
@@ -431,8 +430,9 @@ __device__ __forceinline__ unsigned long long topp_target(float p, unsigned long
 // floor and the k-th largest lane maximum the scan published (four per wave);
 // the candidates at or above it (about k of them) are rank-sorted in LDS, and
 // top-k, top-p and the exact Gumbel-max read the sorted prefix.
-static constexpr int kTops = 4;        // lane maxima published per wave
-static constexpr int kTopsChunks = 64; // chunks whose tops bound the row floor
+static constexpr int kTops = 8;        // lane maxima ranked per wave (tier A bound)
+static constexpr int kTopsPub = 4;     // of them published per wave (row floor)
+static constexpr int kTopsChunks = 64; // chunks whose tops bound the row floor (<= 1024 values)
 static constexpr int kFinCap = 512;    // survivors sorted in LDS
 
 struct FinishShared {
@@ -489,8 +489,8 @@ __device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp,
     fl = a.cand_floor[i];
   }
   if (wave == 0) {
-    const int nvals = min(NC, kTopsChunks) * (kThreads / 64) * kTops;
-    const uint32_t p = row_tops_kth(a.lane_tops + (size_t)b * NC * (kThreads / 64) * kTops, nvals, rp.k) << 16;
+    const int nvals = min(NC, kTopsChunks) * (kThreads / 64) * kTopsPub;
+    const uint32_t p = row_tops_kth(a.lane_tops + (size_t)b * NC * (kThreads / 64) * kTopsPub, nvals, rp.k) << 16;
     if (lane == 0) s.kf = p;
   }
   if (threadIdx.x == 0) s.n = 0;
@@ -504,8 +504,9 @@ __device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp,
     const int c = c0 + (int)(threadIdx.x >> 3);
     int need = 0;
     if (c < NC) {
-      need = F >= s.fl_a[c] ? (int)s.cnt_a[c] : (int)s.cnt[c];
-      bad |= need > kCandCap;
+      // the sampler's lists hold tier A only: a floor below it needs the exact path
+      need = (int)s.cnt_a[c];
+      bad |= F < s.fl_a[c] || need > kCandCap;
       need = min(need, kCandCap);
     }
     const unsigned long long* src = a.cand + ((size_t)b * NC + c) * kCandCap;
@@ -582,7 +583,7 @@ struct ScanShared {
   unsigned long long wkey[kThreads / 64];
   uint32_t wfloor[kThreads / 64];
   float wtop[kThreads / 64];  // each wave's kTops-th largest lane maximum
-  uint32_t cnt, cnt_b;
+  uint32_t cnt, cnt_b, waves;
 };
 
 // Wave-wide max and inclusive prefix sum with DPP row shifts and row
@@ -630,6 +631,24 @@ struct ChunkRegs {
   bool vnan[Q];   // the vector holds a NaN
   bool vok[Q];    // the vector lies inside the row
 
+  // vector q's raw words (q may differ across lanes: a select per vector slot)
+  __device__ __forceinline__ void pick(int q, uint32_t (&wv)[W]) const {
+#pragma unroll
+    for (int d = 0; d < W; ++d) wv[d] = w[0][d];
+#pragma unroll
+    for (int qq = 1; qq < Q; ++qq)
+      if (q == qq) {
+#pragma unroll
+        for (int d = 0; d < W; ++d) wv[d] = w[qq][d];
+      }
+  }
+  static __device__ __forceinline__ float decode(const uint32_t (&wv)[W], int e) {
+    if constexpr (DT == DT_F32) return __uint_as_float(wv[VEC == 1 ? 0 : e]);
+    else {
+      const uint32_t h = VEC == 1 ? wv[0] : ((e & 1) ? wv[e >> 1] >> 16 : wv[e >> 1] & 0xFFFFu);
+      return DT == DT_BF16 ? __uint_as_float(h << 16) : f16_to_f32((uint16_t)h);
+    }
+  }
   __device__ __forceinline__ float elem(int q, int e) const {
     if constexpr (DT == DT_F32) return __uint_as_float(w[q][VEC == 1 ? 0 : e]);
     else {
@@ -786,20 +805,21 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
     wfloor = kk ? wave_kth_prefix(tv, r.vok[0], kk) << 16 : 0xFFFFFFFFu;
     // the wave's kTops largest lane maxima (-inf fills), for the row floor
     float v = r.vok[0] ? tv : -INFINITY;
-    float* tops = a.lane_tops + (((size_t)b * a.nchunks + c) * (kThreads / 64) + wave) * kTops;
+    float* tops = a.lane_tops + (((size_t)b * a.nchunks + c) * (kThreads / 64) + wave) * kTopsPub;
 #pragma unroll
     for (int t = 0; t < kTops; ++t) {
       const float mx = wave_max_f32(v);
-      if (lane == 0) tops[t] = mx;
+      if (lane == 0 && t < kTopsPub) tops[t] = mx;
       if (lane == 0 && t == kTops - 1) sh.wtop[wave] = mx;
       const unsigned long long hm = __ballot(v == mx);
       if (lane == __ffsll((long long)hm) - 1) v = -INFINITY;
     }
-  } else if (topk && lane < kTops) {
-    a.lane_tops[(((size_t)b * a.nchunks + c) * (kThreads / 64) + wave) * kTops + lane] = -INFINITY;
+  } else if (topk && lane < kTopsPub) {
+    if (lane == 0) sh.wtop[wave] = -INFINITY;
+    a.lane_tops[(((size_t)b * a.nchunks + c) * (kThreads / 64) + wave) * kTopsPub + lane] = -INFINITY;
   }
   if (lane == 0) { sh.wkey[wave] = wkey; sh.wfloor[wave] = wfloor; }
-  if (threadIdx.x == 0) { sh.cnt = 0; sh.cnt_b = 0; }
+  if (threadIdx.x == 0) { sh.cnt = 0; sh.cnt_b = 0; sh.waves = 0; }
   __syncthreads();
   unsigned long long cbest = sh.wkey[0];
   uint32_t prefix = sh.wfloor[0];
@@ -821,60 +841,73 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   const float theta_v = theta > 0x007FFFFFu ? radix_value(theta) : -INFINITY;
   // Tier A, written first: candidates at or above t_a = min over waves of the
   // wave's kTops-th largest lane maximum (the chunk holds at least
-  // 4 * kTops elements >= t_a).  A row floor >= t_a needs only tier A.
+  // 4 * kTops elements >= t_a).  A row floor >= t_a needs only tier A, and the
+  // sampler's fast path takes no other (the rare row that needs more takes
+  // the exact path), so only nvjsel_topk writes tier B: the rest down to theta.
   float t_a = sh.wtop[0];
 #pragma unroll
   for (int w = 1; w < kThreads / 64; ++w) t_a = fminf(t_a, sh.wtop[w]);
   const float th_a = fmaxf(t_a, theta_v);
-  uint32_t mine = 0;  // tier A count | tier B count << 16
+  const float lo = a.topk > 0 ? theta_v : th_a;
+  // vectors holding a candidate, walked sparsely: each lane visits only its own
+  uint32_t pend = 0;
   if (!nan_chunk) {
 #pragma unroll
-    for (int q = 0; q < Q; ++q)
-      if (r.vok[q] && r.vmax[q] >= theta_v) {
+    for (int q = 0; q < Q; ++q) pend |= (r.vok[q] && r.vmax[q] >= lo ? 1u : 0u) << q;
+  }
+  uint32_t mine = 0;  // tier A count | tier B count << 16
+  for (uint32_t p = pend; p; p &= p - 1) {
+    uint32_t wv[ChunkRegs<DT, VEC>::W];
+    r.pick(__builtin_ctz(p), wv);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float l = r.elem(q, e);
-          mine += l >= th_a ? 1u : (l >= theta_v ? 0x10000u : 0u);
-        }
-      }
+    for (int e = 0; e < VEC; ++e) {
+      const float l = ChunkRegs<DT, VEC>::decode(wv, e);
+      mine += l >= th_a ? 1u : (l >= lo ? 0x10000u : 0u);
+    }
   }
   // wave-level reservations: one LDS atomic per wave and tier
   const uint32_t incl = wave_incl_sum(mine);
   const uint32_t wtot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
   uint32_t wbase = 0;
   if (lane == 0 && (wtot & 0xFFFFu)) wbase = atomicAdd(&sh.cnt, wtot & 0xFFFFu);
-  uint32_t slot_a = __shfl(wbase, 0, 64) + ((incl - mine) & 0xFFFFu);
-  __syncthreads();
-  const uint32_t n_a = sh.cnt;
-  wbase = 0;
-  if (lane == 0 && (wtot >> 16)) wbase = atomicAdd(&sh.cnt_b, wtot >> 16);
-  uint32_t slot_b = n_a + __shfl(wbase, 0, 64) + ((incl - mine) >> 16);
-  unsigned long long* out = a.cand + ((size_t)b * a.nchunks + c) * kCandCap;
-  if (mine) {
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-      if (r.vok[q] && r.vmax[q] >= theta_v) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float l = r.elem(q, e);
-          if (l >= theta_v) {
-            const bool ta = l >= th_a;
-            const uint32_t slot = ta ? slot_a : slot_b;
-            if (slot < (uint32_t)kCandCap)
-              out[slot] = ((unsigned long long)radix_key(l / rp.tp) << 32) | (uint32_t)elem_index<VEC>(base, q * VEC + e);
-            slot_a += ta ? 1u : 0u;
-            slot_b += ta ? 0u : 1u;
-          }
-        }
-      }
+  uint32_t slot_a = (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase) + ((incl - mine) & 0xFFFFu);
+  uint32_t slot_b = 0;
+  if (a.topk > 0) {
+    __syncthreads();
+    const uint32_t n_a = sh.cnt;
+    wbase = 0;
+    if (lane == 0 && (wtot >> 16)) wbase = atomicAdd(&sh.cnt_b, wtot >> 16);
+    slot_b = n_a + (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase) + ((incl - mine) >> 16);
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t n = n_a + sh.cnt_b;
-    a.cand_floor[(size_t)b * a.nchunks + c] = theta_v;
-    a.cand_count[(size_t)b * a.nchunks + c] = n > (uint32_t)kCandCap ? kCandCap + 1 : n;
-    a.cand_count_a[(size_t)b * a.nchunks + c] = n_a;
-    a.cand_floor_a[(size_t)b * a.nchunks + c] = th_a;
+  unsigned long long* out = a.cand + ((size_t)b * a.nchunks + c) * kCandCap;
+  for (uint32_t p = mine ? pend : 0u; p; p &= p - 1) {
+    const int q = __builtin_ctz(p);
+    uint32_t wv[ChunkRegs<DT, VEC>::W];
+    r.pick(q, wv);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float l = ChunkRegs<DT, VEC>::decode(wv, e);
+      if (l >= lo) {
+        const bool ta = l >= th_a;
+        const uint32_t slot = ta ? slot_a : slot_b;
+        if (slot < (uint32_t)kCandCap)
+          out[slot] = ((unsigned long long)radix_key(l / rp.tp) << 32) | (uint32_t)elem_index<VEC>(base, q * VEC + e);
+        slot_a += ta ? 1u : 0u;
+        slot_b += ta ? 0u : 1u;
+      }
+    }
+  }
+  // the last wave to finish publishes the counts (a block barrier would wait
+  // for every candidate store)
+  if (lane == 0) {
+    const uint32_t done = atomicAdd(&sh.waves, 1u);
+    if (done == kThreads / 64 - 1) {
+      const uint32_t n_a = atomicAdd(&sh.cnt, 0u), n = n_a + atomicAdd(&sh.cnt_b, 0u);
+      a.cand_floor[(size_t)b * a.nchunks + c] = theta_v;
+      a.cand_count[(size_t)b * a.nchunks + c] = n > (uint32_t)kCandCap ? kCandCap + 1 : n;
+      a.cand_count_a[(size_t)b * a.nchunks + c] = n_a;
+      a.cand_floor_a[(size_t)b * a.nchunks + c] = th_a;
+    }
   }
 }
 
@@ -1217,16 +1250,7 @@ __device__ __forceinline__ void queue_chunks(const SampleArgs& a, int b, const R
 }
 
 struct SelectShared {
-  unsigned long long cand[kSelCap];
-  unsigned long long kept[kKeptCap];
   unsigned long long red[kThreads / 64];
-  DescShared d;
-  uint32_t off[1025];
-  uint32_t wsum32[kThreads / 64];
-  unsigned long long wsum64[kThreads / 64];
-  uint32_t n, nk;
-  uint32_t prefix, rem;
-  int flag;
   QueueShared q;
   FinishShared fin;
 };
@@ -1279,81 +1303,19 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     if (threadIdx.x == 0) a.row_state[b] = STATE_DONE;
     return;
   }
-  bool fast = rp.k > 0 && rp.k <= kFastK && NC < 1024;
-  if (fast) {
-    // candidate counts -> offsets (thread t owns chunks 4t..4t+3)
-    uint32_t cnt[4], local = 0;
-    int bad = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int c = threadIdx.x * 4 + q;
-      cnt[q] = c < NC ? a.cand_count[(size_t)b * NC + c] : 0u;
-      bad |= cnt[q] > (uint32_t)kCandCap;
-      local += cnt[q];
-    }
-    uint32_t tot;
-    uint32_t o = block_exclusive_scan<uint32_t>(local, s.wsum32, tot);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int c = threadIdx.x * 4 + q;
-      if (c <= NC) s.off[c] = o;
-      o += cnt[q];
-    }
-    const int anybad = __syncthreads_or(bad);
-    fast = !anybad;
-    if (fast) fast = load_candidates(a, b, rp, s.off, (int)tot, s.cand, kSelCap, &s.n, s.red) <= kSelCap;
+  // Every other FILTER row: top-p-only rows go to the histogram passes, the
+  // rest (k > 256, rows whose floor falls below a chunk's tier A, crowded
+  // ties) to the exact whole-row path.
+  const bool topp_only = rp.k == 0 && rp.p < 1.0f;
+  if (topp_only) {  // the histogram pass accumulates into these
+    for (int d = threadIdx.x; d < kToppBins; d += blockDim.x) a.topp_hist[(size_t)b * kToppBins + d] = 0;
+    if (threadIdx.x == 0) a.topp_n[b] = 0;
   }
-  if (!fast) {
-    const bool topp_only = rp.k == 0 && rp.p < 1.0f;
-    if (topp_only) {  // the histogram pass accumulates into these
-      for (int d = threadIdx.x; d < kToppBins; d += blockDim.x) a.topp_hist[(size_t)b * kToppBins + d] = 0;
-      if (threadIdx.x == 0) a.topp_n[b] = 0;
-    }
-    if (threadIdx.x == 0) {
-      a.row_state[b] = topp_only ? STATE_TOPP : STATE_HEAVY;
-      a.row_m[b] = m;
-      if (topp_only) queue_row(&a.list_n[1], a.list_topp, b);
-    }
-    return;
+  if (threadIdx.x == 0) {
+    a.row_state[b] = topp_only ? STATE_TOPP : STATE_HEAVY;
+    a.row_m[b] = m;
+    if (topp_only) queue_row(&a.list_n[1], a.list_topp, b);
   }
-  const int n = (int)s.n;
-  // exact top-k threshold
-  const uint32_t tk = lds_desc<false>(s.d, s.cand, n, (unsigned long long)rp.k, 0.0f);
-  if (threadIdx.x == 0) s.nk = 0;
-  __syncthreads();
-  for (int e = threadIdx.x; e < n; e += blockDim.x) {
-    if ((uint32_t)(s.cand[e] >> 32) >= tk) {
-      const uint32_t slot = atomicAdd(&s.nk, 1u);
-      if (slot < (uint32_t)kKeptCap) s.kept[slot] = s.cand[e];
-    }
-  }
-  __syncthreads();
-  const int nk = (int)s.nk;
-  if (nk > kKeptCap) {  // too many ties at the k-th value for the LDS path
-    if (threadIdx.x == 0) a.row_state[b] = STATE_HEAVY;
-    return;
-  }
-  uint32_t tau = tk;
-  if (rp.p < 1.0f) {
-    unsigned long long local = 0;
-    for (int e = threadIdx.x; e < nk; e += blockDim.x) local += fixed_mass(radix_value((uint32_t)(s.kept[e] >> 32)), m);
-    unsigned long long Z;
-    block_exclusive_scan<unsigned long long>(local, s.wsum64, Z);
-    tau = lds_desc<true>(s.d, s.kept, nk, topp_target(rp.p, Z), m);
-  }
-  // exact Gumbel-max over the survivors
-  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
-  unsigned long long best = 0;
-  for (int e = threadIdx.x; e < nk; e += blockDim.x) {
-    const unsigned long long ce = s.kept[e];
-    const uint32_t kk = (uint32_t)(ce >> 32);
-    if (kk < tau) continue;
-    const uint32_t i = (uint32_t)ce;
-    const float sc = radix_value(kk) + exact_noise(a, b, key, (int)i);
-    best = max_u64(best, argmax_key(sc, i));
-  }
-  best = block_max_u64(best, s.red);
-  if (threadIdx.x == 0) { a.out_ids[b] = (int32_t)(~(uint32_t)best); a.row_state[b] = STATE_DONE; }
 }
 
 // ------------------------------------------------------------------ 3. exact radix fallback
@@ -1653,7 +1615,7 @@ static WsLayout ws_layout(int B, int V) {
   const size_t nc = (size_t)((V + kChunk - 1) / kChunk);
   WsLayout w;
   size_t o = 0;
-  w.lane_tops = o;  o += align_up((size_t)B * nc * (kThreads / 64) * kTops * 4, 256);
+  w.lane_tops = o;  o += align_up((size_t)B * nc * (kThreads / 64) * kTopsPub * 4, 256);
   w.row_key = o;    o += (size_t)B * kRowPad8 * 8;
   w.row_tau = o;    o += align_up((size_t)B * 4, 256);
   w.row_state = o;  o += align_up((size_t)B * 4, 256);
