@@ -43,6 +43,7 @@
 // the fast path's error; the winner is the exact maximum.  Elements (and whole
 // chunks) whose x plus the largest possible draw cannot beat the row's best
 // exact score so far are skipped.
+#include <climits>
 #include "nvjsel_device.h"
 #include "nvjsel_host.h"
 
@@ -88,7 +89,10 @@ struct SampleArgs {
   float* cand_floor;               // [B, nchunks] logit floor of each chunk's candidates
   unsigned long long* cand;        // [B, nchunks, kCandCap]
   float* row_m;                    // [B]   max of x (top-p rows)
-  unsigned long long* topp_hist;   // [B, kToppBins] zero at rest
+  unsigned long long* topp_hist;   // [B, kToppBins] row histogram, bin D = grid bin row_tb - D
+  unsigned long long* topp_chunk_hist;  // [B, nchunks, kToppBins] chunk histograms (top-p-only rows)
+  int32_t* topp_chunk_tb;          // [B, nchunks] grid bin of each chunk's maximum
+  int32_t* row_tb;                 // [B]
   unsigned long long* topp_cand;   // [B, kToppCap]
   uint32_t* topp_n;                // [B]
   uint32_t* list_n;                // [2]   rows queued for gumbel, for top-p
@@ -171,6 +175,18 @@ __device__ __forceinline__ uint64_t fixed_mass(float x, float m) {
   // exp(x - m) in [0, 1], as an integer multiple of 2^-40
   const float e = expf(x - m);
   return (uint64_t)rintf(e * 1099511627776.0f);
+}
+
+// Top-p masses live on a fixed grid of 1/32-nat bins, bin ib = floor(32 x),
+// so that chunks can histogram them before the row maximum is known: an
+// element's weight is exp(x - top edge of its bin) in (0.969, 1], as an
+// integer multiple of 2^-40 (hardware exp2: the same instruction wherever a
+// weight is formed), and bin ib's weights scale by exp(edge - row edge).
+__device__ __forceinline__ int topp_ibin(float x) { return (int)floorf(x * 32.0f); }
+__device__ __forceinline__ float topp_edge(int ib) { return (float)ib * 0.03125f; }
+__device__ __forceinline__ uint64_t edge_mass(float x, int ib) {
+  const float d = x - topp_edge(ib + 1);
+  return (uint64_t)rintf(__builtin_amdgcn_exp2f(d * 1.44269504088896341f) * 1099511627776.0f);
 }
 
 // Block-wide max of a 64-bit key (every thread gets the result).
@@ -584,6 +600,7 @@ struct ScanShared {
   uint32_t wfloor[kThreads / 64];
   float wtop[kThreads / 64];  // each wave's kTops-th largest lane maximum
   uint32_t cnt, cnt_b, waves;
+  unsigned long long topp_h[kToppBins];  // top-p-only rows: the chunk's grid-bin histogram
 };
 
 // Wave-wide max and inclusive prefix sum with DPP row shifts and row
@@ -820,6 +837,9 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   }
   if (lane == 0) { sh.wkey[wave] = wkey; sh.wfloor[wave] = wfloor; }
   if (threadIdx.x == 0) { sh.cnt = 0; sh.cnt_b = 0; sh.waves = 0; }
+  const bool topp_row = a.topk == 0 && rp.mode == ROW_FILTER && rp.k == 0 && rp.p < 1.0f;
+  if (topp_row)
+    for (int d = threadIdx.x; d < kToppBins; d += kThreads) sh.topp_h[d] = 0;
   __syncthreads();
   unsigned long long cbest = sh.wkey[0];
   uint32_t prefix = sh.wfloor[0];
@@ -832,6 +852,33 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
     a.chunk_max[(size_t)b * a.nchunks + c] = cbest;
     if (c == 0) a.row_done[(size_t)b * kRowPad] = 0;
     if (b == 0 && c == 0) { a.list_n[0] = 0; a.list_n[1] = 0; }  // this call's work lists
+  }
+  if (topp_row) {
+    // grid-bin histogram of the chunk's weights over the 32 nats below its
+    // maximum (below that an element's share of the row's mass is < e^-32)
+    const float cx = unord_f32((uint32_t)(cbest >> 32)) / rp.tp;
+    int tb = INT_MIN;
+    if (fabsf(cx) < 0x1p25f) {  // finite and on the grid
+      tb = topp_ibin(cx);
+      const float lowb = topp_edge(tb - (kToppBins - 1));
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        if (!r.vok[q]) continue;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float x = r.elem(q, e) / rp.tp;
+          if (x >= lowb) {
+            const int ib = topp_ibin(x);
+            atomicAdd(&sh.topp_h[tb - ib], (unsigned long long)edge_mass(x, ib));
+          }
+        }
+      }
+    }
+    __syncthreads();
+    unsigned long long* ch = a.topp_chunk_hist + ((size_t)b * a.nchunks + c) * kToppBins;
+    for (int d = threadIdx.x; d < kToppBins; d += kThreads) ch[d] = sh.topp_h[d];
+    if (threadIdx.x == 0) a.topp_chunk_tb[(size_t)b * a.nchunks + c] = tb;
+    return;
   }
   if (!topk) return;
   // a NaN chunk makes the row non-finite: select answers it without candidates
@@ -924,7 +971,7 @@ struct DescShared {
 };
 
 template <bool MASS>
-__device__ uint32_t lds_desc(DescShared& s, const unsigned long long* v, int n, unsigned long long target, float m) {
+__device__ uint32_t lds_desc(DescShared& s, const unsigned long long* v, int n, unsigned long long target, int ibin) {
   // bytes shared by every key need no pass
   uint32_t kmin = 0xFFFFFFFFu, kmax = 0;
   for (int e = threadIdx.x; e < n; e += blockDim.x) {
@@ -953,7 +1000,7 @@ __device__ uint32_t lds_desc(DescShared& s, const unsigned long long* v, int n, 
       const uint32_t kk = (uint32_t)(v[e] >> 32);
       if ((kk & mask) != prefix) continue;
       const int d = (int)((kk >> sh) & 255u);
-      const unsigned long long w = MASS ? (unsigned long long)fixed_mass(radix_value(kk), m) : 1ull;
+      const unsigned long long w = MASS ? (unsigned long long)edge_mass(radix_value(kk), ibin) : 1ull;
       if (d != cur) {
         if (cur >= 0 && acc) atomicAdd(&s.hist[cur], acc);
         cur = d;
@@ -1170,7 +1217,7 @@ __global__ void __launch_bounds__(kThreads) topk_select_kernel(SampleArgs a, flo
   }
   int m = K;  // entries of s.sel to sort
   if (fast) {
-    const uint32_t tk = lds_desc<false>(s.d, s.cand, n, (unsigned long long)K, 0.0f);
+    const uint32_t tk = lds_desc<false>(s.d, s.cand, n, (unsigned long long)K, 0);
     if (threadIdx.x == 0) s.n = 0;
     __syncthreads();
     for (int e = threadIdx.x; e < n; e += blockDim.x) {
@@ -1251,6 +1298,7 @@ __device__ __forceinline__ void queue_chunks(const SampleArgs& a, int b, const R
 
 struct SelectShared {
   unsigned long long red[kThreads / 64];
+  int tb[1024];
   QueueShared q;
   FinishShared fin;
 };
@@ -1307,14 +1355,47 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
   // rest (k > 256, rows whose floor falls below a chunk's tier A, crowded
   // ties) to the exact whole-row path.
   const bool topp_only = rp.k == 0 && rp.p < 1.0f;
-  if (topp_only) {  // the histogram pass accumulates into these
-    for (int d = threadIdx.x; d < kToppBins; d += blockDim.x) a.topp_hist[(size_t)b * kToppBins + d] = 0;
-    if (threadIdx.x == 0) a.topp_n[b] = 0;
+  if (topp_only) {
+    // the row's histogram from the scan's chunk histograms: chunk c's bin d is
+    // grid bin tb_c - d, the row's bin D is grid bin TB - D (TB = max tb_c)
+    int tbm = INT_MIN;
+    for (int c = threadIdx.x; c < NC; c += kThreads) {
+      const int t = a.topp_chunk_tb[(size_t)b * NC + c];
+      s.tb[c] = t;
+      tbm = max(tbm, t);
+    }
+    const int TB = (int)(uint32_t)(block_max_u64((unsigned long long)(uint32_t)(tbm ^ INT_MIN), s.red)) ^ INT_MIN;
+    constexpr int PER = kToppBins / kThreads;
+    constexpr int U = 8;  // chunks whose loads are in flight together
+    unsigned long long h[PER] = {};
+    for (int c0 = 0; c0 < NC; c0 += U) {
+      unsigned long long v[U][PER];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u;
+        const int tbc = c < NC ? s.tb[c] : INT_MIN;
+        const int sft = (tbc == INT_MIN || TB == INT_MIN) ? kToppBins * 2 : TB - tbc;
+        const unsigned long long* ch = a.topp_chunk_hist + ((size_t)b * NC + c) * kToppBins;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+          const int d = (int)threadIdx.x * PER + q - sft;
+          v[u][q] = d >= 0 ? ch[d] : 0ull;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int q = 0; q < PER; ++q) h[q] += v[u][q];
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) a.topp_hist[(size_t)b * kToppBins + threadIdx.x * PER + q] = h[q];
+    if (threadIdx.x == 0) { a.topp_n[b] = 0; a.row_tb[b] = TB; }
   }
   if (threadIdx.x == 0) {
-    a.row_state[b] = topp_only ? STATE_TOPP : STATE_HEAVY;
+    // a row whose chunk histograms are unusable (maxima beyond the grid) is exact-path work
+    a.row_state[b] = topp_only && a.row_tb[b] != INT_MIN ? STATE_TOPP : STATE_HEAVY;
     a.row_m[b] = m;
-    if (topp_only) queue_row(&a.list_n[1], a.list_topp, b);
+    if (topp_only && a.row_tb[b] != INT_MIN) queue_row(&a.list_n[1], a.list_topp, b);
   }
 }
 
@@ -1396,61 +1477,55 @@ __device__ uint32_t radix_descend(const SampleArgs& a, const char* row, float tp
 // then an exact scan of the one bin where the cumulative mass crosses
 // floor(p * Z) + 1.
 
-__device__ __forceinline__ int topp_bin(float x, float m) {
-  const float d = (m - x) * kToppBinScale;
-  return d < (float)(kToppBins - 1) ? (int)d : kToppBins - 1;
-}
-
 struct ToppShared {
-  unsigned long long hist[kToppBins];
-  unsigned long long wsum[kThreads / 64];
-  uint32_t bin, n, base;
+  double wsum[kThreads / 64];
+  unsigned long long red[kThreads / 64];
+  int bin;  // grid bin ib of the crossing, INT_MIN when the window holds no crossing
+  uint32_t n, base;
   unsigned long long target;
 };
 
-template <int DT, int VEC>
-__global__ void __launch_bounds__(kThreads) sample_topp_hist_kernel(SampleArgs a) {
-  __shared__ ToppShared sh;
-  const long long items = (long long)a.list_n[1] * a.nchunks;
-  for (long long it = blockIdx.x; it < items; it += gridDim.x) {
-    const int b = (int)a.list_topp[it / a.nchunks], c = (int)(it % a.nchunks);
-    const RowParams rp = row_params(a, b);
-    const float m = a.row_m[b];
-    __syncthreads();
-    for (int d = threadIdx.x; d < kToppBins; d += kThreads) sh.hist[d] = 0;
-    __syncthreads();
-    float x[kEPT];
-    uint32_t valid;
-    load_chunk_elems<DT, VEC, kEPT>(row_ptr(a, b), c * kChunk, a.V, false, rp.tp, x, valid);
-#pragma unroll
-    for (int j = 0; j < kEPT; ++j) {
-      if (!((valid >> j) & 1u)) continue;
-      const uint64_t w = fixed_mass(x[j], m);
-      if (w) atomicAdd(&sh.hist[topp_bin(x[j], m)], (unsigned long long)w);
-    }
-    __syncthreads();
-    unsigned long long* gh = a.topp_hist + (size_t)b * kToppBins;
-    for (int d = threadIdx.x; d < kToppBins; d += kThreads)
-      if (sh.hist[d]) atomicAdd(&gh[d], sh.hist[d]);
-  }
-}
-
-// Crossing bin of the row's histogram and the mass still needed inside it.
-__device__ __forceinline__ void topp_crossing(const unsigned long long* gh, float p, ToppShared& sh) {
+// Crossing bin of the row's histogram (bin D holds grid bin TB - D, TB the
+// row's top bin) and the weight still needed inside it: bins are summed in
+// fp64 with their scales exp(-D / 32), the crossing is the first bin whose
+// cumulative mass exceeds p * Z, and the elements of that bin must reach
+// floor((p * Z - mass above) / scale) + 1 of its integer weight units.
+__device__ __forceinline__ void topp_crossing(const unsigned long long* gh, int tb, float p, ToppShared& sh) {
   constexpr int PER = kToppBins / kThreads;
-  unsigned long long h[PER], local = 0;
-#pragma unroll
-  for (int q = 0; q < PER; ++q) { h[q] = gh[threadIdx.x * PER + q]; local += h[q]; }
-  unsigned long long Z;
-  unsigned long long cum = block_exclusive_scan<unsigned long long>(local, sh.wsum, Z);
-  const unsigned long long target = topp_target(p, Z);
+  double mq[PER], sc[PER], local = 0.0;
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
-    if (cum < target && target <= cum + h[q]) {
-      sh.bin = (uint32_t)(threadIdx.x * PER + q);
-      sh.target = target - cum;
+    const int D = threadIdx.x * PER + q;
+    sc[q] = exp2(-(double)D * (1.4426950408889634 / 32.0)) * 0x1p-40;
+    mq[q] = (double)gh[D] * sc[q];
+    local += mq[q];
+  }
+  // exclusive block scan in thread order
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  double incl = local;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const double o = __longlong_as_double(__shfl_up(__double_as_longlong(incl), d, 64));
+    if (lane >= d) incl += o;
+  }
+  if (threadIdx.x == 0) sh.bin = INT_MIN;
+  __syncthreads();
+  if (lane == 63) sh.wsum[wave] = incl;
+  __syncthreads();
+  double before = 0.0, Z = 0.0;
+  for (int w = 0; w < kThreads / 64; ++w) {
+    if (w < wave) before += sh.wsum[w];
+    Z += sh.wsum[w];
+  }
+  const double pz = (double)p * Z;
+  double cum = before + incl - local;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    if (cum <= pz && pz < cum + mq[q]) {
+      sh.bin = tb - (threadIdx.x * PER + q);
+      sh.target = (unsigned long long)floor((pz - cum) / sc[q]) + 1ull;
     }
-    cum += h[q];
+    cum += mq[q];
   }
   __syncthreads();
 }
@@ -1462,10 +1537,11 @@ __global__ void __launch_bounds__(kThreads) sample_topp_collect_kernel(SampleArg
   for (long long it = blockIdx.x; it < items; it += gridDim.x) {
     const int b = (int)a.list_topp[it / a.nchunks], c = (int)(it % a.nchunks);
     const RowParams rp = row_params(a, b);
-    const float m = a.row_m[b];
     __syncthreads();
-    topp_crossing(a.topp_hist + (size_t)b * kToppBins, rp.p, sh);
-    const int bin = (int)sh.bin;
+    topp_crossing(a.topp_hist + (size_t)b * kToppBins, a.row_tb[b], rp.p, sh);
+    const int ib = sh.bin;
+    if (ib == INT_MIN) continue;  // (block-uniform) the finalize kernel takes the exact path
+    const float lo = topp_edge(ib), hi = topp_edge(ib + 1);
     float x[kEPT];
     uint32_t valid;
     const int base = c * kChunk;
@@ -1473,7 +1549,7 @@ __global__ void __launch_bounds__(kThreads) sample_topp_collect_kernel(SampleArg
     uint32_t in_bin = 0;
 #pragma unroll
     for (int j = 0; j < kEPT; ++j)
-      in_bin |= (((valid >> j) & 1u) && topp_bin(x[j], m) == bin ? 1u : 0u) << j;
+      in_bin |= (((valid >> j) & 1u) && x[j] >= lo && x[j] < hi ? 1u : 0u) << j;
     // one global reservation per block: the row's counter is shared by all chunks
     if (threadIdx.x == 0) sh.n = 0;
     __syncthreads();
@@ -1522,15 +1598,16 @@ __global__ void __launch_bounds__(kThreads) sample_finalize_kernel(SampleArgs a)
   const float m = a.row_m[b];
   uint32_t tau = 0;
   if (state == STATE_TOPP) {
-    topp_crossing(a.topp_hist + (size_t)b * kToppBins, rp.p, sh.tf.t);
+    topp_crossing(a.topp_hist + (size_t)b * kToppBins, a.row_tb[b], rp.p, sh.tf.t);
     const unsigned long long target = sh.tf.t.target;
+    const int ib = sh.tf.t.bin;
     const uint32_t n = a.topp_n[b];
-    if (n > (uint32_t)kToppCap) {
+    if (ib == INT_MIN || n > (uint32_t)kToppCap) {
       state = STATE_HEAVY;  // crossing bin too crowded: exact radix path
     } else {
       for (int e = threadIdx.x; e < (int)n; e += kThreads) sh.tf.v[e] = a.topp_cand[(size_t)b * kToppCap + e];
       __syncthreads();
-      tau = lds_desc<true>(sh.tf.d, sh.tf.v, (int)n, target, m);
+      tau = lds_desc<true>(sh.tf.d, sh.tf.v, (int)n, target, ib);
     }
   }
   if (state == STATE_HEAVY) {
@@ -1551,7 +1628,7 @@ __global__ void __launch_bounds__(kThreads) sample_finalize_kernel(SampleArgs a)
     best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
   }
   __syncthreads();
-  best = block_max_u64(best, sh.tf.t.wsum);
+  best = block_max_u64(best, sh.tf.t.red);
   if (threadIdx.x == 0) {
     a.row_key[(size_t)b * kRowPad8] = best;
     a.row_tau[b] = tau;
@@ -1607,7 +1684,7 @@ __global__ void __launch_bounds__(kThreads) sample_gumbel_kernel(SampleArgs a) {
 }
 
 struct WsLayout {
-  size_t lane_tops, row_key, row_tau, row_state, chunk_max, cand_count, cand_count_a, cand_floor_a, cand_floor, cand, row_m, topp_hist, topp_cand, topp_n;
+  size_t lane_tops, topp_chunk_hist, topp_chunk_tb, row_tb, row_key, row_tau, row_state, chunk_max, cand_count, cand_count_a, cand_floor_a, cand_floor, cand, row_m, topp_hist, topp_cand, topp_n;
   size_t list_n, list_gumbel, list_topp, row_done, row_items, total;
 };
 
@@ -1616,6 +1693,9 @@ static WsLayout ws_layout(int B, int V) {
   WsLayout w;
   size_t o = 0;
   w.lane_tops = o;  o += align_up((size_t)B * nc * (kThreads / 64) * kTopsPub * 4, 256);
+  w.topp_chunk_hist = o; o += align_up((size_t)B * nc * kToppBins * 8, 256);
+  w.topp_chunk_tb = o;   o += align_up((size_t)B * nc * 4, 256);
+  w.row_tb = o;          o += align_up((size_t)B * 4, 256);
   w.row_key = o;    o += (size_t)B * kRowPad8 * 8;
   w.row_tau = o;    o += align_up((size_t)B * 4, 256);
   w.row_state = o;  o += align_up((size_t)B * 4, 256);
@@ -1654,6 +1734,9 @@ static SampleArgs make_args(const void* logits, int dtype, int batch, int vocab,
   a.nchunks = (vocab + kChunk - 1) / kChunk;
   a.stride = row_stride;
   a.lane_tops = (float*)(ws + w.lane_tops);
+  a.topp_chunk_hist = (unsigned long long*)(ws + w.topp_chunk_hist);
+  a.topp_chunk_tb = (int32_t*)(ws + w.topp_chunk_tb);
+  a.row_tb = (int32_t*)(ws + w.row_tb);
   a.row_key = (unsigned long long*)(ws + w.row_key);
   a.row_tau = (uint32_t*)(ws + w.row_tau);
   a.row_state = (int32_t*)(ws + w.row_state);
@@ -1734,7 +1817,6 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   const dim3 grid_rows_chunks((unsigned)((long long)batch * a.nchunks));
   const dim3 grid_items((unsigned)((long long)batch * a.nchunks * kGumbelSplit));
   if (top_p) {
-    NVJSEL_LAUNCH_CHUNK(sample_topp_hist_kernel, grid_rows_chunks);
     NVJSEL_LAUNCH_CHUNK(sample_topp_collect_kernel, grid_rows_chunks);
   }
   if (top_k || top_p) {
