@@ -88,18 +88,16 @@ struct SampleArgs {
   float* cand_floor_a;             // [B, nchunks]
   float* cand_floor;               // [B, nchunks] logit floor of each chunk's candidates
   unsigned long long* cand;        // [B, nchunks, kCandCap]
-  float* row_m;                    // [B]   max of x (top-p rows)
-  unsigned long long* topp_hist;   // [B, kToppBins] row histogram, bin D = grid bin row_tb - D
   unsigned long long* topp_chunk_hist;  // [B, nchunks, kToppBins] chunk histograms (top-p-only rows)
   int32_t* topp_chunk_tb;          // [B, nchunks] grid bin of each chunk's maximum
-  int32_t* row_tb;                 // [B]
+  int32_t* row_ib;                 // [B] top-p rows: grid bin of the crossing (INT_MIN: none)
+  unsigned long long* row_target;  // [B] top-p rows: weight units needed inside the crossing bin
   unsigned long long* topp_cand;   // [B, kToppCap]
   uint32_t* topp_n;                // [B]
   uint32_t* list_n;                // [2]   rows queued for gumbel, for top-p
   uint32_t* list_gumbel;           // [B * nchunks] gumbel items: row << 16 | chunk
   uint32_t* row_done;              // [B * kRowPad] gumbel items finished per row
   uint32_t* row_items;             // [B * kRowPad] gumbel items queued per row
-  uint32_t* list_topp;             // [B]
   int32_t* out_ids;
   float* lane_tops;                // [B, nchunks, 4 waves, kTopsPub] largest raw-logit lane maxima
   int topk;  // > 0: top-k selection (nvjsel_topk): every row FILTER with this k on raw logits
@@ -851,7 +849,7 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   if (threadIdx.x == 0) {
     a.chunk_max[(size_t)b * a.nchunks + c] = cbest;
     if (c == 0) a.row_done[(size_t)b * kRowPad] = 0;
-    if (b == 0 && c == 0) { a.list_n[0] = 0; a.list_n[1] = 0; }  // this call's work lists
+    if (b == 0 && c == 0) a.list_n[0] = 0;  // this call's work list
   }
   if (topp_row) {
     // grid-bin histogram of the chunk's weights over the 32 nats below its
@@ -1267,9 +1265,9 @@ struct QueueShared {
 // test.  A row left with no item (it cannot happen: the seed's own chunk
 // qualifies) is answered with the seed.
 __device__ __forceinline__ void queue_chunks(const SampleArgs& a, int b, const RowParams& rp, uint32_t tau,
-                                             unsigned long long best, QueueShared& q) {
+                                             unsigned long long best, QueueShared& q, bool prune = true) {
   const int NC = a.nchunks;
-  const float s_seed = prune_level(best);
+  const float s_seed = prune ? prune_level(best) : -INFINITY;
   auto keep = [&](int c) {
     if (c >= NC) return false;
     const float xv = chunk_max_x(rp, a.chunk_max[(size_t)b * NC + c]);
@@ -1293,109 +1291,6 @@ __device__ __forceinline__ void queue_chunks(const SampleArgs& a, int b, const R
     const uint32_t off = block_exclusive_scan<uint32_t>(k ? 1u : 0u, q.wsum, n);
     if (k) a.list_gumbel[pos + off] = ((uint32_t)b << 16) | (uint32_t)c;
     pos += n;
-  }
-}
-
-struct SelectShared {
-  unsigned long long red[kThreads / 64];
-  int tb[1024];
-  QueueShared q;
-  FinishShared fin;
-};
-
-__global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
-  __shared__ SelectShared s;
-  const int b = blockIdx.x;
-  const RowParams rp = row_params(a, b);
-  const int NC = a.nchunks;
-  if (rp.mode == ROW_FULL) {
-    // seed the row's best with the exact scores of the chunk maxima: a prune
-    // level for the gumbel kernel before any of its blocks has run
-    const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
-    unsigned long long best = 0;
-    for (int c = threadIdx.x; c < NC; c += blockDim.x) {
-      const unsigned long long ck = a.chunk_max[(size_t)b * NC + c];
-      const uint32_t i = ~(uint32_t)ck;
-      const float xv = chunk_max_x(rp, ck);
-      best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
-    }
-    best = block_max_u64(best, s.red);
-    if (threadIdx.x == 0) a.row_key[(size_t)b * kRowPad8] = best;
-    queue_chunks(a, b, rp, 0u, best, s.q);
-    return;
-  }
-  unsigned long long mk = 0;
-  for (int c = threadIdx.x; c < NC; c += blockDim.x) mk = max_u64(mk, a.chunk_max[(size_t)b * NC + c]);
-  mk = block_max_u64(mk, s.red);
-  if (rp.mode == ROW_GREEDY) {  // the row's first maximum
-    if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)mk);
-    return;
-  }
-  const float ml = unord_f32((uint32_t)(mk >> 32));
-  const float m = ml / rp.tp;
-  if (!isfinite(m)) {  // NaN / +inf / all -inf: the first maximum is the answer
-    unsigned long long ans = mk;
-    if (m > 0.0f && ml == ml) {
-      // x = +inf: finite logits may overflow to +inf too, so find the first
-      // index whose x is +inf (T' is tiny and the logits huge; never hot)
-      const char* row = row_ptr(a, b);
-      unsigned long long first = 0;
-      for (int i = threadIdx.x; i < a.V; i += blockDim.x)
-        if (load_logit(a, row, i) / rp.tp == INFINITY) first = max_u64(first, argmax_key(INFINITY, (uint32_t)i));
-      ans = block_max_u64(first, s.red);
-    }
-    if (threadIdx.x == 0) { a.out_ids[b] = (int32_t)(~(uint32_t)ans); a.row_state[b] = STATE_DONE; }
-    return;
-  }
-  if (rp.k > 0 && rp.k <= kFastK && finish_topk_row(a, b, rp, m, s.fin)) {
-    if (threadIdx.x == 0) a.row_state[b] = STATE_DONE;
-    return;
-  }
-  // Every other FILTER row: top-p-only rows go to the histogram passes, the
-  // rest (k > 256, rows whose floor falls below a chunk's tier A, crowded
-  // ties) to the exact whole-row path.
-  const bool topp_only = rp.k == 0 && rp.p < 1.0f;
-  if (topp_only) {
-    // the row's histogram from the scan's chunk histograms: chunk c's bin d is
-    // grid bin tb_c - d, the row's bin D is grid bin TB - D (TB = max tb_c)
-    int tbm = INT_MIN;
-    for (int c = threadIdx.x; c < NC; c += kThreads) {
-      const int t = a.topp_chunk_tb[(size_t)b * NC + c];
-      s.tb[c] = t;
-      tbm = max(tbm, t);
-    }
-    const int TB = (int)(uint32_t)(block_max_u64((unsigned long long)(uint32_t)(tbm ^ INT_MIN), s.red)) ^ INT_MIN;
-    constexpr int PER = kToppBins / kThreads;
-    constexpr int U = 8;  // chunks whose loads are in flight together
-    unsigned long long h[PER] = {};
-    for (int c0 = 0; c0 < NC; c0 += U) {
-      unsigned long long v[U][PER];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int c = c0 + u;
-        const int tbc = c < NC ? s.tb[c] : INT_MIN;
-        const int sft = (tbc == INT_MIN || TB == INT_MIN) ? kToppBins * 2 : TB - tbc;
-        const unsigned long long* ch = a.topp_chunk_hist + ((size_t)b * NC + c) * kToppBins;
-#pragma unroll
-        for (int q = 0; q < PER; ++q) {
-          const int d = (int)threadIdx.x * PER + q - sft;
-          v[u][q] = d >= 0 ? ch[d] : 0ull;
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int q = 0; q < PER; ++q) h[q] += v[u][q];
-    }
-#pragma unroll
-    for (int q = 0; q < PER; ++q) a.topp_hist[(size_t)b * kToppBins + threadIdx.x * PER + q] = h[q];
-    if (threadIdx.x == 0) { a.topp_n[b] = 0; a.row_tb[b] = TB; }
-  }
-  if (threadIdx.x == 0) {
-    // a row whose chunk histograms are unusable (maxima beyond the grid) is exact-path work
-    a.row_state[b] = topp_only && a.row_tb[b] != INT_MIN ? STATE_TOPP : STATE_HEAVY;
-    a.row_m[b] = m;
-    if (topp_only && a.row_tb[b] != INT_MIN) queue_row(&a.list_n[1], a.list_topp, b);
   }
 }
 
@@ -1472,32 +1367,30 @@ __device__ uint32_t radix_descend(const SampleArgs& a, const char* row, float tp
 }
 
 // ------------------------------------------------------------------ 2b. top-p rows (no top-k)
-// mass(x >= v) is found in two steps: a histogram of masses over 1/32-nat
-// bins below the row max (bins are monotone in x, equal values share a bin),
-// then an exact scan of the one bin where the cumulative mass crosses
-// floor(p * Z) + 1.
+// The row's histogram over grid bins (merged by select from the scan's chunk
+// histograms) gives the crossing bin; the gumbel pass then scores the
+// elements above it and collects the elements inside it; the finish kernel
+// finds the exact threshold among those and settles the row.
 
-struct ToppShared {
+struct ToppXShared {
   double wsum[kThreads / 64];
-  unsigned long long red[kThreads / 64];
   int bin;  // grid bin ib of the crossing, INT_MIN when the window holds no crossing
-  uint32_t n, base;
   unsigned long long target;
 };
 
-// Crossing bin of the row's histogram (bin D holds grid bin TB - D, TB the
-// row's top bin) and the weight still needed inside it: bins are summed in
-// fp64 with their scales exp(-D / 32), the crossing is the first bin whose
+// Crossing bin of a row histogram held as h[q] = bin D = PER * t + q of thread
+// t (grid bin TB - D) and the weight still needed inside it: bins are summed
+// in fp64 with their scales exp(-D / 32), the crossing is the first bin whose
 // cumulative mass exceeds p * Z, and the elements of that bin must reach
 // floor((p * Z - mass above) / scale) + 1 of its integer weight units.
-__device__ __forceinline__ void topp_crossing(const unsigned long long* gh, int tb, float p, ToppShared& sh) {
-  constexpr int PER = kToppBins / kThreads;
+template <int PER>
+__device__ __forceinline__ void topp_crossing(const unsigned long long (&h)[PER], int tb, float p, ToppXShared& sh) {
   double mq[PER], sc[PER], local = 0.0;
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const int D = threadIdx.x * PER + q;
     sc[q] = exp2(-(double)D * (1.4426950408889634 / 32.0)) * 0x1p-40;
-    mq[q] = (double)gh[D] * sc[q];
+    mq[q] = (double)h[q] * sc[q];
     local += mq[q];
   }
   // exclusive block scan in thread order
@@ -1530,111 +1423,142 @@ __device__ __forceinline__ void topp_crossing(const unsigned long long* gh, int 
   __syncthreads();
 }
 
-template <int DT, int VEC>
-__global__ void __launch_bounds__(kThreads) sample_topp_collect_kernel(SampleArgs a) {
-  __shared__ ToppShared sh;
-  const long long items = (long long)a.list_n[1] * a.nchunks;
-  for (long long it = blockIdx.x; it < items; it += gridDim.x) {
-    const int b = (int)a.list_topp[it / a.nchunks], c = (int)(it % a.nchunks);
-    const RowParams rp = row_params(a, b);
-    __syncthreads();
-    topp_crossing(a.topp_hist + (size_t)b * kToppBins, a.row_tb[b], rp.p, sh);
-    const int ib = sh.bin;
-    if (ib == INT_MIN) continue;  // (block-uniform) the finalize kernel takes the exact path
-    const float lo = topp_edge(ib), hi = topp_edge(ib + 1);
-    float x[kEPT];
-    uint32_t valid;
-    const int base = c * kChunk;
-    load_chunk_elems<DT, VEC, kEPT>(row_ptr(a, b), base, a.V, false, rp.tp, x, valid);
-    uint32_t in_bin = 0;
-#pragma unroll
-    for (int j = 0; j < kEPT; ++j)
-      in_bin |= (((valid >> j) & 1u) && x[j] >= lo && x[j] < hi ? 1u : 0u) << j;
-    // one global reservation per block: the row's counter is shared by all chunks
-    if (threadIdx.x == 0) sh.n = 0;
-    __syncthreads();
-    const uint32_t mine = __popc(in_bin);
-    const uint32_t off = mine ? atomicAdd(&sh.n, mine) : 0u;
-    __syncthreads();
-    if (threadIdx.x == 0) sh.base = sh.n ? atomicAdd(&a.topp_n[b], sh.n) : 0u;
-    __syncthreads();
-    uint32_t slot = sh.base + off;
-#pragma unroll
-    for (int j = 0; j < kEPT; ++j) {
-      if (!((in_bin >> j) & 1u)) continue;
-      if (slot < (uint32_t)kToppCap)
-        a.topp_cand[(size_t)b * kToppCap + slot] =
-            ((unsigned long long)radix_key(x[j]) << 32) | (uint32_t)elem_index<VEC>(base, j);
-      ++slot;
-    }
-  }
-}
-
-struct ToppFinalShared {
-  ToppShared t;
-  DescShared d;
-  unsigned long long v[kToppCap];
-};
-
-struct FinalizeShared {
+struct SelectShared {
+  unsigned long long red[kThreads / 64];
+  int tb[1024];
+  QueueShared q;
+  ToppXShared tx;
   union {
-    ToppFinalShared tf;
+    FinishShared fin;
     HeavyShared hv;
   };
-  QueueShared q;
 };
 
-// Rows left by select: top-p-only rows (crossing bin of the histogram ->
-// exact threshold) and rows for the exact radix fallback.  Each ends with its
-// threshold, its best score seeded from the kept chunk maxima, and a place in
-// the gumbel queue.
-__global__ void __launch_bounds__(kThreads) sample_finalize_kernel(SampleArgs a) {
-  __shared__ FinalizeShared sh;
+__global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
+  __shared__ SelectShared s;
   const int b = blockIdx.x;
   const RowParams rp = row_params(a, b);
-  if (rp.mode != ROW_FILTER) return;
-  int state = a.row_state[b];
-  if (state != STATE_TOPP && state != STATE_HEAVY) return;
-  const float m = a.row_m[b];
-  uint32_t tau = 0;
-  if (state == STATE_TOPP) {
-    topp_crossing(a.topp_hist + (size_t)b * kToppBins, a.row_tb[b], rp.p, sh.tf.t);
-    const unsigned long long target = sh.tf.t.target;
-    const int ib = sh.tf.t.bin;
-    const uint32_t n = a.topp_n[b];
-    if (ib == INT_MIN || n > (uint32_t)kToppCap) {
-      state = STATE_HEAVY;  // crossing bin too crowded: exact radix path
-    } else {
-      for (int e = threadIdx.x; e < (int)n; e += kThreads) sh.tf.v[e] = a.topp_cand[(size_t)b * kToppCap + e];
-      __syncthreads();
-      tau = lds_desc<true>(sh.tf.d, sh.tf.v, (int)n, target, ib);
+  const int NC = a.nchunks;
+  if (rp.mode == ROW_FULL) {
+    // seed the row's best with the exact scores of the chunk maxima: a prune
+    // level for the gumbel kernel before any of its blocks has run
+    const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+    unsigned long long best = 0;
+    for (int c = threadIdx.x; c < NC; c += blockDim.x) {
+      const unsigned long long ck = a.chunk_max[(size_t)b * NC + c];
+      const uint32_t i = ~(uint32_t)ck;
+      const float xv = chunk_max_x(rp, ck);
+      best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
     }
+    best = block_max_u64(best, s.red);
+    if (threadIdx.x == 0) {
+      a.row_key[(size_t)b * kRowPad8] = best;
+      a.row_ib[b] = INT_MIN;
+      a.row_state[b] = STATE_NEEDS_GUMBEL;
+    }
+    queue_chunks(a, b, rp, 0u, best, s.q);
+    return;
   }
-  if (state == STATE_HEAVY) {
+  unsigned long long mk = 0;
+  for (int c = threadIdx.x; c < NC; c += blockDim.x) mk = max_u64(mk, a.chunk_max[(size_t)b * NC + c]);
+  mk = block_max_u64(mk, s.red);
+  if (rp.mode == ROW_GREEDY) {  // the row's first maximum
+    if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)mk);
+    return;
+  }
+  const float ml = unord_f32((uint32_t)(mk >> 32));
+  const float m = ml / rp.tp;
+  if (!isfinite(m)) {  // NaN / +inf / all -inf: the first maximum is the answer
+    unsigned long long ans = mk;
+    if (m > 0.0f && ml == ml) {
+      // x = +inf: finite logits may overflow to +inf too, so find the first
+      // index whose x is +inf (T' is tiny and the logits huge; never hot)
+      const char* row = row_ptr(a, b);
+      unsigned long long first = 0;
+      for (int i = threadIdx.x; i < a.V; i += blockDim.x)
+        if (load_logit(a, row, i) / rp.tp == INFINITY) first = max_u64(first, argmax_key(INFINITY, (uint32_t)i));
+      ans = block_max_u64(first, s.red);
+    }
+    if (threadIdx.x == 0) { a.out_ids[b] = (int32_t)(~(uint32_t)ans); a.row_state[b] = STATE_DONE; }
+    return;
+  }
+  if (rp.k > 0 && rp.k <= kFastK && finish_topk_row(a, b, rp, m, s.fin)) {
+    if (threadIdx.x == 0) a.row_state[b] = STATE_DONE;
+    return;
+  }
+  // Every other FILTER row.  Top-p-only rows: crossing bin from the merged
+  // histogram, the gumbel pass scores the elements above the bin and collects
+  // the bin.  The rest (k > 256, rows whose floor falls below a chunk's tier A,
+  // crowded ties, top-p rows without a usable histogram): exact threshold by a
+  // whole-row radix descent here, then the gumbel pass over x >= threshold.
+  const bool topp_only = rp.k == 0 && rp.p < 1.0f;
+  int ib = INT_MIN;
+  if (topp_only) {
+    // the row's histogram from the scan's chunk histograms: chunk c's bin d is
+    // grid bin tb_c - d, the row's bin D is grid bin TB - D (TB = max tb_c)
+    int tbm = INT_MIN;
+    for (int c = threadIdx.x; c < NC; c += kThreads) {
+      const int t = a.topp_chunk_tb[(size_t)b * NC + c];
+      s.tb[c] = t;
+      tbm = max(tbm, t);
+    }
+    const int TB = (int)(uint32_t)(block_max_u64((unsigned long long)(uint32_t)(tbm ^ INT_MIN), s.red)) ^ INT_MIN;
+    constexpr int PER = kToppBins / kThreads;
+    constexpr int U = 8;  // chunks whose loads are in flight together
+    unsigned long long h[PER] = {};
+    for (int c0 = 0; c0 < NC; c0 += U) {
+      unsigned long long v[U][PER];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u;
+        const int tbc = c < NC ? s.tb[c] : INT_MIN;
+        const int sft = (tbc == INT_MIN || TB == INT_MIN) ? kToppBins * 2 : TB - tbc;
+        const unsigned long long* ch = a.topp_chunk_hist + ((size_t)b * NC + c) * kToppBins;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+          const int d = (int)threadIdx.x * PER + q - sft;
+          v[u][q] = d >= 0 ? ch[d] : 0ull;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int q = 0; q < PER; ++q) h[q] += v[u][q];
+    }
+    if (TB != INT_MIN) topp_crossing<PER>(h, TB, rp.p, s.tx);
+    ib = TB != INT_MIN ? s.tx.bin : INT_MIN;
+  }
+  uint32_t tau;
+  if (ib != INT_MIN) {
+    tau = radix_key(topp_edge(ib + 1));  // the gumbel pass scores x above the crossing bin
+  } else {
     __syncthreads();
     const char* row = row_ptr(a, b);
     tau = 0;
-    if (rp.k > 0) tau = radix_descend<false>(a, row, rp.tp, m, 0u, (unsigned long long)rp.k, 1.0f, sh.hv);
-    if (rp.p < 1.0f) tau = radix_descend<true>(a, row, rp.tp, m, tau, 1ull, rp.p, sh.hv);
+    if (rp.k > 0) tau = radix_descend<false>(a, row, rp.tp, m, 0u, (unsigned long long)rp.k, 1.0f, s.hv);
+    if (rp.p < 1.0f) tau = radix_descend<true>(a, row, rp.tp, m, tau, 1ull, rp.p, s.hv);
   }
-  // seed the row's best with the exact scores of the kept chunk maxima
+  // seed the row's best with the exact scores of the chunk maxima >= tau
   const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
   unsigned long long best = 0;
-  for (int c = threadIdx.x; c < a.nchunks; c += kThreads) {
-    const unsigned long long ck = a.chunk_max[(size_t)b * a.nchunks + c];
+  for (int c = threadIdx.x; c < NC; c += kThreads) {
+    const unsigned long long ck = a.chunk_max[(size_t)b * NC + c];
     const float xv = chunk_max_x(rp, ck);
     if (radix_key(xv) < tau) continue;
     const uint32_t i = ~(uint32_t)ck;
     best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
   }
-  __syncthreads();
-  best = block_max_u64(best, sh.tf.t.red);
+  best = block_max_u64(best, s.red);
   if (threadIdx.x == 0) {
     a.row_key[(size_t)b * kRowPad8] = best;
     a.row_tau[b] = tau;
-    a.row_state[b] = STATE_NEEDS_GUMBEL;
+    a.row_ib[b] = ib;
+    a.row_state[b] = ib != INT_MIN ? STATE_TOPP : STATE_NEEDS_GUMBEL;
+    if (ib != INT_MIN) { a.row_target[b] = s.tx.target; a.topp_n[b] = 0; }
   }
-  queue_chunks(a, b, rp, tau, best, sh.q);
+  // top-p rows queue every chunk reaching the crossing bin (its elements are collected)
+  if (ib != INT_MIN) queue_chunks(a, b, rp, radix_key(topp_edge(ib)), best, s.q, false);
+  else queue_chunks(a, b, rp, tau, best, s.q);
 }
 
 // ------------------------------------------------------------------ 4. gumbel over kept (heavy rows)
@@ -1651,6 +1575,7 @@ __device__ __forceinline__ void gumbel_item(const SampleArgs& a, uint32_t item, 
   uint32_t valid;
   load_chunk_elems<DT, VEC, kGumbelEPT>(row, base, a.V, true, 1.0f, x, valid);
   const uint32_t tau = rp.mode == ROW_FILTER ? a.row_tau[b] : 0u;
+  const int ib = a.row_ib[b];
   const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
   // the row's current best (other blocks keep raising it); read per wave
   unsigned long long* rk = &a.row_key[(size_t)b * kRowPad8];
@@ -1661,6 +1586,25 @@ __device__ __forceinline__ void gumbel_item(const SampleArgs& a, uint32_t item, 
   for (int j = 0; j < kGumbelEPT; ++j) {
     x[j] = x[j] / rp.tp;
     act |= (((valid >> j) & 1u) && radix_key(x[j]) >= tau ? 1u : 0u) << j;
+  }
+  if (ib != INT_MIN) {  // (block-uniform) top-p row: collect the crossing bin
+    const float lo = topp_edge(ib), hi = topp_edge(ib + 1);
+    uint32_t in_bin = 0;
+#pragma unroll
+    for (int j = 0; j < kGumbelEPT; ++j) in_bin |= (((valid >> j) & 1u) && x[j] >= lo && x[j] < hi ? 1u : 0u) << j;
+    uint32_t n;
+    uint32_t pos = block_exclusive_scan<uint32_t>((uint32_t)__popc(in_bin), sh.wsum, n);
+    if (threadIdx.x == 0) sh.n = n ? atomicAdd(&a.topp_n[b], n) : 0u;  // one reservation per block
+    __syncthreads();
+    pos += sh.n;
+#pragma unroll
+    for (int j = 0; j < kGumbelEPT; ++j)
+      if ((in_bin >> j) & 1u) {
+        if (pos < (uint32_t)kToppCap)
+          a.topp_cand[(size_t)b * kToppCap + pos] =
+              ((unsigned long long)radix_key(x[j]) << 32) | (uint32_t)elem_index<VEC>(base, j);
+        ++pos;
+      }
   }
   const unsigned long long best = block_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, act, s_cur, sh);
   // The row's last item writes its id.  A block whose best does not exceed
@@ -1683,9 +1627,66 @@ __global__ void __launch_bounds__(kThreads) sample_gumbel_kernel(SampleArgs a) {
   gumbel_item<DT, VEC>(a, a.list_gumbel[it], (int)(blockIdx.x % kGumbelSplit), sh);
 }
 
+// ------------------------------------------------------------------ 5. top-p rows: finish
+// After the gumbel pass: the exact threshold tau inside the crossing bin (the
+// largest key whose weight from the top of the bin reaches the row's target),
+// then the best of the row's score above the bin (the gumbel pass's result)
+// and the exact scores of the collected bin elements >= tau.  A bin too
+// crowded for LDS takes an exact whole-row descent and a rescan of the bin.
+struct ToppFinishShared {
+  DescShared d;
+  unsigned long long red[kThreads / 64];
+  union {
+    unsigned long long v[kToppCap];
+    HeavyShared hv;
+  };
+};
+
+__global__ void __launch_bounds__(kThreads) sample_topp_finish_kernel(SampleArgs a) {
+  __shared__ ToppFinishShared sh;
+  const int b = blockIdx.x;
+  const RowParams rp = row_params(a, b);
+  if (rp.mode != ROW_FILTER || rp.k != 0 || a.row_state[b] != STATE_TOPP) return;
+  const int ib = a.row_ib[b];
+  const uint32_t n = a.topp_n[b];
+  unsigned long long* rk = &a.row_key[(size_t)b * kRowPad8];
+  const unsigned long long above = load_row_best(rk);
+  const float s_cur = prune_level(above);
+  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+  const float lo = topp_edge(ib), hi = topp_edge(ib + 1);
+  unsigned long long best = 0;
+  if (n <= (uint32_t)kToppCap) {
+    for (int e = threadIdx.x; e < (int)n; e += kThreads) sh.v[e] = a.topp_cand[(size_t)b * kToppCap + e];
+    __syncthreads();
+    const uint32_t tau = lds_desc<true>(sh.d, sh.v, (int)n, a.row_target[b], ib);
+    for (int e = threadIdx.x; e < (int)n; e += kThreads) {
+      const unsigned long long ce = sh.v[e];
+      const uint32_t kk = (uint32_t)(ce >> 32);
+      const float xv = radix_value(kk);
+      if (kk < tau || xv + NVJSEL_GUMBEL_MAX < s_cur) continue;
+      const uint32_t i = (uint32_t)ce;
+      best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
+    }
+  } else {
+    unsigned long long mk = 0;
+    for (int c = threadIdx.x; c < a.nchunks; c += kThreads) mk = max_u64(mk, a.chunk_max[(size_t)b * a.nchunks + c]);
+    mk = block_max_u64(mk, sh.red);
+    const float m = chunk_max_x(rp, mk);
+    const char* row = row_ptr(a, b);
+    const uint32_t tau = radix_descend<true>(a, row, rp.tp, m, 0u, 1ull, rp.p, sh.hv);
+    for (int i = threadIdx.x; i < a.V; i += kThreads) {
+      const float xv = load_logit(a, row, i) / rp.tp;
+      if (!(xv >= lo && xv < hi) || radix_key(xv) < tau || xv + NVJSEL_GUMBEL_MAX < s_cur) continue;
+      best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, i), (uint32_t)i));
+    }
+  }
+  best = max_u64(block_max_u64(best, sh.red), above);
+  if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)best);
+}
+
 struct WsLayout {
-  size_t lane_tops, topp_chunk_hist, topp_chunk_tb, row_tb, row_key, row_tau, row_state, chunk_max, cand_count, cand_count_a, cand_floor_a, cand_floor, cand, row_m, topp_hist, topp_cand, topp_n;
-  size_t list_n, list_gumbel, list_topp, row_done, row_items, total;
+  size_t lane_tops, topp_chunk_hist, topp_chunk_tb, row_ib, row_target, row_key, row_tau, row_state, chunk_max, cand_count, cand_count_a, cand_floor_a, cand_floor, cand, topp_cand, topp_n;
+  size_t list_n, list_gumbel, row_done, row_items, total;
 };
 
 static WsLayout ws_layout(int B, int V) {
@@ -1695,7 +1696,8 @@ static WsLayout ws_layout(int B, int V) {
   w.lane_tops = o;  o += align_up((size_t)B * nc * (kThreads / 64) * kTopsPub * 4, 256);
   w.topp_chunk_hist = o; o += align_up((size_t)B * nc * kToppBins * 8, 256);
   w.topp_chunk_tb = o;   o += align_up((size_t)B * nc * 4, 256);
-  w.row_tb = o;          o += align_up((size_t)B * 4, 256);
+  w.row_ib = o;          o += align_up((size_t)B * 4, 256);
+  w.row_target = o;      o += align_up((size_t)B * 8, 256);
   w.row_key = o;    o += (size_t)B * kRowPad8 * 8;
   w.row_tau = o;    o += align_up((size_t)B * 4, 256);
   w.row_state = o;  o += align_up((size_t)B * 4, 256);
@@ -1705,13 +1707,10 @@ static WsLayout ws_layout(int B, int V) {
   w.cand_floor_a = o; o += align_up((size_t)B * nc * 4, 256);
   w.cand_floor = o; o += align_up((size_t)B * nc * 4, 256);
   w.cand = o;       o += align_up((size_t)B * nc * kCandCap * 8, 256);
-  w.row_m = o;      o += align_up((size_t)B * 4, 256);
-  w.topp_hist = o;  o += align_up((size_t)B * kToppBins * 8, 256);
   w.topp_cand = o;  o += align_up((size_t)B * kToppCap * 8, 256);
   w.topp_n = o;     o += align_up((size_t)B * 4, 256);
   w.list_n = o;     o += 256;
   w.list_gumbel = o; o += align_up((size_t)B * nc * 4, 256);
-  w.list_topp = o;  o += align_up((size_t)B * 4, 256);
   w.row_done = o;   o += (size_t)B * kRowPad * 4;
   w.row_items = o;  o += (size_t)B * kRowPad * 4;
   w.total = o;
@@ -1736,7 +1735,8 @@ static SampleArgs make_args(const void* logits, int dtype, int batch, int vocab,
   a.lane_tops = (float*)(ws + w.lane_tops);
   a.topp_chunk_hist = (unsigned long long*)(ws + w.topp_chunk_hist);
   a.topp_chunk_tb = (int32_t*)(ws + w.topp_chunk_tb);
-  a.row_tb = (int32_t*)(ws + w.row_tb);
+  a.row_ib = (int32_t*)(ws + w.row_ib);
+  a.row_target = (unsigned long long*)(ws + w.row_target);
   a.row_key = (unsigned long long*)(ws + w.row_key);
   a.row_tau = (uint32_t*)(ws + w.row_tau);
   a.row_state = (int32_t*)(ws + w.row_state);
@@ -1746,13 +1746,10 @@ static SampleArgs make_args(const void* logits, int dtype, int batch, int vocab,
   a.cand_floor_a = (float*)(ws + w.cand_floor_a);
   a.cand_floor = (float*)(ws + w.cand_floor);
   a.cand = (unsigned long long*)(ws + w.cand);
-  a.row_m = (float*)(ws + w.row_m);
-  a.topp_hist = (unsigned long long*)(ws + w.topp_hist);
   a.topp_cand = (unsigned long long*)(ws + w.topp_cand);
   a.topp_n = (uint32_t*)(ws + w.topp_n);
   a.list_n = (uint32_t*)(ws + w.list_n);
   a.list_gumbel = (uint32_t*)(ws + w.list_gumbel);
-  a.list_topp = (uint32_t*)(ws + w.list_topp);
   a.row_done = (uint32_t*)(ws + w.row_done);
   a.row_items = (uint32_t*)(ws + w.row_items);
   return a;
@@ -1814,16 +1811,12 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   NVJSEL_LAUNCH_CHUNK(sample_scan_kernel, grid_chunks);
   hipLaunchKernelGGL(sample_select_kernel, dim3(batch), dim3(kThreads), 0, s, a);
   NVJSEL_CHECK_LAUNCH("sample_select_kernel");
-  const dim3 grid_rows_chunks((unsigned)((long long)batch * a.nchunks));
   const dim3 grid_items((unsigned)((long long)batch * a.nchunks * kGumbelSplit));
-  if (top_p) {
-    NVJSEL_LAUNCH_CHUNK(sample_topp_collect_kernel, grid_rows_chunks);
-  }
-  if (top_k || top_p) {
-    hipLaunchKernelGGL(sample_finalize_kernel, dim3(batch), dim3(kThreads), 0, s, a);
-    NVJSEL_CHECK_LAUNCH("sample_finalize_kernel");
-  }
   NVJSEL_LAUNCH_CHUNK(sample_gumbel_kernel, grid_items);
+  if (top_p) {
+    hipLaunchKernelGGL(sample_topp_finish_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+    NVJSEL_CHECK_LAUNCH("sample_topp_finish_kernel");
+  }
 #undef NVJSEL_LAUNCH_CHUNK
   return NVJSEL_OK;
 }
