@@ -455,23 +455,46 @@ struct FinishShared {
   unsigned long long red[kThreads / 64];
   unsigned long long wsum64[kThreads / 64];
   uint32_t wsum32[kThreads / 64];
-  uint32_t cnt[kThreads], cnt_a[kThreads];
+  uint32_t cnt_a[kThreads];
   float fl_a[kThreads];
   uint32_t n, kf, tau;
 };
 
+// The first loads of a fast top-k row, issued by select before it reduces the
+// chunk maxima so that both are in flight together: each chunk's tier A count
+// and floors (thread c), and in wave 0 the row's published lane maxima as
+// 16-bit keys (at most 1024 of them).
+struct TopkPrefetch {
+  uint32_t cnt_a;
+  float fl_a, fl;
+  uint32_t key[16];
+};
+
+__device__ __forceinline__ void topk_prefetch(const SampleArgs& a, int b, TopkPrefetch& pf) {
+  const int NC = a.nchunks;
+  pf.cnt_a = 0;
+  pf.fl_a = -INFINITY;
+  pf.fl = -INFINITY;
+  if ((int)threadIdx.x < NC) {
+    const size_t i = (size_t)b * NC + threadIdx.x;
+    pf.cnt_a = a.cand_count_a[i];
+    pf.fl_a = a.cand_floor_a[i];
+    pf.fl = a.cand_floor[i];
+  }
+  const int nvals = min(NC, kTopsChunks) * (kThreads / 64) * kTopsPub;
+  const float* tops = a.lane_tops + (size_t)b * NC * (kThreads / 64) * kTopsPub;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int j = (threadIdx.x & 63) + 64 * i;
+    pf.key[i] = threadIdx.x < 64 && j < nvals ? radix_key(tops[j]) >> 16 : 0u;
+  }
+}
+
 // Largest 16-bit prefix p with at least k of the row's published lane maxima
 // at or above p << 16 (0 when fewer than k are published).  Every published
 // value is a distinct element of the row, so (p << 16) <= the row's k-th
-// largest raw logit key.  Run by one wave; `nvals` <= 1024.
-__device__ __forceinline__ uint32_t row_tops_kth(const float* tops, int nvals, int k) {
-  const int lane = threadIdx.x & 63;
-  uint32_t key[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int j = lane + 64 * i;
-    key[i] = j < nvals ? radix_key(tops[j]) >> 16 : 0u;
-  }
+// largest raw logit key.  Run by one wave.
+__device__ __forceinline__ uint32_t row_tops_kth(const uint32_t (&key)[16], int nvals, int k) {
   const int nv = (nvals + 63) >> 6;
   uint32_t p = 0;
 #pragma unroll 1
@@ -487,28 +510,24 @@ __device__ __forceinline__ uint32_t row_tops_kth(const float* tops, int nvals, i
 }
 
 // Top-k (then top-p, then exact Gumbel-max) of a FILTER row with k <= 256 from
-// the scan's candidates, with the thresholds of the select kernel's candidate
-// path.  Returns false (nothing written) when a chunk's list overflowed or the
-// survivors do not fit in LDS.
-__device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp, float m, FinishShared& s) {
+// the scan's candidates (tier A lists), after topk_prefetch.  Returns false
+// (nothing written) when a chunk's list overflowed, the row floor falls below
+// a chunk's tier A, or the survivors do not fit in LDS.
+__device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp, float m, const TopkPrefetch& pf,
+                                FinishShared& s) {
   const int NC = a.nchunks, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (NC > kThreads) return false;
-  // round 1: chunk counts and floors, and (wave 0) the published lane maxima
-  float fl = -INFINITY;
   if ((int)threadIdx.x < NC) {
-    const size_t i = (size_t)b * NC + threadIdx.x;
-    s.cnt[threadIdx.x] = a.cand_count[i];
-    s.cnt_a[threadIdx.x] = a.cand_count_a[i];
-    s.fl_a[threadIdx.x] = a.cand_floor_a[i];
-    fl = a.cand_floor[i];
+    s.cnt_a[threadIdx.x] = pf.cnt_a;
+    s.fl_a[threadIdx.x] = pf.fl_a;
   }
   if (wave == 0) {
     const int nvals = min(NC, kTopsChunks) * (kThreads / 64) * kTopsPub;
-    const uint32_t p = row_tops_kth(a.lane_tops + (size_t)b * NC * (kThreads / 64) * kTopsPub, nvals, rp.k) << 16;
+    const uint32_t p = row_tops_kth(pf.key, nvals, rp.k) << 16;
     if (lane == 0) s.kf = p;
   }
   if (threadIdx.x == 0) s.n = 0;
-  const float flmax = unord_f32((uint32_t)block_max_u64(ord_f32(fl), s.red));  // (barriers)
+  const float flmax = unord_f32((uint32_t)block_max_u64(ord_f32(pf.fl), s.red));  // (barriers)
   // the row floor (raw logits) and, per chunk, how much of its list can reach it
   const float F = fmaxf(s.kf > 0x007FFFFFu ? radix_value(s.kf) : -INFINITY, flmax);
   const uint32_t kf = radix_key(F / rp.tp);
@@ -1459,6 +1478,9 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     queue_chunks(a, b, rp, 0u, best, s.q);
     return;
   }
+  const bool fast_topk = rp.mode == ROW_FILTER && rp.k > 0 && rp.k <= kFastK;
+  TopkPrefetch pf;
+  if (fast_topk) topk_prefetch(a, b, pf);
   unsigned long long mk = 0;
   for (int c = threadIdx.x; c < NC; c += blockDim.x) mk = max_u64(mk, a.chunk_max[(size_t)b * NC + c]);
   mk = block_max_u64(mk, s.red);
@@ -1482,7 +1504,7 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     if (threadIdx.x == 0) { a.out_ids[b] = (int32_t)(~(uint32_t)ans); a.row_state[b] = STATE_DONE; }
     return;
   }
-  if (rp.k > 0 && rp.k <= kFastK && finish_topk_row(a, b, rp, m, s.fin)) {
+  if (fast_topk && finish_topk_row(a, b, rp, m, pf, s.fin)) {
     if (threadIdx.x == 0) a.row_state[b] = STATE_DONE;
     return;
   }
