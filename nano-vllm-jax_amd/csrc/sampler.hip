@@ -1277,19 +1277,20 @@ struct QueueShared {
 };
 
 // Whole block, after the row's seed `best` (an exact score some kept element
-// reaches) is known: appends a gumbel item (b << 16 | c) for every chunk c that
+// reaches) is known, with the row's chunk maxima ck[] (in LDS): appends a gumbel item (b << 16 | c) for every chunk c that
 // can hold the row's maximum -- it has a kept element (chunk max >= tau) whose
 // best possible score, chunk max + the largest Gumbel draw, is not below the
 // seed -- and records the row's item count for the gumbel kernel's last-item
 // test.  A row left with no item (it cannot happen: the seed's own chunk
 // qualifies) is answered with the seed.
 __device__ __forceinline__ void queue_chunks(const SampleArgs& a, int b, const RowParams& rp, uint32_t tau,
-                                             unsigned long long best, QueueShared& q, bool prune = true) {
+                                             unsigned long long best, const unsigned long long* ck, QueueShared& q,
+                                             bool prune = true) {
   const int NC = a.nchunks;
   const float s_seed = prune ? prune_level(best) : -INFINITY;
   auto keep = [&](int c) {
     if (c >= NC) return false;
-    const float xv = chunk_max_x(rp, a.chunk_max[(size_t)b * NC + c]);
+    const float xv = chunk_max_x(rp, ck[c]);
     return radix_key(xv) >= tau && !(xv + NVJSEL_GUMBEL_MAX < s_seed);
   };
   uint32_t mine = 0;
@@ -1444,6 +1445,7 @@ __device__ __forceinline__ void topp_crossing(const unsigned long long (&h)[PER]
 
 struct SelectShared {
   unsigned long long red[kThreads / 64];
+  unsigned long long ck[1024];  // the row's chunk maxima
   int tb[1024];
   QueueShared q;
   ToppXShared tx;
@@ -1465,6 +1467,7 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     unsigned long long best = 0;
     for (int c = threadIdx.x; c < NC; c += blockDim.x) {
       const unsigned long long ck = a.chunk_max[(size_t)b * NC + c];
+      s.ck[c] = ck;
       const uint32_t i = ~(uint32_t)ck;
       const float xv = chunk_max_x(rp, ck);
       best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
@@ -1475,14 +1478,26 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
       a.row_ib[b] = INT_MIN;
       a.row_state[b] = STATE_NEEDS_GUMBEL;
     }
-    queue_chunks(a, b, rp, 0u, best, s.q);
+    queue_chunks(a, b, rp, 0u, best, s.ck, s.q);
     return;
   }
   const bool fast_topk = rp.mode == ROW_FILTER && rp.k > 0 && rp.k <= kFastK;
+  const bool topp_only = rp.mode == ROW_FILTER && rp.k == 0 && rp.p < 1.0f;
   TopkPrefetch pf;
   if (fast_topk) topk_prefetch(a, b, pf);
+  int tbm = INT_MIN;  // top-p-only rows: the chunks' top grid bins, loaded with the maxima
+  if (topp_only)
+    for (int c = threadIdx.x; c < NC; c += kThreads) {
+      const int t = a.topp_chunk_tb[(size_t)b * NC + c];
+      s.tb[c] = t;
+      tbm = max(tbm, t);
+    }
   unsigned long long mk = 0;
-  for (int c = threadIdx.x; c < NC; c += blockDim.x) mk = max_u64(mk, a.chunk_max[(size_t)b * NC + c]);
+  for (int c = threadIdx.x; c < NC; c += blockDim.x) {
+    const unsigned long long ck = a.chunk_max[(size_t)b * NC + c];
+    s.ck[c] = ck;
+    mk = max_u64(mk, ck);
+  }
   mk = block_max_u64(mk, s.red);
   if (rp.mode == ROW_GREEDY) {  // the row's first maximum
     if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)mk);
@@ -1513,20 +1528,13 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
   // the bin.  The rest (k > 256, rows whose floor falls below a chunk's tier A,
   // crowded ties, top-p rows without a usable histogram): exact threshold by a
   // whole-row radix descent here, then the gumbel pass over x >= threshold.
-  const bool topp_only = rp.k == 0 && rp.p < 1.0f;
   int ib = INT_MIN;
   if (topp_only) {
     // the row's histogram from the scan's chunk histograms: chunk c's bin d is
     // grid bin tb_c - d, the row's bin D is grid bin TB - D (TB = max tb_c)
-    int tbm = INT_MIN;
-    for (int c = threadIdx.x; c < NC; c += kThreads) {
-      const int t = a.topp_chunk_tb[(size_t)b * NC + c];
-      s.tb[c] = t;
-      tbm = max(tbm, t);
-    }
     const int TB = (int)(uint32_t)(block_max_u64((unsigned long long)(uint32_t)(tbm ^ INT_MIN), s.red)) ^ INT_MIN;
     constexpr int PER = kToppBins / kThreads;
-    constexpr int U = 8;  // chunks whose loads are in flight together
+    constexpr int U = 32;  // chunks whose loads are in flight together
     unsigned long long h[PER] = {};
     for (int c0 = 0; c0 < NC; c0 += U) {
       unsigned long long v[U][PER];
@@ -1564,7 +1572,7 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
   const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
   unsigned long long best = 0;
   for (int c = threadIdx.x; c < NC; c += kThreads) {
-    const unsigned long long ck = a.chunk_max[(size_t)b * NC + c];
+    const unsigned long long ck = s.ck[c];
     const float xv = chunk_max_x(rp, ck);
     if (radix_key(xv) < tau) continue;
     const uint32_t i = ~(uint32_t)ck;
@@ -1579,8 +1587,8 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     if (ib != INT_MIN) { a.row_target[b] = s.tx.target; a.topp_n[b] = 0; }
   }
   // top-p rows queue every chunk reaching the crossing bin (its elements are collected)
-  if (ib != INT_MIN) queue_chunks(a, b, rp, radix_key(topp_edge(ib)), best, s.q, false);
-  else queue_chunks(a, b, rp, tau, best, s.q);
+  if (ib != INT_MIN) queue_chunks(a, b, rp, radix_key(topp_edge(ib)), best, s.ck, s.q, false);
+  else queue_chunks(a, b, rp, tau, best, s.ck, s.q);
 }
 
 // ------------------------------------------------------------------ 4. gumbel over kept (heavy rows)
