@@ -439,6 +439,32 @@ __device__ __forceinline__ unsigned long long topp_target(float p, unsigned long
   if (Z > 0 && P > Z - 1) P = Z - 1;
   return P + 1;
 }
+// Wave-wide max and inclusive prefix sum with DPP row shifts and row
+// broadcasts (no LDS round trips): the result of the max is in every lane,
+// the scan is inclusive in lane order.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f32(float v, float old) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = fmaxf(v, dpp_f32<0x111, 0xF>(v, -INFINITY));  // row_shr:1
+  v = fmaxf(v, dpp_f32<0x112, 0xF>(v, -INFINITY));  // row_shr:2
+  v = fmaxf(v, dpp_f32<0x114, 0xF>(v, -INFINITY));  // row_shr:4
+  v = fmaxf(v, dpp_f32<0x118, 0xF>(v, -INFINITY));  // row_shr:8
+  v = fmaxf(v, dpp_f32<0x142, 0xA>(v, -INFINITY));  // row_bcast:15
+  v = fmaxf(v, dpp_f32<0x143, 0xC>(v, -INFINITY));  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);
+  return v;
+}
+
 // ------------------------------------------------------------------ top-k rows from candidates
 // A FILTER row with k <= 256: the row floor is the larger of the largest chunk
 // floor and the k-th largest lane maximum the scan published (four per wave);
@@ -500,10 +526,10 @@ __device__ __forceinline__ uint32_t row_tops_kth(const uint32_t (&key)[16], int 
 #pragma unroll 1
   for (int bit = 15; bit >= 0; --bit) {
     const uint32_t c = p | (1u << bit);
-    uint32_t cnt = 0;
+    uint32_t cnt = 0;  // this lane's values >= c, then the wave's (DPP sum, lane 63)
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      if (i < nv) cnt += (uint32_t)__popcll(__ballot(key[i] >= c));
+    for (int i = 0; i < 16; ++i) cnt += (i < nv && key[i] >= c) ? 1u : 0u;
+    cnt = (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_sum(cnt), 63);
     if (cnt >= (uint32_t)k) p = c;
   }
   return p;
@@ -619,32 +645,6 @@ struct ScanShared {
   uint32_t cnt, cnt_b, waves;
   unsigned long long topp_h[kToppBins];  // top-p-only rows: the chunk's grid-bin histogram
 };
-
-// Wave-wide max and inclusive prefix sum with DPP row shifts and row
-// broadcasts (no LDS round trips): the result of the max is in every lane,
-// the scan is inclusive in lane order.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_f32(float v, float old) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
-}
-__device__ __forceinline__ float wave_max_f32(float v) {
-  v = fmaxf(v, dpp_f32<0x111, 0xF>(v, -INFINITY));  // row_shr:1
-  v = fmaxf(v, dpp_f32<0x112, 0xF>(v, -INFINITY));  // row_shr:2
-  v = fmaxf(v, dpp_f32<0x114, 0xF>(v, -INFINITY));  // row_shr:4
-  v = fmaxf(v, dpp_f32<0x118, 0xF>(v, -INFINITY));  // row_shr:8
-  v = fmaxf(v, dpp_f32<0x142, 0xA>(v, -INFINITY));  // row_bcast:15
-  v = fmaxf(v, dpp_f32<0x143, 0xC>(v, -INFINITY));  // row_bcast:31
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v) {
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);
-  return v;
-}
 
 typedef short nvjsel_s16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short nvjsel_u16x2 __attribute__((ext_vector_type(2)));
