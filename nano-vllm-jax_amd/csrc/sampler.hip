@@ -12,30 +12,28 @@
 //
 // Kernels, all asynchronous on the caller's stream:
 //   1. scan       grid (chunks, B), each block holds an 8192-element chunk in
-//                 registers.  Writes the chunk's (max, ~index) key.  GREEDY rows
-//                 finish here.  FILTER
-//                 rows with 0 < k <= 256 emit a superset of the chunk's top-k:
-//                 every element >= the k-th largest of the 256 per-thread
-//                 maxima (at least k elements reach that value, so the chunk's
-//                 k-th largest is not below it).
-//   2. select     grid (B): FULL rows seed their best score with the exact
-//                 scores of the chunk maxima (a prune level for step 4).
-//                 Small-k FILTER rows: exact top-k over the candidates in
-//                 LDS (radix select), top-p over the survivors (radix descent
-//                 weighted by fixed-point mass), exact Gumbel-max over what is
-//                 kept.
-//                 Other FILTER rows (top-p only, k > 256, candidate overflow)
-//                 are marked heavy.
-//   3. threshold  grid (B), heavy rows only: radix descent (11/11/10-bit digits)
-//                 over the whole row for the k-th largest (counts) and the
-//                 top-p crossing (masses).
-//   4. gumbel     grid (chunks, B), FULL rows and heavy rows: Gumbel-max over
-//                 x >= tau (tau = 0 for FULL rows).
-//   5. finish     ids from the keys; re-zero the accumulators.
+//                 registers.  Writes the chunk's (max, ~index) key.  FILTER
+//                 rows with 0 < k <= 256 also write the chunk's largest
+//                 candidates (every element at or above a floor that is not
+//                 above the chunk's k-th largest, kept only down to the level
+//                 that 32 of the chunk's elements reach) and each wave's four
+//                 largest lane maxima; top-p-only rows a histogram of the
+//                 chunk's masses on a fixed 1/32-nat grid.
+//   2. select     grid (B): GREEDY rows finish.  Small-k FILTER rows finish from
+//                 the candidates above a tight row floor (rank sort in LDS,
+//                 top-k, top-p prefix, exact Gumbel-max).  FULL rows seed their
+//                 best score; top-p-only rows find their crossing bin; the rest
+//                 take an exact whole-row radix descent.  Every unfinished row
+//                 queues the chunks that can hold its winner.
+//   3. gumbel     one block per queued chunk quarter: Gumbel-max over
+//                 x >= tau; top-p-only rows score x above the crossing bin and
+//                 collect the bin's elements.  The row's last block writes its id.
+//   4. topp finish grid (B), top-p-only rows: exact threshold inside the
+//                 crossing bin and the final id.
 //
-// Mass is exp(x - max) in 2^-40 fixed point summed in 64-bit integers -- exact,
-// order-independent and deterministic, so "mass(x >= v) > p * Z" is decided
-// without accumulation-order noise.
+// Top-k survivors' masses are exp(x - max) in 2^-40 fixed point summed in
+// 64-bit integers; top-p-only rows use integer weights per grid bin combined
+// in fp64 (see topp_ibin).  Both are deterministic.
 //
 // Gumbel-max with few exact draws: a block computes every score with the
 // hardware fp32 log, takes the block maximum m, then recomputes exactly (fp64
