@@ -819,11 +819,7 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   // waves then hold at least sum kk_w >= k lane maxima >= theta, so theta <=
   // the chunk's k-th largest logit.  Less a margin of 8 orderable units for
   // values the division by T' may merge.
-#ifdef NVJSEL_PROBE_NOTOPK
-  const bool topk = false;
-#else
   const bool topk = rp.mode == ROW_FILTER && rp.k > 0 && rp.k <= kFastK;
-#endif
   uint32_t wfloor = 0xFFFFFFFFu;
   if (topk && !wnan) {
     // lane t holds an element iff its first vector (index t) lies in the row
