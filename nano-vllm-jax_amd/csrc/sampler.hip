@@ -1683,13 +1683,28 @@ __global__ void __launch_bounds__(kThreads) sample_topp_finish_kernel(SampleArgs
     for (int e = threadIdx.x; e < (int)n; e += kThreads) sh.v[e] = a.topp_cand[(size_t)b * kToppCap + e];
     __syncthreads();
     const uint32_t tau = lds_desc<true>(sh.d, sh.v, (int)n, a.row_target[b], ib);
+    // fast scores first; exact ones only within the fast path's error of the
+    // block maximum, and only if that maximum can beat the score above the bin
+    float fm = -INFINITY;
     for (int e = threadIdx.x; e < (int)n; e += kThreads) {
       const unsigned long long ce = sh.v[e];
       const uint32_t kk = (uint32_t)(ce >> 32);
       const float xv = radix_value(kk);
       if (kk < tau || xv + NVJSEL_GUMBEL_MAX < s_cur) continue;
-      const uint32_t i = (uint32_t)ce;
-      best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
+      fm = fmaxf(fm, xv + fast_noise(a, b, key, (int)(uint32_t)ce));
+    }
+    fm = unord_f32((uint32_t)block_max_u64(ord_f32(fm), sh.red));
+    const float margin = 1e-3f + fabsf(fm) * 4.8e-7f;
+    if (fm + margin >= s_cur) {
+      for (int e = threadIdx.x; e < (int)n; e += kThreads) {
+        const unsigned long long ce = sh.v[e];
+        const uint32_t kk = (uint32_t)(ce >> 32);
+        const float xv = radix_value(kk);
+        if (kk < tau || xv + NVJSEL_GUMBEL_MAX < s_cur) continue;
+        const uint32_t i = (uint32_t)ce;
+        if (xv + fast_noise(a, b, key, (int)i) < fm - margin) continue;
+        best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
+      }
     }
   } else {
     unsigned long long mk = 0;
