@@ -218,3 +218,40 @@ def test_strided_rows_and_unaligned_vocab(dtype):
     torch.cuda.synchronize()
     used = lt.float().cpu().numpy()
     check_sampled(out.cpu().numpy(), used, T, K, P, keys, ctx="strided")
+
+
+def test_topk_clustered_in_one_chunk_takes_exact_path():
+    """The row's top-k all sit in one 8192-element chunk: the row floor falls
+    below that chunk's tier-A level, so the fast path must hand the row to the
+    exact whole-row descent (and still agree with the oracle)."""
+    rng = np.random.default_rng(21)
+    B, V = 4, 248320
+    l = rng.standard_normal((B, V)).astype(np.float32)
+    for b in range(B):
+        base = 8192 * (3 + b)
+        l[b, base:base + 400] = 8.0 + rng.standard_normal(400).astype(np.float32)
+    T = [1.0] * B
+    K = [256, 100, 64, 256]
+    P = [1.0, 0.9, 1.0, 0.8]
+    ids, used, keys = _sample(l, T, top_k=K, top_p=P)
+    check_sampled(ids, used, T, K, P, keys, ctx="clustered top-k")
+
+
+def test_topp_crossing_bin_overflow_and_far_chunks():
+    """Top-p-only rows whose crossing bin holds far more than the LDS list
+    (200k equal values), rows with whole chunks far below the row maximum or
+    all -inf (outside the 32-nat histogram window), in f32 and bf16."""
+    rng = np.random.default_rng(22)
+    B, V = 4, 248320
+    l = np.full((B, V), -3.0, dtype=np.float32)
+    l[0, rng.choice(V, 50, replace=False)] = 1.0          # crossing bin = the -3.0 plateau
+    l[1] = rng.standard_normal(V).astype(np.float32)
+    l[1, 8192 * 5:8192 * 9] = -200.0                        # chunks 40+ nats below the maximum
+    l[2] = rng.standard_normal(V).astype(np.float32)
+    l[2, 8192 * 2:8192 * 3] = -np.inf                      # a chunk of -inf
+    l[3] = (rng.standard_normal(V) * 4).astype(np.float32)
+    T = [1.0, 0.7, 1.0, 0.5]
+    P = [0.5, 0.9, 0.95, 0.8]
+    for dtype in (torch.float32, torch.bfloat16):
+        ids, used, keys = _sample(l, T, top_k=[0] * B, top_p=P, dtype=dtype)
+        check_sampled(ids, used, T, [0] * B, P, keys, ctx=f"top-p edges {dtype}")
