@@ -479,7 +479,7 @@ struct FinishShared {
   unsigned long long red[kThreads / 64];
   unsigned long long wsum64[kThreads / 64];
   uint32_t wsum32[kThreads / 64];
-  uint32_t cnt_a[kThreads];
+  uint32_t cnt[kThreads], cnt_a[kThreads];
   float fl_a[kThreads];
   uint32_t n, kf, tau;
 };
@@ -489,18 +489,20 @@ struct FinishShared {
 // and floors (thread c), and in wave 0 the row's published lane maxima as
 // 16-bit keys (at most 1024 of them).
 struct TopkPrefetch {
-  uint32_t cnt_a;
+  uint32_t cnt, cnt_a;
   float fl_a, fl;
   uint32_t key[16];
 };
 
 __device__ __forceinline__ void topk_prefetch(const SampleArgs& a, int b, TopkPrefetch& pf) {
   const int NC = a.nchunks;
+  pf.cnt = 0;
   pf.cnt_a = 0;
   pf.fl_a = -INFINITY;
   pf.fl = -INFINITY;
   if ((int)threadIdx.x < NC) {
     const size_t i = (size_t)b * NC + threadIdx.x;
+    pf.cnt = a.cand_count[i];
     pf.cnt_a = a.cand_count_a[i];
     pf.fl_a = a.cand_floor_a[i];
     pf.fl = a.cand_floor[i];
@@ -533,15 +535,19 @@ __device__ __forceinline__ uint32_t row_tops_kth(const uint32_t (&key)[16], int 
   return p;
 }
 
-// Top-k (then top-p, then exact Gumbel-max) of a FILTER row with k <= 256 from
-// the scan's candidates (tier A lists), after topk_prefetch.  Returns false
-// (nothing written) when a chunk's list overflowed, the row floor falls below
-// a chunk's tier A, or the survivors do not fit in LDS.
-__device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp, float m, const TopkPrefetch& pf,
-                                FinishShared& s) {
+// The survivors of a row with k <= 256 (after topk_prefetch), sorted in
+// s.srt[0..n) by (key descending, index ascending) as (key << 32 | ~index):
+// every candidate at or above the row floor F = max(k-th largest published
+// lane maximum, largest chunk floor) <= the row's k-th largest, so the row's
+// top-k (ties included) is a prefix.  Returns -1 when a chunk's list
+// overflowed, F falls below a chunk's tier A and the list holds no tier B
+// (the sampler's), or the survivors do not fit in LDS.
+__device__ int topk_sorted_survivors(const SampleArgs& a, int b, const RowParams& rp, const TopkPrefetch& pf,
+                                     FinishShared& s) {
   const int NC = a.nchunks, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (NC > kThreads) return false;
+  if (NC > kThreads) return -1;
   if ((int)threadIdx.x < NC) {
+    s.cnt[threadIdx.x] = pf.cnt;
     s.cnt_a[threadIdx.x] = pf.cnt_a;
     s.fl_a[threadIdx.x] = pf.fl_a;
   }
@@ -555,15 +561,19 @@ __device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp,
   // the row floor (raw logits) and, per chunk, how much of its list can reach it
   const float F = fmaxf(s.kf > 0x007FFFFFu ? radix_value(s.kf) : -INFINITY, flmax);
   const uint32_t kf = radix_key(F / rp.tp);
-  // round 2: eight threads per chunk read what they need of its list
+  // eight threads per chunk read what they need of its list
   int bad = 0;
   for (int c0 = 0; c0 < NC; c0 += kThreads / 8) {
     const int c = c0 + (int)(threadIdx.x >> 3);
     int need = 0;
     if (c < NC) {
-      // the sampler's lists hold tier A only: a floor below it needs the exact path
-      need = (int)s.cnt_a[c];
-      bad |= F < s.fl_a[c] || need > kCandCap;
+      if (F >= s.fl_a[c]) {
+        need = (int)s.cnt_a[c];
+      } else {
+        need = (int)s.cnt[c];
+        bad |= a.topk == 0;  // the sampler's lists stop at tier A
+      }
+      bad |= need > kCandCap;
       need = min(need, kCandCap);
     }
     const unsigned long long* src = a.cand + ((size_t)b * NC + c) * kCandCap;
@@ -575,14 +585,14 @@ __device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp,
       for (int q = 0; q < 4; ++q)
         if (e0 + 8 * q < need && (uint32_t)(v[q] >> 32) >= kf) {
           const uint32_t slot = atomicAdd(&s.n, 1u);
-          if (slot < (uint32_t)kFinCap) s.ent[slot] = v[q];
+          if (slot < (uint32_t)kFinCap) s.ent[slot] = (v[q] & 0xFFFFFFFF00000000ull) | (uint32_t)~(uint32_t)v[q];
         }
     }
   }
-  if (__syncthreads_or(bad)) return false;
+  if (__syncthreads_or(bad)) return -1;
   __syncthreads();
   const int n = (int)s.n;
-  if (n > kFinCap || n < rp.k) return false;
+  if (n > kFinCap || n < rp.k) return -1;
   // rank sort, descending (keys are unique: they carry the index)
   for (int i = threadIdx.x; i < n; i += kThreads) {
     const unsigned long long e = s.ent[i];
@@ -591,6 +601,16 @@ __device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp,
     s.srt[rank] = e;
   }
   __syncthreads();
+  return n;
+}
+
+// Top-k (then top-p, then exact Gumbel-max) of a FILTER row with k <= 256 from
+// the scan's candidates.  Returns false (nothing written) when
+// topk_sorted_survivors cannot settle the row.
+__device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp, float m, const TopkPrefetch& pf,
+                                FinishShared& s) {
+  const int n = topk_sorted_survivors(a, b, rp, pf, s);
+  if (n < 0) return false;
   // kept: every survivor >= the k-th largest (ties kept) -- a prefix
   const uint32_t thr = (uint32_t)(s.srt[rp.k - 1] >> 32);
   uint32_t mine = 0;
@@ -621,7 +641,7 @@ __device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp,
     const unsigned long long ce = s.srt[i];
     const uint32_t kk = (uint32_t)(ce >> 32);
     if (kk < tau) continue;
-    const uint32_t idx = (uint32_t)ce;
+    const uint32_t idx = ~(uint32_t)ce;
     best = max_u64(best, argmax_key(radix_value(kk) + exact_noise(a, b, key, (int)idx), idx));
   }
   best = block_max_u64(best, s.red);
@@ -1103,6 +1123,7 @@ static constexpr int kTopkMax = 256;
 static constexpr int kTopkSort = 2048;
 
 struct TopkShared {
+  FinishShared fin;
   unsigned long long cand[kSelCap];
   unsigned long long sel[kTopkSort];
   DescShared d;
@@ -1196,11 +1217,25 @@ __global__ void __launch_bounds__(kThreads) topk_select_kernel(SampleArgs a, flo
   __shared__ TopkShared s;
   const int b = blockIdx.x, K = a.topk, NC = a.nchunks;
   const char* row = row_ptr(a, b);
+  TopkPrefetch pf;
+  topk_prefetch(a, b, pf);
   // the row's maximum key tells whether it holds a NaN
   unsigned long long mk = 0;
   for (int c = threadIdx.x; c < NC; c += blockDim.x) mk = max_u64(mk, a.chunk_max[(size_t)b * NC + c]);
   mk = block_max_u64(mk, s.red);
   bool fast = (uint32_t)(mk >> 32) != 0xFFFFFFFFu;
+  if (fast) {
+    // the sorted survivors above the row floor: their first K are the answer
+    const int ns = topk_sorted_survivors(a, b, row_params(a, b), pf, s.fin);
+    if (ns >= K) {
+      for (int j = threadIdx.x; j < K; j += blockDim.x) {
+        const uint32_t i = ~(uint32_t)s.fin.srt[j];
+        out_indices[(size_t)b * K + j] = (int32_t)i;
+        out_values[(size_t)b * K + j] = load_logit_t<DT>(row, (int)i);
+      }
+      return;
+    }
+  }
   int n = 0;
   if (fast) {
     uint32_t cnt[4], local = 0;
