@@ -481,17 +481,18 @@ struct FinishShared {
   uint32_t wsum32[kThreads / 64];
   uint32_t cnt[kThreads], cnt_a[kThreads];
   float fl_a[kThreads];
-  uint32_t n, kf, tau;
+  uint32_t hist[256];
+  uint32_t n, kf, tau, rem;
 };
 
 // The first loads of a fast top-k row, issued by select before it reduces the
 // chunk maxima so that both are in flight together: each chunk's tier A count
-// and floors (thread c), and in wave 0 the row's published lane maxima as
-// 16-bit keys (at most 1024 of them).
+// and floors (thread c), and the row's published lane maxima as 16-bit keys
+// (at most 1024 of them, four per thread).
 struct TopkPrefetch {
   uint32_t cnt, cnt_a;
   float fl_a, fl;
-  uint32_t key[16];
+  uint32_t key[4];  // published lane maxima t + 256 i, as 16-bit keys (0: none)
 };
 
 __device__ __forceinline__ void topk_prefetch(const SampleArgs& a, int b, TopkPrefetch& pf) {
@@ -510,29 +511,39 @@ __device__ __forceinline__ void topk_prefetch(const SampleArgs& a, int b, TopkPr
   const int nvals = min(NC, kTopsChunks) * (kThreads / 64) * kTopsPub;
   const float* tops = a.lane_tops + (size_t)b * NC * (kThreads / 64) * kTopsPub;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int j = (threadIdx.x & 63) + 64 * i;
-    pf.key[i] = threadIdx.x < 64 && j < nvals ? radix_key(tops[j]) >> 16 : 0u;
+  for (int i = 0; i < 4; ++i) {
+    const int j = (int)threadIdx.x + kThreads * i;
+    pf.key[i] = j < nvals ? radix_key(tops[j]) >> 16 : 0u;
   }
 }
 
 // Largest 16-bit prefix p with at least k of the row's published lane maxima
 // at or above p << 16 (0 when fewer than k are published).  Every published
 // value is a distinct element of the row, so (p << 16) <= the row's k-th
-// largest raw logit key.  Run by one wave.
-__device__ __forceinline__ uint32_t row_tops_kth(const uint32_t (&key)[16], int nvals, int k) {
-  const int nv = (nvals + 63) >> 6;
-  uint32_t p = 0;
+// largest raw logit key.  Two 8-bit radix passes over an LDS histogram; thread
+// t owns digit 255 - t, so one block scan finds each digit.
+__device__ __forceinline__ uint32_t row_tops_kth(const uint32_t (&key)[4], int k, FinishShared& s) {
+  uint32_t prefix = 0, rem = (uint32_t)k;
 #pragma unroll 1
-  for (int bit = 15; bit >= 0; --bit) {
-    const uint32_t c = p | (1u << bit);
-    uint32_t cnt = 0;  // this lane's values >= c, then the wave's (DPP sum, lane 63)
+  for (int pass = 0; pass < 2; ++pass) {
+    const int sh = pass == 0 ? 8 : 0;
+    s.hist[threadIdx.x] = 0;
+    if (threadIdx.x == 0) { s.kf = 0; s.rem = 0; }
+    __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 16; ++i) cnt += (i < nv && key[i] >= c) ? 1u : 0u;
-    cnt = (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_sum(cnt), 63);
-    if (cnt >= (uint32_t)k) p = c;
+    for (int i = 0; i < 4; ++i)
+      if (key[i] != 0u && (pass == 0 || (key[i] >> 8) == (prefix >> 8))) atomicAdd(&s.hist[(key[i] >> sh) & 255u], 1u);
+    __syncthreads();
+    const uint32_t h = s.hist[255 - threadIdx.x];
+    uint32_t tot;
+    const uint32_t above = block_exclusive_scan<uint32_t>(h, s.wsum32, tot);
+    if (above < rem && rem <= above + h) { s.kf = prefix | ((uint32_t)(255 - threadIdx.x) << sh); s.rem = rem - above; }
+    __syncthreads();
+    if (pass == 0 && tot < rem) return 0u;  // fewer than k published values
+    prefix = s.kf;
+    rem = s.rem;
   }
-  return p;
+  return prefix;
 }
 
 // The survivors of a row with k <= 256 (after topk_prefetch), sorted in
@@ -551,15 +562,11 @@ __device__ int topk_sorted_survivors(const SampleArgs& a, int b, const RowParams
     s.cnt_a[threadIdx.x] = pf.cnt_a;
     s.fl_a[threadIdx.x] = pf.fl_a;
   }
-  if (wave == 0) {
-    const int nvals = min(NC, kTopsChunks) * (kThreads / 64) * kTopsPub;
-    const uint32_t p = row_tops_kth(pf.key, nvals, rp.k) << 16;
-    if (lane == 0) s.kf = p;
-  }
+  const uint32_t kf16 = row_tops_kth(pf.key, rp.k, s) << 16;
   if (threadIdx.x == 0) s.n = 0;
   const float flmax = unord_f32((uint32_t)block_max_u64(ord_f32(pf.fl), s.red));  // (barriers)
   // the row floor (raw logits) and, per chunk, how much of its list can reach it
-  const float F = fmaxf(s.kf > 0x007FFFFFu ? radix_value(s.kf) : -INFINITY, flmax);
+  const float F = fmaxf(kf16 > 0x007FFFFFu ? radix_value(kf16) : -INFINITY, flmax);
   const uint32_t kf = radix_key(F / rp.tp);
   // eight threads per chunk read what they need of its list
   int bad = 0;
