@@ -185,13 +185,22 @@ __device__ __forceinline__ uint64_t edge_mass(float x, int ib) {
   return (uint64_t)rintf(__builtin_amdgcn_exp2f(d * 1.44269504088896341f) * 1099511627776.0f);
 }
 
+// A block barrier that orders LDS only: unlike __syncthreads it does not wait
+// for the block's outstanding global stores and atomics, so those stay in
+// flight across it (nothing global is exchanged through these barriers).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Block-wide max of a 64-bit key (every thread gets the result).
 __device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v, unsigned long long* sh) {
   v = wave_max_u64(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
+  lds_barrier();
   if (lane == 0) sh[wave] = v;
-  __syncthreads();
+  lds_barrier();
   unsigned long long m = 0;
   for (int w = 0; w < (int)(blockDim.x >> 6); ++w) m = max_u64(m, sh[w]);
   return m;
@@ -313,7 +322,7 @@ __device__ __forceinline__ unsigned long long block_gumbel(const SampleArgs& a, 
       sh.di[pos] = (uint32_t)elem_index<VEC>(base, j);
       ++pos;
     }
-  __syncthreads();
+  lds_barrier();
   // dense entry e = 4 * kThreads * g + 4 * t + j
   constexpr int G = EPT / 4;
   float st[EPT];
@@ -366,9 +375,9 @@ __device__ __forceinline__ unsigned long long block_gumbel(const SampleArgs& a, 
       if (4 * kThreads * g + 4 * (int)threadIdx.x + j < (int)n && st[4 * g + j] >= thr) cm |= 1u << (4 * g + j);
   unsigned long long best = 0;
   for (;;) {
-    __syncthreads();
+    lds_barrier();
     if (threadIdx.x == 0) sh.n = 0;
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int q = 0; q < EPT; ++q) {
       if (!((cm >> q) & 1u)) continue;
@@ -380,7 +389,7 @@ __device__ __forceinline__ unsigned long long block_gumbel(const SampleArgs& a, 
         cm &= ~(1u << q);
       }
     }
-    __syncthreads();
+    lds_barrier();
     const uint32_t nq = sh.n;
     const int lim = nq < (uint32_t)kExactCap ? (int)nq : kExactCap;
     for (int e = threadIdx.x; e < lim; e += kThreads) {
@@ -410,9 +419,9 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* ws, T& total) {
     }
     if (lane >= d) incl += o;
   }
-  __syncthreads();
+  lds_barrier();
   if (lane == 63) ws[wave] = incl;
-  __syncthreads();
+  lds_barrier();
   T before = 0, tot = 0;
   for (int w = 0; w < nw; ++w) {
     const T t = ws[w];
@@ -878,7 +887,7 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   const bool topp_row = a.topk == 0 && rp.mode == ROW_FILTER && rp.k == 0 && rp.p < 1.0f;
   if (topp_row)
     for (int d = threadIdx.x; d < kToppBins; d += kThreads) sh.topp_h[d] = 0;
-  __syncthreads();
+  lds_barrier();
   unsigned long long cbest = sh.wkey[0];
   uint32_t prefix = sh.wfloor[0];
 #pragma unroll
@@ -912,7 +921,7 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     unsigned long long* ch = a.topp_chunk_hist + ((size_t)b * a.nchunks + c) * kToppBins;
     for (int d = threadIdx.x; d < kToppBins; d += kThreads) ch[d] = sh.topp_h[d];
     if (threadIdx.x == 0) a.topp_chunk_tb[(size_t)b * a.nchunks + c] = tb;
@@ -958,7 +967,7 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   uint32_t slot_a = (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase) + ((incl - mine) & 0xFFFFu);
   uint32_t slot_b = 0;
   if (a.topk > 0) {
-    __syncthreads();
+    lds_barrier();
     const uint32_t n_a = sh.cnt;
     wbase = 0;
     if (lane == 0 && (wtot >> 16)) wbase = atomicAdd(&sh.cnt_b, wtot >> 16);
@@ -1661,7 +1670,7 @@ __device__ __forceinline__ void gumbel_item(const SampleArgs& a, uint32_t item, 
     uint32_t n;
     uint32_t pos = block_exclusive_scan<uint32_t>((uint32_t)__popc(in_bin), sh.wsum, n);
     if (threadIdx.x == 0) sh.n = n ? atomicAdd(&a.topp_n[b], n) : 0u;  // one reservation per block
-    __syncthreads();
+    lds_barrier();
     pos += sh.n;
 #pragma unroll
     for (int j = 0; j < kGumbelEPT; ++j)
