@@ -63,6 +63,9 @@
 #ifndef NVJSEL_GEMV_BPC
 #define NVJSEL_GEMV_BPC 1  // blocks per CU for the streaming GEMV (0 = occupancy)
 #endif
+#ifndef NVJSEL_TILE_QCAP
+#define NVJSEL_TILE_QCAP 768  // queue entries per epilogue wave (sample mode)
+#endif
 #ifndef NVJSEL_GEMV_R
 #define NVJSEL_GEMV_R 4  // rows per wave step of the streaming GEMV
 #endif
@@ -249,17 +252,17 @@ __device__ __forceinline__ void finish_rows(unsigned long long* row_keys, unsign
 // Scores N consecutive vocabulary entries v0.. of one batch row (raw fp32
 // dots).  Greedy: folds argmax keys into `best`.  Sample: computes the fast
 // approximate scores for all N in one straight-line block (N interleaved
-// Threefry chains), then queues with push(x, v) every entry that can still be
-// the row's exact maximum:
+// Threefry chains) and marks in q[] (scaled logit xq[], approximate score aq[])
+// every entry that can still be the row's exact maximum:
 // |approx - exact| <= d(s) = 1e-4 + 4.8e-7 |s| (hardware log error ~1e-6 on the
 // draw, plus one ulp of the sum), so the exact maximum j has
 // approx_j >= approx_k - d(s_j) - d(s_k) for every k and is queued when it
 // arrives, whatever set of approximate scores `amax` is the maximum of.
 // Magnitudes are clamped so -inf stays -inf; a NaN scaled logit scores +inf.
-template <int MODE, int N, typename Push>
+template <int MODE, int N>
 __device__ __forceinline__ void score_run(const float (&raw)[N], int v0, int V, int reduce_cast, bool greedy_row,
                                           bool unit_tp, float tp, const TfKey& key, float& amax,
-                                          unsigned long long& best, Push&& push) {
+                                          unsigned long long& best, bool (&q)[N], float (&xq)[N], float (&aq)[N]) {
   // one branch per run, not per element: the cast and the bounds are uniform
   float val[N];
   if (reduce_cast == 1) {
@@ -295,19 +298,14 @@ __device__ __forceinline__ void score_run(const float (&raw)[N], int v0, int V, 
     // every draw feeds an unconditional select, so none is sunk into a branch
     const float am = amax;
     const float sam = fminf(fabsf(am), 1e30f);
-    bool q[N], anyq = false;
 #pragma unroll
     for (int e = 0; e < N; ++e) {
       const bool ok = v0 + e < V;
       const float slack = 2e-4f + 4.8e-7f * (fminf(fabsf(ap[e]), 1e30f) + sam);
       q[e] = ok && !(ap[e] + slack < am);
-      anyq |= q[e];
+      xq[e] = xv[e];
+      aq[e] = ap[e];
       amax = fmaxf(amax, ok ? ap[e] : -INFINITY);
-    }
-    if (anyq) {  // rare once the row's maximum is established
-#pragma unroll
-      for (int e = 0; e < N; ++e)
-        if (q[e]) push(xv[e], v0 + e);
     }
   } else {
 #pragma unroll
@@ -680,7 +678,9 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
 // One barrier per tile orders both rings, so a tile costs max(GEMM, epilogue)
 // rather than their sum, and the epilogue's VALU work (Threefry + logs) runs
 // beside the GEMM waves' LDS, MFMA and memory waits on the same SIMDs.
-template <int NB, int GW, int MODE, int DEPTH, int EPM>
+// PN: the final RMSNorm prologue is compiled in (a.prenorm set); kept out of
+// the plain kernel so its registers do not constrain the main loops.
+template <int NB, int GW, int MODE, int DEPTH, int EPM, bool PN>
 __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmArgs a) {
   constexpr int EW = NB * EPM;     // epilogue waves
   constexpr int EPL = 4 / EPM;     // vocabulary rows per epilogue lane per tile
@@ -695,12 +695,16 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
   constexpr int LPT = 2048 / NTG;  // 16-byte loads per GEMM thread per 32 KB tile
   static_assert(2048 % NTG == 0, "tile loads split evenly");
   constexpr int ROWS = NB * 16;    // batch rows of the block
-  constexpr int QCAP = 64 * 4 + 64;
+  // per-epilogue-wave queue of entries that may be their row's maximum; it is
+  // filtered against the rows' current approximate maxima when it fills and
+  // at the end, and only the survivors are rescored exactly
+  constexpr int QCAP = NVJSEL_TILE_QCAP * 4 / (EW > 4 ? EW : 4);  // LDS: 12 B per entry
+  static_assert(QCAP >= 2 * 64 * EPL, "room for a filtered queue plus one tile");
   __shared__ u32x4_t wt[2][16 * 128];
   __shared__ f32x4_t part[2][KSPLIT * NB * 64];
   __shared__ float qx[MODE == MODE_SAMPLE ? EW : 1][QCAP];
   __shared__ uint32_t qv[MODE == MODE_SAMPLE ? EW : 1][QCAP];
-  __shared__ uint32_t qn[EW];
+  __shared__ float qa[MODE == MODE_SAMPLE ? EW : 1][QCAP];
   __shared__ unsigned long long qbest[MODE == MODE_SAMPLE ? EW : 1][64];
   __shared__ unsigned long long red[EW * 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -725,6 +729,7 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
   TfKey key = tf_key(0u, 0u);
   unsigned long long best = 0;
   float amax = -INFINITY;
+  uint32_t qcount = 0;  // wave-uniform: entries in this epilogue wave's queue
 
   auto load_tile = [&](u32x4_t(&dst)[LPT], int i) NVJSEL_INLINE {
     const int tile = blockIdx.x + i * grid;
@@ -741,7 +746,7 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
   // x and (vocab << 6 | lane that found it); results fold into qbest[lane]
   auto flush = [&]() {
     if constexpr (MODE == MODE_SAMPLE) {
-      const uint32_t n = qn[ew];
+      const uint32_t n = qcount;
       for (uint32_t e0 = 0; e0 < n; e0 += 64) {  // wave-uniform trip count
         const uint32_t e = e0 + lane;
         const bool live = e < n;
@@ -752,14 +757,45 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
                        (uint32_t)__shfl((int)key.k2, (int)src, 64)};
         if (live) atomicMax(&qbest[ew][src], argmax_key(qx[ew][e] + gumbel_at(k2, v), v));
       }
-      if (lane == 0) qn[ew] = 0;
+      qcount = 0;
+    }
+  };
+  // drops the queued entries that can no longer be their row's maximum: an
+  // entry (approximate score a) survives while a + slack(a, m) >= m for the
+  // current maximum m of the lane that queued it -- the test it passed when
+  // it was queued, against a maximum that has only grown since.  Compaction
+  // in place: a wave reads each 64-entry group before writing survivors at or
+  // below it.
+  auto compact = [&]() {
+    if constexpr (MODE == MODE_SAMPLE) {
+      uint32_t nk = 0;
+      for (uint32_t e0 = 0; e0 < qcount; e0 += 64) {  // wave-uniform trip count
+        const uint32_t e = e0 + lane;
+        const bool live = e < qcount;
+        const float x = live ? qx[ew][e] : 0.0f;
+        const float ap = live ? qa[ew][e] : -INFINITY;
+        const uint32_t pv = live ? qv[ew][e] : 0u;
+        const float am = __shfl(amax, (int)(pv & 63u), 64);
+        const float slack = 2e-4f + 4.8e-7f * (fminf(fabsf(ap), 1e30f) + fminf(fabsf(am), 1e30f));
+        const bool keep = live && !(ap + slack < am);
+        const unsigned long long m = __ballot(keep);
+        if (keep) {
+          const uint32_t slot = nk + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+          qx[ew][slot] = x;
+          qa[ew][slot] = ap;
+          qv[ew][slot] = pv;
+        }
+        nk += (uint32_t)__popcll(m);
+      }
+      qcount = nk;
     }
   };
 
   __shared__ float pre_ss[KSPLIT][ROWS];
   if (gemm) {
     const int brow = nb * 16 + r;
-    if (!a.prenorm) {
+    if constexpr (!PN) {
       const uint16_t* hp = (const uint16_t*)a.hidden + (size_t)(brow < B ? brow : 0) * 1024;
 #pragma unroll
       for (int kk = 0; kk < KPW; ++kk) {
@@ -789,7 +825,6 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
       tp = temp_floor(t);
       unit_tp = (tp == 1.0f);  // x / 1 == x exactly
       if (erow < B) key = tf_key(a.keys[2 * erow], a.keys[2 * erow + 1]);
-      if (lane == 0) qn[ew] = 0;
       qbest[ew][lane] = 0;
     }
   }
@@ -801,7 +836,7 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
   // pass 2 of the RMSNorm prologue (GEMM waves), run once the first W tiles
   // are in flight; its barrier pairs with the epilogue waves' first one
   auto finish_prenorm = [&]() NVJSEL_INLINE {
-    if (!a.prenorm) return;
+    if constexpr (!PN) return;
     __syncthreads();  // the row sums are in LDS
     // pass 2: normalise, round, pack this lane's fragments
     const int brow = nb * 16 + r;
@@ -844,7 +879,7 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
     }, finish_prenorm);
     __syncthreads();  // the epilogue waves' last iteration
   } else {
-    if (a.prenorm) __syncthreads();  // pairs with the GEMM waves' prologue barrier
+    if constexpr (PN) __syncthreads();  // pairs with the GEMM waves' prologue barrier
     for (int i = 0; i <= my_tiles; ++i) {
       __syncthreads();
       if (i == 0) continue;
@@ -866,23 +901,47 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
 #pragma unroll
           for (int m = ROWS; m < 64; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
         }
-        if (qn[ew] >= 64u) flush();  // full waves of exact work; room for this tile
+        if (qcount > (uint32_t)(QCAP - 64 * EPL)) {  // room for this tile
+          compact();
+          if (qcount > (uint32_t)(QCAP - 64 * EPL)) flush();
+        }
       }
+      bool q[EPL];
+      float xq[EPL], aq[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) q[e] = false;
       if (erow < B) {
         float raw[EPL];
 #pragma unroll
         for (int e = 0; e < EPL; ++e) raw[e] = EPL == 4 ? s[e] : (c0 == 0 ? s[e] : s[e + 2]);
-        score_run<MODE, EPL>(raw, v0, V, a.reduce_cast, greedy_row, unit_tp, tp, key, amax, best,
-                           [&](float x, int v) {
-                             const uint32_t slot = atomicAdd(&qn[ew], 1u);
-                             qx[ew][slot] = x;
-                             qv[ew][slot] = ((uint32_t)v << 6) | (uint32_t)lane;
-                           });
+        score_run<MODE, EPL>(raw, v0, V, a.reduce_cast, greedy_row, unit_tp, tp, key, amax, best, q, xq, aq);
+      }
+      if constexpr (MODE == MODE_SAMPLE) {
+        // queue the marked entries with the whole wave active: slots from a
+        // ballot, no LDS counter
+        bool anyq = false;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) anyq |= q[e];
+        if (__any(anyq)) {
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) {
+            const unsigned long long m = __ballot(q[e]);
+            if (q[e]) {
+              const uint32_t slot = qcount + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+              qx[ew][slot] = xq[e];
+              qa[ew][slot] = aq[e];
+              qv[ew][slot] = ((uint32_t)(v0 + e) << 6) | (uint32_t)lane;
+            }
+            qcount += (uint32_t)__popcll(m);
+          }
+        }
       }
     }
   }
   if (!gemm) {
     if constexpr (MODE == MODE_SAMPLE) {
+      compact();
       flush();
       if (!greedy_row) best = max_u64(best, qbest[ew][lane]);
     }
@@ -916,10 +975,11 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
 
 template <int NB, int GW, int MODE>
 static int launch_tile(const LmArgs& a, hipStream_t stream) {
-  // a second epilogue wave per batch tile pays off where the register budget
-  // allows it (measured, sample mode: B=32 91 -> 81 us; B=64 would spill)
-  constexpr int EPM = (MODE == MODE_SAMPLE && NB == 2) ? 2 : 1;
-  auto kern = lm_head_tile_kernel<NB, GW, MODE, NVJSEL_TILE_DEPTH, EPM>;
+  // a second epilogue wave per batch tile (sample mode; measured B=32 91 ->
+  // 81 us, B=64 125 -> 118 us): two waves per SIMD issue the draws
+  constexpr int EPM = (MODE == MODE_SAMPLE && NB >= 2) ? 2 : 1;
+  auto kern = a.prenorm ? lm_head_tile_kernel<NB, GW, MODE, NVJSEL_TILE_DEPTH, EPM, true>
+                        : lm_head_tile_kernel<NB, GW, MODE, NVJSEL_TILE_DEPTH, EPM, false>;
   int grid = NVJSEL_TILE_BPC * device_cu_count();
   const int ntiles = (a.V + 15) / 16;
   if (grid > ntiles) grid = ntiles;

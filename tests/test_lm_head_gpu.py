@@ -178,6 +178,35 @@ def test_fused_lm_head_sample_full_vocab_c4():
     assert namb <= 4
 
 
+@pytest.mark.parametrize("batch", [20, 64])
+def test_fused_lm_head_sample_nan_rows_fill_queue(batch):
+    """Rows whose hidden holds a NaN have NaN logits everywhere: every entry
+    scores +inf approximately, so each one stays a candidate, the epilogue's
+    candidate queue overflows and is rescored exactly mid-run (several times
+    at V=20011); those rows take the first index (first NaN wins, as
+    jnp.argmax), and the finite rows beside them stay exact."""
+    from tests.gpu_helpers import check_fused_sampled, engine_keys, keys_tensor
+
+    rng = np.random.default_rng(900 + batch)
+    H, V = 1024, 20011
+    hn = rng.standard_normal((batch, H))
+    nan_rows = [1, batch // 2, batch - 1]
+    for b in nan_rows:
+        hn[b, 17] = np.nan
+    h = bf16_tensor(hn)
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    T = [1.0] * batch
+    keys = engine_keys(batch, 23)
+    ids = nvjsel.lm_head_sample_token_ids(h, W, temperatures=torch.tensor(T).cuda(),
+                                          rng_keys=keys_tensor(keys), weight_layout="vh")
+    torch.cuda.synchronize()
+    got = ids.cpu().numpy()
+    assert [int(got[b]) for b in nan_rows] == [0] * len(nan_rows)
+    z = sel.lm_head_logits(as_f32(h), as_f32(W))
+    namb = check_fused_sampled(got, z, T, keys, 1, f"fused NaN rows B={batch}")
+    assert namb <= max(1, batch // 8)
+
+
 @pytest.mark.parametrize("seq_len", [1, 3])
 def test_mtp_draft_top1_casts_and_flattens(seq_len):
     """mtp/mtp_layer.py:220-248: fp32 x_normed [B, T, H] cast to the weight's
