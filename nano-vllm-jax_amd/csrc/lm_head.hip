@@ -295,14 +295,19 @@ __device__ __forceinline__ void score_run(const float (&raw)[N], int v0, int V, 
       const float t = xv[e] + gumbel_fast_from_bits(bits[e]);
       ap[e] = (t != t) ? INFINITY : t;
     }
-    // every draw feeds an unconditional select, so none is sunk into a branch
+    // every draw feeds an unconditional select, so none is sunk into a branch.
+    // One threshold per run instead of the per-entry slack: an entry that
+    // passes ap + 2e-4 + 4.8e-7 (|ap| + |am|) >= am has |ap| <= |am| + slack,
+    // so slack <= 2.01e-4 + 9.61e-7 |am| and ap >= am - that bound: the
+    // queued set only grows (the filter before exact rescoring applies the
+    // per-entry test).  am = -inf queues every entry, am = +inf only +inf.
     const float am = amax;
-    const float sam = fminf(fabsf(am), 1e30f);
+    const float thr = am - (2.01e-4f + 9.61e-7f * fminf(fabsf(am), 1e30f));
+    const bool all_in = v0 + N <= V;  // uniform per run except in the last tile
 #pragma unroll
     for (int e = 0; e < N; ++e) {
-      const bool ok = v0 + e < V;
-      const float slack = 2e-4f + 4.8e-7f * (fminf(fabsf(ap[e]), 1e30f) + sam);
-      q[e] = ok && !(ap[e] + slack < am);
+      const bool ok = all_in || v0 + e < V;
+      q[e] = ok && ap[e] >= thr;
       xq[e] = xv[e];
       aq[e] = ap[e];
       amax = fmaxf(amax, ok ? ap[e] : -INFINITY);

@@ -220,12 +220,9 @@ __device__ __forceinline__ uint32_t after(uint64_t v) {
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
 // fp32 -> bf16 -> fp32 with round-to-nearest-even (NaN kept NaN).
-__device__ __forceinline__ float round_bf16(float v) {
-  uint32_t u = __float_as_uint(v);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return v;
-  u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
-  return __uint_as_float(u);
-}
+// fp32 -> bf16 -> fp32, round to nearest even: gfx950's v_cvt_pk_bf16_f32
+// (a NaN stays a NaN).
+__device__ __forceinline__ float round_bf16(float v) { return (float)(__bf16)v; }
 
 __device__ __forceinline__ float round_f16(float v) { return (float)(_Float16)v; }
 
