@@ -55,6 +55,9 @@ static constexpr int kRowPad8 = 32;  // uint64 words
 
 enum { STATE_DONE = 1, STATE_HEAVY = 2, STATE_NEEDS_GUMBEL = 3, STATE_TOPP = 4 };
 
+#ifndef NVJSEL_SAMPLE_ONEPASS
+#define NVJSEL_SAMPLE_ONEPASS 1  // calls without top-k/top-p arrays: one-pass Gumbel-max
+#endif
 static constexpr int kThreads = 256;
 static constexpr int kEPT = 32;                    // elements per thread in chunk kernels
 static constexpr int kChunk = kThreads * kEPT;     // 8192 elements per block
@@ -1702,6 +1705,59 @@ __global__ void __launch_bounds__(kThreads) sample_gumbel_kernel(SampleArgs a) {
   gumbel_item<DT, VEC>(a, a.list_gumbel[it], (int)(blockIdx.x % kGumbelSplit), sh);
 }
 
+// ------------------------------------------------------------------ one pass (no top-k, no top-p)
+// Calls without top-k and top-p arrays hold only greedy and temperature rows
+// (model.py:929-936): every element of a temperature row may need its draw,
+// so the scan / select / seed stages buy little.  One block per
+// (2048-element sub-chunk, row) scores its elements directly -- greedy rows
+// by argmax key of the raw logit, temperature rows by the block Gumbel-max
+// (fast draws, exact rescoring near the block maximum) -- and leaves one key
+// per block; a per-row kernel takes the maximum.
+template <int DT, int VEC>
+__global__ void __launch_bounds__(kThreads) sample_onepass_kernel(SampleArgs a) {
+  __shared__ GumbelShared sh;
+  const int b = blockIdx.y;
+  const int base = blockIdx.x * (kThreads * kGumbelEPT);
+  const RowParams rp = row_params(a, b);
+  float x[kGumbelEPT];
+  uint32_t valid;
+  load_chunk_elems<DT, VEC, kGumbelEPT>(row_ptr(a, b), base, a.V, true, 1.0f, x, valid);
+  unsigned long long best = 0;
+  if (rp.mode == ROW_GREEDY) {  // block-uniform
+#pragma unroll
+    for (int j = 0; j < kGumbelEPT; ++j)
+      if ((valid >> j) & 1u) best = max_u64(best, argmax_key(x[j], (uint32_t)elem_index<VEC>(base, j)));
+    best = block_max_u64(best, sh.red);
+  } else {
+    // a NaN or +inf scaled logit scores NaN / +inf whatever its draw: the
+    // first NaN, else the first +inf, is the row's argmax (jnp.argmax); their
+    // keys exceed every finite score's
+    unsigned long long nf = 0;
+#pragma unroll
+    for (int j = 0; j < kGumbelEPT; ++j) {
+      x[j] = x[j] / rp.tp;
+      if (((valid >> j) & 1u) && (x[j] != x[j] || x[j] == INFINITY))
+        nf = max_u64(nf, argmax_key(x[j], (uint32_t)elem_index<VEC>(base, j)));
+    }
+    nf = block_max_u64(nf, sh.red);
+    if (nf) {
+      best = nf;
+    } else {
+      const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+      best = block_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, valid, -INFINITY, sh);
+    }
+  }
+  if (threadIdx.x == 0) a.cand[(size_t)b * gridDim.x + blockIdx.x] = best;
+}
+
+__global__ void __launch_bounds__(64) sample_onepass_finish_kernel(SampleArgs a, int nsub) {
+  const int b = blockIdx.x;
+  unsigned long long m = 0;
+  for (int i = threadIdx.x; i < nsub; i += 64) m = max_u64(m, a.cand[(size_t)b * nsub + i]);
+  m = wave_max_u64(m);
+  if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)m);
+}
+
 // ------------------------------------------------------------------ 5. top-p rows: finish
 // After the gumbel pass: the exact threshold tau inside the crossing bin (the
 // largest key whose weight from the top of the bin reaches the row's target),
@@ -1898,6 +1954,16 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
     }                                                                                           \
     NVJSEL_CHECK_LAUNCH(#KERN);                                                                 \
   } while (0)
+  // one pass when the call has no top-k/top-p arrays and its blocks fit one
+  // round on the device (8 per CU): a latency-bound call saves the scan and
+  // select launches; larger ones keep the seeded, pruned Gumbel pass
+  const int nsub = (vocab + kThreads * kGumbelEPT - 1) / (kThreads * kGumbelEPT);
+  if (!top_k && !top_p && NVJSEL_SAMPLE_ONEPASS && (long long)batch * nsub <= 8LL * device_cu_count()) {
+    NVJSEL_LAUNCH_CHUNK(sample_onepass_kernel, dim3(nsub, batch));
+    hipLaunchKernelGGL(sample_onepass_finish_kernel, dim3(batch), dim3(64), 0, s, a, nsub);
+    NVJSEL_CHECK_LAUNCH("sample_onepass_finish_kernel");
+    return NVJSEL_OK;
+  }
   NVJSEL_LAUNCH_CHUNK(sample_scan_kernel, grid_chunks);
   hipLaunchKernelGGL(sample_select_kernel, dim3(batch), dim3(kThreads), 0, s, a);
   NVJSEL_CHECK_LAUNCH("sample_select_kernel");

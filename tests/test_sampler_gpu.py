@@ -105,6 +105,29 @@ def test_heavy_ties_and_quantised_logits():
     check_sampled(ids, used, T, K, P, keys, ctx="ties")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_onepass_matches_pipeline(dtype):
+    """Calls without top-k/top-p arrays take the one-pass Gumbel-max; the same
+    rows passed with disabled arrays (k=0, p=1) take the scan/select/gumbel
+    pipeline.  Both are exact, so the ids must agree row for row; the oracle
+    pins them too.  Rows: greedy, several temperatures, spikes, a NaN row, a
+    +inf row, an all -inf row."""
+    B, V = 12, 50_021
+    rng = np.random.default_rng(321)
+    l = (rng.standard_normal((B, V)) * 3).astype(np.float32)
+    l[2, rng.choice(V, 5, replace=False)] += 12.0
+    l[5, [777, 40_000]] = np.nan
+    l[6, [9_000, 30_000]] = np.inf
+    l[7] = -np.inf
+    T = [0.0, 0.7, 1.0, 0.3, 2.0, 1.0, 1.0, 1.0, 0.0, 0.05, 1.0, 0.7]
+    keys = engine_keys(B, 5)
+    ids1, used, _ = _sample(l, T, keys=keys, dtype=dtype)
+    ids2, _, _ = _sample(l, T, top_k=[0] * B, top_p=[1.0] * B, keys=keys, dtype=dtype)
+    assert ids1.tolist() == ids2.tolist()
+    assert ids1[5] == 777 and ids1[6] == 9_000 and ids1[7] == 0
+    check_sampled(ids1, used, T, [0] * B, [1.0] * B, keys, ctx="onepass")
+
+
 def test_nonfinite_rows():
     B, V = 5, 4000
     rng = np.random.default_rng(7)
