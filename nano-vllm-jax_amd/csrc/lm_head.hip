@@ -58,7 +58,7 @@
 #define NVJSEL_GEMV_WAVES 4  // waves per block of the streaming GEMV
 #endif
 #ifndef NVJSEL_GEMV_DEPTH
-#define NVJSEL_GEMV_DEPTH 4  // row groups in flight per wave
+#define NVJSEL_GEMV_DEPTH 3  // row groups in flight per wave (measured: 3 > 4, 5 > 2)
 #endif
 #ifndef NVJSEL_GEMV_BPC
 #define NVJSEL_GEMV_BPC 1  // blocks per CU for the streaming GEMV (0 = occupancy)
