@@ -56,7 +56,11 @@ __device__ __forceinline__ void threefry2x32(const TfKey& k, uint32_t c0, uint32
 // the compiler's scheduler otherwise emits the chains one after another to
 // save registers, and pads every separate asm block with a wait state.
 // Only vector instructions.  Rotations are written as right-rotations by
-// 32 - r (v_alignbit_b32 x, x, x, s == rotr(x, s)).
+// 32 - r (v_alignbit_b32 x, x, x, s == rotr(x, s)).  On gfx950 a
+// three-source VALU op (v_alignbit_b32, v_add3_u32, ...) issues at about
+// half the rate of a two-source one, so the key injections use precomputed
+// sums: x1 += (k + c) is one two-source add, and x0 += k is folded with the
+// next round's x0 += x1 into one v_add3_u32.
 #define NVJSEL_TF4_ROUND(s)                                                              \
   "v_add_u32 %0, %0, %4\n\tv_add_u32 %1, %1, %5\n\tv_add_u32 %2, %2, %6\n\t"            \
   "v_add_u32 %3, %3, %7\n\t"                                                            \
@@ -64,29 +68,47 @@ __device__ __forceinline__ void threefry2x32(const TfKey& k, uint32_t c0, uint32
   "v_alignbit_b32 %6, %6, %6, " #s "\n\tv_alignbit_b32 %7, %7, %7, " #s "\n\t"         \
   "v_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\t"            \
   "v_xor_b32 %7, %7, %3\n\t"
-// key injection: x0 += ka; x1 += kb + c   (operands %8, %9, %10 = k0, k1, k2)
-#define NVJSEL_TF4_INJECT(ka, kb, c)                                                     \
-  "v_add_u32 %0, %0, " ka "\n\tv_add_u32 %1, %1, " ka "\n\tv_add_u32 %2, %2, " ka        \
-  "\n\tv_add_u32 %3, %3, " ka "\n\t"                                                     \
-  "v_add3_u32 %4, %4, " kb ", " #c "\n\tv_add3_u32 %5, %5, " kb ", " #c "\n\t"           \
-  "v_add3_u32 %6, %6, " kb ", " #c "\n\tv_add3_u32 %7, %7, " kb ", " #c "\n\t"
-// rotations {13, 15, 26, 6} and {17, 29, 16, 24} as right-rotations
+// first round after an injection: x0 += ka folded into x0 += x1
+#define NVJSEL_TF4_ROUND_K(s, ka)                                                        \
+  "v_add3_u32 %0, %0, " ka ", %4\n\tv_add3_u32 %1, %1, " ka ", %5\n\t"                  \
+  "v_add3_u32 %2, %2, " ka ", %6\n\tv_add3_u32 %3, %3, " ka ", %7\n\t"                  \
+  "v_alignbit_b32 %4, %4, %4, " #s "\n\tv_alignbit_b32 %5, %5, %5, " #s "\n\t"         \
+  "v_alignbit_b32 %6, %6, %6, " #s "\n\tv_alignbit_b32 %7, %7, %7, " #s "\n\t"         \
+  "v_xor_b32 %4, %4, %0\n\tv_xor_b32 %5, %5, %1\n\tv_xor_b32 %6, %6, %2\n\t"            \
+  "v_xor_b32 %7, %7, %3\n\t"
+// x1 += (kb + c), the sum precomputed
+#define NVJSEL_TF4_INJECT_X1(kc)                                                         \
+  "v_add_u32 %4, %4, " kc "\n\tv_add_u32 %5, %5, " kc "\n\tv_add_u32 %6, %6, " kc        \
+  "\n\tv_add_u32 %7, %7, " kc "\n\t"
+// rotations {13, 15, 26, 6} and {17, 29, 16, 24} as right-rotations; the
+// groups after an injection start with the folded round
 #define NVJSEL_TF4_ROUNDS_A NVJSEL_TF4_ROUND(19) NVJSEL_TF4_ROUND(17) NVJSEL_TF4_ROUND(6) NVJSEL_TF4_ROUND(26)
-#define NVJSEL_TF4_ROUNDS_B NVJSEL_TF4_ROUND(15) NVJSEL_TF4_ROUND(3) NVJSEL_TF4_ROUND(16) NVJSEL_TF4_ROUND(8)
+#define NVJSEL_TF4_ROUNDS_A_K(ka) \
+  NVJSEL_TF4_ROUND_K(19, ka) NVJSEL_TF4_ROUND(17) NVJSEL_TF4_ROUND(6) NVJSEL_TF4_ROUND(26)
+#define NVJSEL_TF4_ROUNDS_B_K(ka) \
+  NVJSEL_TF4_ROUND_K(15, ka) NVJSEL_TF4_ROUND(3) NVJSEL_TF4_ROUND(16) NVJSEL_TF4_ROUND(8)
 
+// Injection s (1..5) adds K[s % 3] to x0 and K[(s + 1) % 3] + s to x1, with
+// K = (k0, k1, k2): kc[s - 1] holds the x1 sums.
 __device__ __forceinline__ void threefry4_rounds(uint32_t (&x0)[4], uint32_t (&x1)[4], uint32_t k0, uint32_t k1,
                                                  uint32_t k2) {
-  asm volatile(NVJSEL_TF4_ROUNDS_A NVJSEL_TF4_INJECT("%9", "%10", 1)
-               NVJSEL_TF4_ROUNDS_B NVJSEL_TF4_INJECT("%10", "%8", 2)
-               NVJSEL_TF4_ROUNDS_A NVJSEL_TF4_INJECT("%8", "%9", 3)
-               NVJSEL_TF4_ROUNDS_B NVJSEL_TF4_INJECT("%9", "%10", 4)
-               NVJSEL_TF4_ROUNDS_A NVJSEL_TF4_INJECT("%10", "%8", 5)
+  uint32_t kc1 = k2 + 1u, kc2 = k0 + 2u, kc3 = k1 + 3u, kc4 = k2 + 4u, kc5 = k0 + 5u;
+  asm volatile(NVJSEL_TF4_ROUNDS_A NVJSEL_TF4_INJECT_X1("%11")
+               NVJSEL_TF4_ROUNDS_B_K("%9") NVJSEL_TF4_INJECT_X1("%12")
+               NVJSEL_TF4_ROUNDS_A_K("%10") NVJSEL_TF4_INJECT_X1("%13")
+               NVJSEL_TF4_ROUNDS_B_K("%8") NVJSEL_TF4_INJECT_X1("%14")
+               NVJSEL_TF4_ROUNDS_A_K("%9")
+               "v_add_u32 %0, %0, %10\n\tv_add_u32 %1, %1, %10\n\tv_add_u32 %2, %2, %10\n\t"
+               "v_add_u32 %3, %3, %10\n\t" NVJSEL_TF4_INJECT_X1("%15")
                : "+v"(x0[0]), "+v"(x0[1]), "+v"(x0[2]), "+v"(x0[3]), "+v"(x1[0]), "+v"(x1[1]), "+v"(x1[2]),
-                 "+v"(x1[3]), "+v"(k0), "+v"(k1), "+v"(k2));  // in-out: no key word shares x0's register
+                 "+v"(x1[3]), "+v"(k0), "+v"(k1), "+v"(k2), "+v"(kc1), "+v"(kc2), "+v"(kc3), "+v"(kc4),
+                 "+v"(kc5));  // in-out: no key word shares a state word's register
 }
 #undef NVJSEL_TF4_ROUNDS_A
-#undef NVJSEL_TF4_ROUNDS_B
-#undef NVJSEL_TF4_INJECT
+#undef NVJSEL_TF4_ROUNDS_A_K
+#undef NVJSEL_TF4_ROUNDS_B_K
+#undef NVJSEL_TF4_INJECT_X1
+#undef NVJSEL_TF4_ROUND_K
 #undef NVJSEL_TF4_ROUND
 
 template <int N>
@@ -100,20 +122,21 @@ __device__ __forceinline__ void random_bits32_n(const TfKey& k, const uint32_t (
     for (int e = 0; e < N; ++e) out[e] = x0[e] ^ x1[e];
     return;
   }
+  const uint32_t kc[5] = {k.k2 + 1u, k.k0 + 2u, k.k1 + 3u, k.k2 + 4u, k.k0 + 5u};
 #define NVJSEL_TF_ROUND_N(r) \
   _Pragma("unroll") for (int e = 0; e < N; ++e) { x0[e] += x1[e]; x1[e] = rotl32(x1[e], r); x1[e] ^= x0[e]; }
-#define NVJSEL_TF_INJECT_N(a, b, c) \
-  _Pragma("unroll") for (int e = 0; e < N; ++e) { x0[e] += (a); x1[e] += (b) + (uint32_t)(c); }
+#define NVJSEL_TF_INJECT_N(a, s) \
+  _Pragma("unroll") for (int e = 0; e < N; ++e) { x0[e] += (a); x1[e] += kc[(s) - 1]; }
   NVJSEL_TF_ROUND_N(13) NVJSEL_TF_ROUND_N(15) NVJSEL_TF_ROUND_N(26) NVJSEL_TF_ROUND_N(6)
-  NVJSEL_TF_INJECT_N(k.k1, k.k2, 1)
+  NVJSEL_TF_INJECT_N(k.k1, 1)
   NVJSEL_TF_ROUND_N(17) NVJSEL_TF_ROUND_N(29) NVJSEL_TF_ROUND_N(16) NVJSEL_TF_ROUND_N(24)
-  NVJSEL_TF_INJECT_N(k.k2, k.k0, 2)
+  NVJSEL_TF_INJECT_N(k.k2, 2)
   NVJSEL_TF_ROUND_N(13) NVJSEL_TF_ROUND_N(15) NVJSEL_TF_ROUND_N(26) NVJSEL_TF_ROUND_N(6)
-  NVJSEL_TF_INJECT_N(k.k0, k.k1, 3)
+  NVJSEL_TF_INJECT_N(k.k0, 3)
   NVJSEL_TF_ROUND_N(17) NVJSEL_TF_ROUND_N(29) NVJSEL_TF_ROUND_N(16) NVJSEL_TF_ROUND_N(24)
-  NVJSEL_TF_INJECT_N(k.k1, k.k2, 4)
+  NVJSEL_TF_INJECT_N(k.k1, 4)
   NVJSEL_TF_ROUND_N(13) NVJSEL_TF_ROUND_N(15) NVJSEL_TF_ROUND_N(26) NVJSEL_TF_ROUND_N(6)
-  NVJSEL_TF_INJECT_N(k.k2, k.k0, 5)
+  NVJSEL_TF_INJECT_N(k.k2, 5)
 #undef NVJSEL_TF_ROUND_N
 #undef NVJSEL_TF_INJECT_N
 #pragma unroll
