@@ -1582,7 +1582,10 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     // grid bin tb_c - d, the row's bin D is grid bin TB - D (TB = max tb_c)
     const int TB = (int)(uint32_t)(block_max_u64((unsigned long long)(uint32_t)(tbm ^ INT_MIN), s.red)) ^ INT_MIN;
     constexpr int PER = kToppBins / kThreads;
-    constexpr int U = 32;  // chunks whose loads are in flight together
+    // U chunks' loads in flight together, issued unconditionally (clamped
+    // addresses, masked after the load): a guarded load per bin compiles to
+    // a branch per load, which made this merge the row's longest phase
+    constexpr int U = 16;
     unsigned long long h[PER] = {};
     for (int c0 = 0; c0 < NC; c0 += U) {
       unsigned long long v[U][PER];
@@ -1591,11 +1594,12 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
         const int c = c0 + u;
         const int tbc = c < NC ? s.tb[c] : INT_MIN;
         const int sft = (tbc == INT_MIN || TB == INT_MIN) ? kToppBins * 2 : TB - tbc;
-        const unsigned long long* ch = a.topp_chunk_hist + ((size_t)b * NC + c) * kToppBins;
+        const unsigned long long* ch = a.topp_chunk_hist + ((size_t)b * NC + (c < NC ? c : NC - 1)) * kToppBins;
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
-          const int d = (int)threadIdx.x * PER + q - sft;
-          v[u][q] = d >= 0 ? ch[d] : 0ull;
+          const int d = (int)threadIdx.x * PER + q - sft;  // < kToppBins: sft >= 0
+          v[u][q] = ch[d >= 0 ? d : 0];
+          v[u][q] = d >= 0 ? v[u][q] : 0ull;
         }
       }
 #pragma unroll
