@@ -154,7 +154,7 @@ def build_configs(torch, which):
                                    keys.data_ptr(), None, out.data_ptr(), w.data_ptr(), w.numel(), stream())
             assert rc == 0, lib.nvjsel_last_error()
 
-        cfgs.append(Cfg("c2_temperature_b8", B, B * V_FULL * 4, launch, "sample_gumbel_kernel",
+        cfgs.append(Cfg("c2_temperature_b8", B, B * V_FULL * 4, launch, "sample_onepass_kernel",
                         "temperature sampling, f32 logits [8,248320], T=0.7"))
 
     if "c3" in which:
