@@ -88,7 +88,7 @@ struct SampleArgs {
   uint32_t* cand_count_a;          // [B, nchunks] tier A: the list's first entries, those >= cand_floor_a
   float* cand_floor_a;             // [B, nchunks]
   float* cand_floor;               // [B, nchunks] logit floor of each chunk's candidates
-  unsigned long long* cand;        // [B, nchunks, kCandCap]
+  unsigned long long* cand;        // [B, nchunks, kCandCap]; one-pass calls: [B, sub-chunks] block keys
   unsigned long long* topp_chunk_hist;  // [B, nchunks, kToppBins] chunk histograms (top-p-only rows)
   int32_t* topp_chunk_tb;          // [B, nchunks] grid bin of each chunk's maximum
   int32_t* row_ib;                 // [B] top-p rows: grid bin of the crossing (INT_MIN: none)
