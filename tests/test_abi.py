@@ -135,3 +135,18 @@ def test_mtp_registry_and_shape_contract():
     import nvjsel
     with pytest.raises(ValueError, match=r"\[B, T, H\]"):
         nvjsel.mtp_greedy_top1_token_ids(torch.zeros(2, 8), torch.zeros(16, 8, dtype=torch.bfloat16))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """Every box has one GPU: bench.py --gpus N > 1 exits with a JSON message
+    (status 2) before touching a device."""
+    import json
+    import subprocess
+    import sys
+
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    msg = json.loads(r.stdout.strip().splitlines()[-1])
+    assert msg["n_gpus"] == 2 and "one GPU" in msg["error"]
