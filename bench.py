@@ -4,17 +4,25 @@ Prints ONE JSON line.  The headline workload (``value``) is BASELINE config 0:
 greedy LM-head top-1 at B=1, V=248320, H=1024, bf16 -- the configuration the
 metric's HBM-roofline target is quoted on.  The other four BASELINE configs
 (temperature sampling B=8, top-k/top-p B=64, fused LM-head + Gumbel B=64,
-mixed per-row parameters B=256) are timed in the same run and reported under
-``per_config``.  Inputs are synthetic, seeded, and resident in HBM before the
-timed region; each step is one call of the C ABI on torch's current stream.
+mixed per-row parameters B=256) and the extension workloads (x*) are timed in
+the same run and reported under ``per_config``.
 
-``cpu_baseline`` times the numpy oracle (fp32 matmul + argmax) for config 0 on
-the host cores, on a bounded sample.
+Inputs are synthetic, seeded per config (``make_inputs``, which the GPU parity
+tests reuse so they check exactly what is timed), and resident in HBM before
+the timed region.  Every config rotates through enough copies of its inputs
+to exceed the 256 MB MALL (cold numbers, the headline); the warm numbers
+reuse one copy.  Each timed region is exactly ``--steps`` calls of the C ABI
+on torch's current stream, bracketed by device synchronisation; it is
+repeated ``--repeats`` times and the median and p90 per-step times are
+reported.
+
+``cpu_baseline`` times the numpy oracle on the host cores, on a bounded sample
+of each config's own inputs (kind "port": the build's restatement of the
+reference expressions; jax is not installed).
 """
 from __future__ import annotations
 
 import argparse
-import ctypes
 import json
 import os
 import sys
@@ -26,17 +34,24 @@ for _p in (ROOT, os.path.join(ROOT, "nano-vllm-jax_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK = 8.0e12  # bytes/s, MI355X
+MALL_BYTES = 256 * 1024 * 1024
 V_FULL, H_FULL = 248320, 1024
+ALL_CONFIGS = "c1,c2,c3,c4,c5,x1,x2"
+# per-config generator seeds: each config's inputs depend only on its own seed
+SEEDS = {"c1": 101, "c2": 102, "c3": 103, "c4": 104, "c5": 105, "x1": 201, "x2": 202}
 
 
 def _parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,x1,x2")
-    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bounded CPU-baseline sample")
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--repeats", type=int, default=5, help="timed regions per config (median / p90)")
+    ap.add_argument("--configs", default=ALL_CONFIGS)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bounded CPU-baseline sample for C1")
+    ap.add_argument("--cpu-seconds-other", type=float, default=3.0, help="... for each other config")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-warm", action="store_true", help="skip the warm (single-copy) timings")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 512 MiB device copy (rocprofv3 counter calibration)")
     return ap.parse_args()
@@ -68,15 +83,17 @@ def calibrate_copy(torch):
     print(json.dumps({"calibration_copy_bytes": n}))
 
 
-class Cfg:
-    """One BASELINE config: device inputs + a launch closure + algorithmic bytes."""
+# ----------------------------------------------------------------------------- inputs
 
-    def __init__(self, name, batch, nbytes, launch, kernel, desc):
-        self.name, self.batch, self.nbytes, self.launch, self.kernel, self.desc = (
-            name, batch, nbytes, launch, kernel, desc)
+def _gen(torch, dev, name):
+    g = torch.Generator(device=dev)
+    g.manual_seed(SEEDS[name])
+    return g
 
 
 def _zipf_rows(torch, gen, batch, vocab, s_lo, s_hi, noise_sd, dev):
+    """log Zipf(s) profile (s uniform in [s_lo, s_hi] per row), permuted per
+    row, plus N(0, noise_sd) noise, f32."""
     ranks = torch.arange(1, vocab + 1, device=dev, dtype=torch.float32)
     s = s_lo + (s_hi - s_lo) * torch.rand(batch, 1, device=dev, generator=gen)
     lp = -s * torch.log(ranks)[None, :]
@@ -86,216 +103,320 @@ def _zipf_rows(torch, gen, batch, vocab, s_lo, s_hi, noise_sd, dev):
     return lp + noise_sd * torch.randn(batch, vocab, device=dev, generator=gen)
 
 
-def build_configs(torch, which):
+def _engine_keys(torch, batch, dev):
+    """The executor's keys fold_in(fold_in(PRNGKey(0), slot = row), counter = 0), derived on device."""
+    from nvjsel import derive_rng_keys
+
+    keys, _ = derive_rng_keys(torch.arange(batch, dtype=torch.int32, device=dev),
+                              torch.zeros(batch, dtype=torch.int32, device=dev))
+    return keys
+
+
+def _seed_keys(torch, batch, dev):
+    """PRNGKey(seed = row) = (0, row) for 32-bit seeds."""
+    k = torch.zeros(batch, 2, dtype=torch.int32, device=dev)
+    k[:, 1] = torch.arange(batch, dtype=torch.int32, device=dev)
+    return k
+
+
+def lm_weight(torch, dev, seed=7):
+    """Tied LM-head table [V, H] bf16 ~N(0, 0.02)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    return (torch.randn(V_FULL, H_FULL, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+
+
+def make_inputs(torch, name, dev):
+    """Device inputs of one workload (besides the LM-head weight), as a dict."""
+    gen = _gen(torch, dev, name)
+    if name in ("c1", "x1"):
+        d = {"batch": 1}
+        if name == "c1":
+            d["hidden"] = torch.randn(1, H_FULL, device=dev, generator=gen).to(torch.bfloat16)
+        else:
+            d["hidden"] = (torch.randn(1, H_FULL, device=dev, generator=gen) * 4).to(torch.bfloat16)
+            d["norm_weight"] = (torch.randn(H_FULL, device=dev, generator=gen) * 0.1).float()
+        return d
+    if name == "c2":
+        B = 8
+        l = torch.randn(B, V_FULL, device=dev, generator=gen) * 3
+        for b in range(B):
+            idx = torch.randperm(V_FULL, device=dev, generator=gen)[:5]
+            l[b, idx] += 12.0
+        return {"batch": B, "logits": l.contiguous(), "temperature": torch.full((B,), 0.7, device=dev),
+                "top_k": None, "top_p": None, "keys": _seed_keys(torch, B, dev)}
+    if name in ("c3", "x2"):
+        B = 64
+        l = _zipf_rows(torch, gen, B, V_FULL, 1.1, 1.1, 0.5, dev).float().contiguous()
+        d = {"batch": B, "logits": l}
+        if name == "c3":
+            d.update(temperature=torch.full((B,), 0.8, device=dev),
+                     top_k=torch.full((B,), 50, dtype=torch.int32, device=dev),
+                     top_p=torch.full((B,), 0.9, device=dev), keys=_engine_keys(torch, B, dev))
+        else:
+            d["k"] = 50
+        return d
+    if name == "c4":
+        B = 64
+        return {"batch": B, "hidden": torch.randn(B, H_FULL, device=dev, generator=gen).to(torch.bfloat16),
+                "temperature": torch.ones(B, device=dev), "keys": _engine_keys(torch, B, dev)}
+    if name == "c5":
+        B = 256
+        l = _zipf_rows(torch, gen, B, V_FULL, 1.05, 1.3, 1.0, dev).to(torch.bfloat16).contiguous()
+
+        def choice(vals, dt):
+            return torch.tensor(vals, device=dev, dtype=dt)[
+                torch.randint(0, len(vals), (B,), device=dev, generator=gen)]
+
+        return {"batch": B, "logits": l, "temperature": choice([0.0, 0.6, 1.0], torch.float32),
+                "top_k": choice([0, 20, 100], torch.int32), "top_p": choice([1.0, 0.95, 0.8], torch.float32),
+                "keys": _engine_keys(torch, B, dev)}
+    raise KeyError(name)
+
+
+# ----------------------------------------------------------------------------- workloads
+
+class Cfg:
+    """One workload: launch(copy index) runs one step on input copy i."""
+
+    def __init__(self, name, batch, nbytes, launch, ncopies, kernel, desc, cpu=None):
+        self.name, self.batch, self.nbytes, self.launch = name, batch, nbytes, launch
+        self.ncopies, self.kernel, self.desc, self.cpu = ncopies, kernel, desc, cpu
+
+
+def _copies_for(nbytes):
+    """Input copies whose total exceeds the MALL (at least 2)."""
+    return max(2, -(-(MALL_BYTES + 1) // max(1, nbytes)))
+
+
+def build_configs(torch, which, with_cpu):
     import numpy as np
 
     from nvjsel import _lib
 
     lib = _lib.load()
     dev = torch.device("cuda:0")
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(0)
     stream = lambda: torch.cuda.current_stream(dev).cuda_stream  # noqa: E731
     cfgs = []
-    W = None
+    Wcache = []
 
     def weights():
-        nonlocal W
-        if W is None:
-            # two copies, alternated per step, so the 508 MB table cannot sit in the 256 MB MALL
-            W = [(torch.randn(V_FULL, H_FULL, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
-                 for _ in range(2)]
-        return W
-
-    def keys_for(batch, row_seed=False):
-        if row_seed:  # PRNGKey(seed) = (0, seed) for 32-bit seeds
-            k = np.stack([np.zeros(batch, np.uint32), np.arange(batch, dtype=np.uint32)], axis=1)
-            return torch.from_numpy(k.view(np.int32).copy()).to(dev)
-        # the executor's keys fold_in(fold_in(PRNGKey(0), slot), counter), derived on device
-        from nvjsel import derive_rng_keys
-
-        keys, _ = derive_rng_keys(torch.arange(batch, dtype=torch.int32, device=dev),
-                                  torch.zeros(batch, dtype=torch.int32, device=dev))
-        return keys
+        # two copies, alternated per step, so the 508 MB table cannot sit in the 256 MB MALL
+        if not Wcache:
+            Wcache.extend([lm_weight(torch, dev, 7), lm_weight(torch, dev, 8)])
+        return Wcache
 
     def ws(nbytes):
         return torch.zeros(max(int(nbytes), 4096), dtype=torch.uint8, device=dev)
 
+    def ck(rc):
+        if rc != 0:
+            raise RuntimeError(lib.nvjsel_last_error().decode())
+
+    def sampler_cfg(name, d, kernel, desc):
+        B = d["batch"]
+        n = _copies_for(d["logits"].numel() * d["logits"].element_size())
+        Ls = [d["logits"]] + [d["logits"].clone() for _ in range(n - 1)]
+        dt = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[d["logits"].dtype]
+        out = torch.empty(B, dtype=torch.int32, device=dev)
+        w = ws(lib.nvjsel_sample_workspace_size(B, V_FULL))
+        t, k, p, keys = d["temperature"], d["top_k"], d["top_p"], d["keys"]
+        kp = k.data_ptr() if k is not None else None
+        pp = p.data_ptr() if p is not None else None
+
+        def launch(i):
+            ck(lib.nvjsel_sample(Ls[i].data_ptr(), dt, B, V_FULL, V_FULL, t.data_ptr(), kp, pp, keys.data_ptr(),
+                                 None, out.data_ptr(), w.data_ptr(), w.numel(), stream()))
+
+        cpu = (lambda secs, d=d: cpu_sampler(d, secs)) if with_cpu else None
+        return Cfg(name, B, d["logits"].numel() * d["logits"].element_size(), launch, n, kernel, desc, cpu)
+
     if "c1" in which:
         Ws = weights()
-        h = torch.randn(1, H_FULL, device=dev, generator=gen).to(torch.bfloat16)
+        d = make_inputs(torch, "c1", dev)
+        h = d["hidden"]
         out = torch.empty(1, dtype=torch.int32, device=dev)
         w = ws(lib.nvjsel_lm_head_workspace_size(1))
-        state = {"i": 0}
 
-        def launch(Ws=Ws, h=h, out=out, w=w, state=state):
-            Wi = Ws[state["i"] & 1]
-            state["i"] += 1
-            rc = lib.nvjsel_lm_head_top1(h.data_ptr(), 1, Wi.data_ptr(), 1, 0, 1, H_FULL, V_FULL, 1,
-                                         out.data_ptr(), None, w.data_ptr(), w.numel(), stream())
-            assert rc == 0, lib.nvjsel_last_error()
+        def launch(i, Ws=Ws, h=h, out=out, w=w):
+            ck(lib.nvjsel_lm_head_top1(h.data_ptr(), 1, Ws[i].data_ptr(), 1, 0, 1, H_FULL, V_FULL, 1,
+                                       out.data_ptr(), None, w.data_ptr(), w.numel(), stream()))
 
-        cfgs.append(Cfg("c1_greedy_lm_head_b1", 1, V_FULL * H_FULL * 2 + H_FULL * 2, launch,
-                        "lm_head_gemv_kernel", "greedy LM-head top-1, B=1, bf16 W[248320,1024]"))
+        cfgs.append(Cfg("c1_greedy_lm_head_b1", 1, V_FULL * H_FULL * 2 + H_FULL * 2, launch, 2,
+                        "lm_head_gemv_kernel", "greedy LM-head top-1, B=1, bf16 W[248320,1024]",
+                        (lambda secs, h=h: cpu_lm_head(h, None, secs)) if with_cpu else None))
 
     if "c2" in which:
-        B = 8
-        l = torch.randn(B, V_FULL, device=dev, generator=gen) * 3
-        for b in range(B):
-            idx = torch.randperm(V_FULL, device=dev, generator=gen)[:5]
-            l[b, idx] += 12.0
-        t = torch.full((B,), 0.7, device=dev)
-        keys = keys_for(B, row_seed=True)
-        out = torch.empty(B, dtype=torch.int32, device=dev)
-        w = ws(lib.nvjsel_sample_workspace_size(B, V_FULL))
-
-        def launch(l=l, t=t, keys=keys, out=out, w=w, B=B):
-            rc = lib.nvjsel_sample(l.data_ptr(), 0, B, V_FULL, V_FULL, t.data_ptr(), None, None,
-                                   keys.data_ptr(), None, out.data_ptr(), w.data_ptr(), w.numel(), stream())
-            assert rc == 0, lib.nvjsel_last_error()
-
-        cfgs.append(Cfg("c2_temperature_b8", B, B * V_FULL * 4, launch, "sample_onepass_kernel",
-                        "temperature sampling, f32 logits [8,248320], T=0.7"))
-
+        cfgs.append(sampler_cfg("c2_temperature_b8", make_inputs(torch, "c2", dev), "sample_onepass_kernel",
+                                "temperature sampling, f32 logits [8,248320], T=0.7"))
     if "c3" in which:
-        B = 64
-        l = _zipf_rows(torch, gen, B, V_FULL, 1.1, 1.1, 0.5, dev).float().contiguous()
-        t = torch.full((B,), 0.8, device=dev)
-        k = torch.full((B,), 50, dtype=torch.int32, device=dev)
-        p = torch.full((B,), 0.9, device=dev)
-        keys = keys_for(B)
-        out = torch.empty(B, dtype=torch.int32, device=dev)
-        w = ws(lib.nvjsel_sample_workspace_size(B, V_FULL))
-
-        def launch(l=l, t=t, k=k, p=p, keys=keys, out=out, w=w, B=B):
-            rc = lib.nvjsel_sample(l.data_ptr(), 0, B, V_FULL, V_FULL, t.data_ptr(), k.data_ptr(),
-                                   p.data_ptr(), keys.data_ptr(), None, out.data_ptr(), w.data_ptr(),
-                                   w.numel(), stream())
-            assert rc == 0, lib.nvjsel_last_error()
-
-        cfgs.append(Cfg("c3_topk_topp_b64", B, B * V_FULL * 4, launch, "sample_select_kernel",
-                        "top-k=50 / top-p=0.9 / T=0.8, f32 logits [64,248320] Zipf(1.1)"))
+        cfgs.append(sampler_cfg("c3_topk_topp_b64", make_inputs(torch, "c3", dev), "sample_scan_kernel",
+                                "top-k=50 / top-p=0.9 / T=0.8, f32 logits [64,248320] Zipf(1.1)"))
 
     if "c4" in which:
-        B = 64
         Ws = weights()
-        h = torch.randn(B, H_FULL, device=dev, generator=gen).to(torch.bfloat16)
-        t = torch.ones(B, device=dev)
-        keys = keys_for(B)
+        d = make_inputs(torch, "c4", dev)
+        B, h, t, keys = d["batch"], d["hidden"], d["temperature"], d["keys"]
         out = torch.empty(B, dtype=torch.int32, device=dev)
         w = ws(lib.nvjsel_lm_head_workspace_size(B))
-        state = {"i": 0}
 
-        def launch(h=h, t=t, keys=keys, out=out, w=w, B=B, Ws=Ws, state=state):
-            Wi = Ws[state["i"] & 1]
-            state["i"] += 1
-            rc = lib.nvjsel_lm_head_sample(h.data_ptr(), 1, Wi.data_ptr(), 1, 0, B, H_FULL, V_FULL, 1,
-                                           t.data_ptr(), keys.data_ptr(), out.data_ptr(), w.data_ptr(),
-                                           w.numel(), stream())
-            assert rc == 0, lib.nvjsel_last_error()
+        def launch(i, h=h, t=t, keys=keys, out=out, w=w, B=B, Ws=Ws):
+            ck(lib.nvjsel_lm_head_sample(h.data_ptr(), 1, Ws[i].data_ptr(), 1, 0, B, H_FULL, V_FULL, 1,
+                                         t.data_ptr(), keys.data_ptr(), out.data_ptr(), w.data_ptr(),
+                                         w.numel(), stream()))
 
-        cfgs.append(Cfg("c4_fused_lm_head_gumbel_b64", B, V_FULL * H_FULL * 2 + B * H_FULL * 2, launch,
-                        "lm_head_tile_kernel", "fused LM-head + Gumbel-max, B=64, T=1"))
+        cfgs.append(Cfg("c4_fused_lm_head_gumbel_b64", B, V_FULL * H_FULL * 2 + B * H_FULL * 2, launch, 2,
+                        "lm_head_tile_kernel", "fused LM-head + Gumbel-max, B=64, T=1",
+                        (lambda secs, h=h, d=d: cpu_lm_head(h, d, secs)) if with_cpu else None))
 
     if "c5" in which:
-        B = 256
-        l = _zipf_rows(torch, gen, B, V_FULL, 1.05, 1.3, 1.0, dev).to(torch.bfloat16).contiguous()
-        choice = lambda vals, dt: torch.tensor(vals, device=dev, dtype=dt)[  # noqa: E731
-            torch.randint(0, len(vals), (B,), device=dev, generator=gen)]
-        t = choice([0.0, 0.6, 1.0], torch.float32)
-        k = choice([0, 20, 100], torch.int32)
-        p = choice([1.0, 0.95, 0.8], torch.float32)
-        keys = keys_for(B)
-        out = torch.empty(B, dtype=torch.int32, device=dev)
-        w = ws(lib.nvjsel_sample_workspace_size(B, V_FULL))
+        cfgs.append(sampler_cfg("c5_mixed_b256_bf16", make_inputs(torch, "c5", dev), "sample_scan_kernel",
+                                "mixed per-row T/top-k/top-p, bf16 logits [256,248320]"))
 
-        def launch(l=l, t=t, k=k, p=p, keys=keys, out=out, w=w, B=B):
-            rc = lib.nvjsel_sample(l.data_ptr(), 1, B, V_FULL, V_FULL, t.data_ptr(), k.data_ptr(),
-                                   p.data_ptr(), keys.data_ptr(), None, out.data_ptr(), w.data_ptr(),
-                                   w.numel(), stream())
-            assert rc == 0, lib.nvjsel_last_error()
-
-        cfgs.append(Cfg("c5_mixed_b256_bf16", B, B * V_FULL * 2, launch, "sample_gumbel_kernel",
-                        "mixed per-row T/top-k/top-p, bf16 logits [256,248320]"))
     if "x1" in which:  # the final-RMSNorm prologue fused into the C1 launch
         Ws = weights()
-        h = (torch.randn(1, H_FULL, device=dev, generator=gen) * 4).to(torch.bfloat16)
-        nw = (torch.randn(H_FULL, device=dev, generator=gen) * 0.1).float()
+        d = make_inputs(torch, "x1", dev)
+        h, nw = d["hidden"], d["norm_weight"]
         out = torch.empty(1, dtype=torch.int32, device=dev)
         w = ws(lib.nvjsel_lm_head_prenorm_workspace_size(1, H_FULL))
-        state = {"i": 0}
 
-        def launch(Ws=Ws, h=h, nw=nw, out=out, w=w, state=state):
-            Wi = Ws[state["i"] & 1]
-            state["i"] += 1
-            rc = lib.nvjsel_lm_head_top1_prenorm(h.data_ptr(), 1, nw.data_ptr(), 0, 1e-6, 1, Wi.data_ptr(), 1, 0,
-                                                 1, H_FULL, V_FULL, 1, out.data_ptr(), None, w.data_ptr(),
-                                                 w.numel(), stream())
-            assert rc == 0, lib.nvjsel_last_error()
+        def launch(i, Ws=Ws, h=h, nw=nw, out=out, w=w):
+            ck(lib.nvjsel_lm_head_top1_prenorm(h.data_ptr(), 1, nw.data_ptr(), 0, 1e-6, 1, Ws[i].data_ptr(), 1, 0,
+                                               1, H_FULL, V_FULL, 1, out.data_ptr(), None, w.data_ptr(),
+                                               w.numel(), stream()))
 
-        cfgs.append(Cfg("x1_prenorm_greedy_lm_head_b1", 1, V_FULL * H_FULL * 2 + H_FULL * 2, launch,
+        cfgs.append(Cfg("x1_prenorm_greedy_lm_head_b1", 1, V_FULL * H_FULL * 2 + H_FULL * 2, launch, 2,
                         "lm_head_gemv_kernel", "C1 with the final RMSNorm applied in the launch (bf16 act)"))
 
     if "x2" in which:  # top-k values/indices of the verifier route on the C3 logits shape
-        B, K = 64, 50
-        l = _zipf_rows(torch, gen, B, V_FULL, 1.1, 1.1, 0.5, dev).float().contiguous()
+        d = make_inputs(torch, "x2", dev)
+        B, K = d["batch"], d["k"]
+        n = _copies_for(d["logits"].numel() * 4)
+        Ls = [d["logits"]] + [d["logits"].clone() for _ in range(n - 1)]
         vals = torch.empty(B, K, dtype=torch.float32, device=dev)
         idx = torch.empty(B, K, dtype=torch.int32, device=dev)
         w = ws(lib.nvjsel_topk_workspace_size(B, V_FULL))
 
-        def launch(l=l, vals=vals, idx=idx, w=w, B=B, K=K):
-            rc = lib.nvjsel_topk(l.data_ptr(), 0, B, V_FULL, V_FULL, K, vals.data_ptr(), idx.data_ptr(),
-                                 w.data_ptr(), w.numel(), stream())
-            assert rc == 0, lib.nvjsel_last_error()
+        def launch(i, Ls=Ls, vals=vals, idx=idx, w=w, B=B, K=K):
+            ck(lib.nvjsel_topk(Ls[i].data_ptr(), 0, B, V_FULL, V_FULL, K, vals.data_ptr(), idx.data_ptr(),
+                               w.data_ptr(), w.numel(), stream()))
 
-        cfgs.append(Cfg("x2_topk50_b64", B, B * V_FULL * 4, launch, "topk_select_kernel",
+        cfgs.append(Cfg("x2_topk50_b64", B, B * V_FULL * 4, launch, n, "sample_scan_kernel",
                         "top-k values+indices k=50, f32 logits [64,248320] Zipf(1.1)"))
     torch.cuda.synchronize()
+    del np
     return cfgs
 
 
-def time_config(torch, cfg, steps, warmup):
-    for _ in range(warmup):
-        cfg.launch()
-    torch.cuda.synchronize()
+# ----------------------------------------------------------------------------- timing
+
+def time_region(torch, cfg, steps, ncopies):
+    """One timed region: exactly `steps` calls, synchronised on both sides."""
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     start.record()
-    for _ in range(steps):
-        cfg.launch()
+    for s in range(steps):
+        cfg.launch(s % ncopies)
     stop.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / steps
-    return ms
+    return start.elapsed_time(stop) / steps
 
 
-def cpu_baseline_c1(seconds):
-    """numpy oracle for config 0 (fp32 matmul + argmax) on the host cores."""
-    import numpy as np
+def time_config(torch, cfg, steps, warmup, repeats, ncopies):
+    for s in range(warmup):
+        cfg.launch(s % ncopies)
+    ms = sorted(time_region(torch, cfg, steps, ncopies) for _ in range(repeats))
+    med = ms[len(ms) // 2] if len(ms) % 2 else 0.5 * (ms[len(ms) // 2 - 1] + ms[len(ms) // 2])
+    p90 = ms[min(len(ms) - 1, int(round(0.9 * (len(ms) - 1))))]
+    return med, p90, ms
 
+
+# ----------------------------------------------------------------------------- CPU baselines
+
+def _threads():
     try:
         from threadpoolctl import threadpool_info
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        return int(max([i.get("num_threads", 1) for i in threadpool_info()] or [1]))
     except Exception:
-        threads = len(os.sched_getaffinity(0))
-    rng = np.random.default_rng(0)
-    h = rng.standard_normal((1, H_FULL)).astype(np.float32)
-    W = (rng.standard_normal((V_FULL, H_FULL), dtype=np.float32) * 0.02)
-    np.argmax(h @ W.T, axis=1)  # warm
+        return len(os.sched_getaffinity(0))
+
+
+def _bounded(fn, seconds):
+    fn()  # warm
     n, t0 = 0, time.perf_counter()
     while True:
-        np.argmax(h @ W.T, axis=1)
+        fn()
         n += 1
         el = time.perf_counter() - t0
         if el >= seconds:
-            break
-    per = el / n
-    return {"value": 1.0 / per, "unit": "tokens/s", "cores": int(threads), "kind": "port",
-            "sample": f"{n} calls of numpy fp32 [1,1024]x[1024,248320] matmul + argmax "
-                      f"({el:.1f} s); threads = BLAS pool size",
-            "ms_per_call": per * 1e3}
+            return el / n, n, el
 
+
+def cpu_lm_head(hidden, sample_inputs, seconds):
+    """numpy oracle for the LM-head configs: fp32 matmul of the config's own
+    hidden against a seeded W [248320,1024] + argmax (greedy); for the fused
+    sampling config also the Gumbel draws (numpy Threefry) of a bounded subset
+    of rows, scaled to the batch."""
+    import numpy as np
+
+    from oracle import jax_random as jr
+    from oracle import selection as sel
+
+    rng = np.random.default_rng(0)
+    h = hidden.float().cpu().numpy()
+    W = rng.standard_normal((V_FULL, H_FULL), dtype=np.float32) * np.float32(0.02)
+    per, n, el = _bounded(lambda: np.argmax(h @ W.T, axis=1), seconds)
+    B = h.shape[0]
+    sample = f"{n} calls of numpy fp32 [{B},1024]x[1024,248320] matmul + argmax ({el:.1f} s)"
+    if sample_inputs is not None:
+        keys = sample_inputs["keys"].cpu().numpy().view(np.uint32)
+        z = (h[:4] @ W.T).astype(np.float32)
+        rows = min(4, B)
+
+        def draws():
+            for b in range(rows):
+                x = sel.scale_logits(z[b], 1.0)
+                jr.argmax_first(x + jr.gumbel((keys[b, 0], keys[b, 1]), V_FULL))
+
+        per_rows, n2, el2 = _bounded(draws, max(1.0, seconds / 2))
+        per += per_rows / rows * B
+        sample += f"; + Gumbel-max of {rows} rows x {n2} ({el2:.1f} s) scaled to {B} rows"
+    return {"value": round(B / per, 2), "unit": "tokens/s", "cores": _threads(), "kind": "port",
+            "sample": sample + "; threads = BLAS pool size", "ms_per_step": round(per * 1e3, 3)}
+
+
+def cpu_sampler(d, seconds):
+    """numpy oracle (oracle.selection.sample_rows) on a bounded subset of the
+    config's own rows, scaled to the batch (the reference has no CPU top-k /
+    top-p sampler: this is the build's restatement, labelled as such)."""
+    import numpy as np
+
+    from oracle import selection as sel
+
+    B = d["batch"]
+    logits = d["logits"].float().cpu().numpy()
+    T = d["temperature"].cpu().numpy()
+    K = d["top_k"].cpu().numpy() if d["top_k"] is not None else np.zeros(B, np.int32)
+    P = d["top_p"].cpu().numpy() if d["top_p"] is not None else np.ones(B, np.float32)
+    keys = d["keys"].cpu().numpy().view(np.uint32)
+    rows = []
+    t0, per_row = time.perf_counter(), []
+    for b in range(B):  # a bounded number of whole rows, in order
+        s = time.perf_counter()
+        sel.sample_rows(logits[b:b + 1], T[b:b + 1], K[b:b + 1], P[b:b + 1], keys[b:b + 1])
+        per_row.append(time.perf_counter() - s)
+        rows.append(b)
+        if time.perf_counter() - t0 >= seconds:
+            break
+    per = float(np.mean(per_row)) * B
+    return {"value": round(B / per, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle sample_rows on rows 0..{rows[-1]} of {B} ({sum(per_row):.1f} s), "
+                      f"mean per row x {B}", "ms_per_step": round(per * 1e3, 3)}
+
+
+# ----------------------------------------------------------------------------- main
 
 def main():
     args = _parse()
@@ -311,27 +432,44 @@ def main():
         return
     which = set(args.configs.split(","))
     which.add("c1")
-    cfgs = build_configs(torch, which)
+    cfgs = build_configs(torch, which, with_cpu=not args.no_cpu)
     per = {}
     for cfg in cfgs:
-        ms = time_config(torch, cfg, args.steps, args.warmup)
-        us = ms * 1e3
-        per[cfg.name] = {
+        med, p90, all_ms = time_config(torch, cfg, args.steps, args.warmup, args.repeats, cfg.ncopies)
+        us = med * 1e3
+        e = {
             "desc": cfg.desc,
             "us_per_step": round(us, 3),
-            "tokens_per_s": round(cfg.batch / (ms * 1e-3), 1),
+            "us_p90": round(p90 * 1e3, 3),
+            "us_repeats": [round(m * 1e3, 3) for m in all_ms],
+            "input_copies": cfg.ncopies,
+            "tokens_per_s": round(cfg.batch / (med * 1e-3), 1),
             "hbm_bytes_per_step": cfg.nbytes,
-            "hbm_frac": round(cfg.nbytes / (ms * 1e-3) / HBM_PEAK, 4),
+            "hbm_frac": round(cfg.nbytes / (med * 1e-3) / HBM_PEAK, 4),
             "dominant_kernel": cfg.kernel,
         }
-        print(f"# {cfg.name}: {us:.2f} us/step, {per[cfg.name]['tokens_per_s']:.0f} tok/s, "
-              f"{per[cfg.name]['hbm_frac'] * 100:.1f}% of HBM peak", file=sys.stderr, flush=True)
+        if not args.no_warm:
+            wmed, wp90, _ = time_config(torch, cfg, args.steps, args.warmup, args.repeats, 1)
+            e["us_per_step_warm"] = round(wmed * 1e3, 3)
+            e["us_p90_warm"] = round(wp90 * 1e3, 3)
+        per[cfg.name] = e
+        print(f"# {cfg.name}: median {us:.2f} us/step (p90 {p90 * 1e3:.2f}), "
+              f"{e['tokens_per_s']:.0f} tok/s, {e['hbm_frac'] * 100:.1f}% of HBM peak"
+              + (f"; warm {e['us_per_step_warm']:.2f}" if "us_per_step_warm" in e else ""),
+              file=sys.stderr, flush=True)
+    cpu = None
+    if not args.no_cpu:
+        for cfg in cfgs:
+            if cfg.cpu is None:
+                continue
+            secs = args.cpu_seconds if cfg.name.startswith("c1") else args.cpu_seconds_other
+            per[cfg.name]["cpu_baseline"] = cfg.cpu(secs)
+            print(f"# cpu {cfg.name}: {per[cfg.name]['cpu_baseline']['ms_per_step']} ms/step",
+                  file=sys.stderr, flush=True)
+        cpu = per["c1_greedy_lm_head_b1"].get("cpu_baseline")
     head = per["c1_greedy_lm_head_b1"]
     ms_head = head["us_per_step"] / 1e3
     achieved = head["hbm_bytes_per_step"] / (ms_head * 1e-3)
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline_c1(args.cpu_seconds)
     line = {
         "metric": "sampled tokens/s at B=1,64,256 (V=248k) + % of 8 TB/s HBM roofline",
         "value": head["tokens_per_s"],
@@ -347,9 +485,11 @@ def main():
         "data": "synthetic (seeded torch RNG on device; random-init weights)",
         "config": {"workload": "c1_greedy_lm_head_b1: greedy LM-head top-1, hidden [1,1024] bf16 x "
                                "W [248320,1024] bf16, fp32 accumulate, bf16-rounded logits",
-                   "batch": 1, "vocab": V_FULL, "hidden": H_FULL},
-        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": committed_traffic()},
+                   "batch": 1, "vocab": V_FULL, "hidden": H_FULL, "repeats": args.repeats,
+                   "timing": "median over repeats of exactly `steps` calls; W alternates between 2 copies"},
+        "roofline": {"bound": "hbm", "kernel": "lm_head_gemv_kernel", "achieved": round(achieved / 1e9, 1),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                     "traffic": committed_traffic()},
         "cpu_baseline": cpu,
         "per_config": per,
     }

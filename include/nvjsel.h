@@ -209,10 +209,22 @@ int nvjsel_derive_keys(const int32_t* slots, const int32_t* counters, int batch,
  * counter); table.at[slot_ids].set(counters + 1)).  Negative slots read slot 0
  * (model_runner.py:4785); slots >= num_slots read the last entry and are not
  * written (jnp gather clamps, scatter drops).  Rows sharing a slot read the
- * same counter.  counter_table [num_slots] int32, updated in place.
+ * same counter: every row's counter is read before any is written, for any
+ * batch.  counter_table [num_slots] int32, updated in place.  batch <= 8192
+ * (NVJSEL_EUNSUPPORTED above).
  */
 int nvjsel_derive_keys_table(const int32_t* slots, int batch, int32_t* counter_table, int num_slots,
                              uint32_t* keys, void* stream);
+
+/*
+ * Diagnostic (no counterpart in the reference): the Gumbel draw of every
+ * 23-bit uniform mantissa m in [first, first + n), i.e. random bits
+ * (m << 9), two ways -- fast[i] with the hardware fp32 log the kernels use to
+ * pre-select candidates, exact[i] with the correctly rounded log every
+ * returned token is decided on.  first + n <= 2^23.  Lets a test bound the
+ * fast draw's error over its whole domain.
+ */
+int nvjsel_debug_gumbel_draws(uint32_t first, int n, float* fast, float* exact, void* stream);
 
 #ifdef __cplusplus
 }

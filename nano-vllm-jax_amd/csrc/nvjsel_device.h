@@ -166,8 +166,9 @@ __device__ __forceinline__ float gumbel_at(const TfKey& k, uint32_t i) {
   return gumbel_from_bits(random_bits32(k, i));
 }
 
-// The same draw with the hardware fp32 log (v_log_f32): within ~2e-5 of
-// gumbel_from_bits over its whole range.  Used only to find the few elements
+// The same draw with the hardware fp32 log (v_log_f32): within 1.91e-6 of
+// gumbel_from_bits over its whole range (all 2^23 mantissas measured on
+// gfx950; the largest errors sit at u -> 1).  Used only to find the few elements
 // that can be the maximum; the winner is always decided on exact values.
 // Both logs take normal arguments (u >= FLT_MIN, and -log2(u) >= 1.7e-7), so
 // the hardware log2 (v_log_f32) is used bare:

@@ -120,8 +120,19 @@ def test_product_code_never_imports_the_oracle():
     root = Path(__file__).resolve().parents[1]
     for f in list((root / "nano-vllm-jax_amd").rglob("*.py")) + list((root / "nano-vllm-jax_amd").rglob("*.hip")):
         assert "oracle" not in f.read_text(), f
-    bench = (root / "bench.py").read_text()
-    assert "import oracle" not in bench and "from oracle" not in bench
+    # bench.py imports the oracle only inside its CPU-baseline functions (cpu_*)
+    import ast
+
+    tree = ast.parse((root / "bench.py").read_text())
+    allowed = set()
+    for fn in ast.walk(tree):
+        if isinstance(fn, ast.FunctionDef) and fn.name.startswith("cpu_"):
+            allowed.update(id(n) for n in ast.walk(fn))
+    for node in ast.walk(tree):
+        if isinstance(node, (ast.Import, ast.ImportFrom)):
+            names = [a.name for a in node.names] + ([node.module] if isinstance(node, ast.ImportFrom) else [])
+            if any(n and n.split(".")[0] == "oracle" for n in names):
+                assert id(node) in allowed, f"bench.py line {node.lineno} imports the oracle outside cpu_*"
 
 
 def test_mtp_registry_and_shape_contract():

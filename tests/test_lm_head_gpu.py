@@ -220,3 +220,37 @@ def test_mtp_draft_top1_casts_and_flattens(seq_len):
     assert tuple(ids.shape) == (B, seq_len) and ids.dtype == torch.int32
     xb = sel.round_bf16(x.reshape(-1, H))  # the cast the contract requires
     check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(xb, as_f32(W)), 1, f"mtp T={seq_len}")
+
+
+@pytest.mark.parametrize("name", ["c1", "c4"])
+def test_last_block_reduce_is_consistent_over_1000_calls(name):
+    """The cross-block reduce (per-row atomicMax, then the last block by ticket
+    writes the ids and re-zeroes the workspace) at the C1 / C4 shapes: 1,000
+    back-to-back launches on one workspace must all return the first call's
+    ids.  Each launch writes its own output row; the first mismatch is named."""
+    import bench
+    from nvjsel import _lib
+
+    dev = torch.device("cuda:0")
+    d = bench.make_inputs(torch, name, dev)
+    W = bench.lm_weight(torch, dev)
+    B, N = d["batch"], 1000
+    lib = _lib.load()
+    out = torch.full((N, B), -1, dtype=torch.int32, device=dev)
+    ws = torch.zeros(lib.nvjsel_lm_head_workspace_size(B), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    h = d["hidden"]
+    for i in range(N):
+        o = out[i].data_ptr()
+        if name == "c1":
+            _lib.call("nvjsel_lm_head_top1", h.data_ptr(), 1, W.data_ptr(), 1, 0, B, 1024, W.shape[0], 1, o, None,
+                      ws.data_ptr(), ws.numel(), stream)
+        else:
+            _lib.call("nvjsel_lm_head_sample", h.data_ptr(), 1, W.data_ptr(), 1, 0, B, 1024, W.shape[0], 1,
+                      d["temperature"].data_ptr(), d["keys"].data_ptr(), o, ws.data_ptr(), ws.numel(), stream)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    bad = np.nonzero((got != got[0]).any(axis=1))[0]
+    assert bad.size == 0, f"call {bad[0]} differs from call 0: {got[bad[0]][:8]} vs {got[0][:8]}"
+    assert np.all((got[0] >= 0) & (got[0] < W.shape[0]))
+    assert not ws.any().item()  # the workspace is zero at rest

@@ -278,3 +278,57 @@ def test_topp_crossing_bin_overflow_and_far_chunks():
     for dtype in (torch.float32, torch.bfloat16):
         ids, used, keys = _sample(l, T, top_k=[0] * B, top_p=P, dtype=dtype)
         check_sampled(ids, used, T, [0] * B, P, keys, ctx=f"top-p edges {dtype}")
+
+
+def test_counter_table_gathers_before_scatter_across_rounds():
+    """A slot repeated far apart in a large batch (past every 256-row block
+    round): each row reads the counter as it was before the call."""
+    table = torch.arange(0, 64, dtype=torch.int32).cuda() * 3
+    B = 600
+    rng = np.random.default_rng(31)
+    slots = rng.integers(0, 64, B).astype(np.int32)
+    slots[[5, 300, 599]] = 17  # 17 in three different 256-row rounds
+    slots[[10, 520]] = -4      # slot 0 through the clamp
+    slots[[7, 400]] = 90       # past the table: read its last entry, not written
+    before = table.cpu().numpy().copy()
+    keys = nvjsel.derive_rng_keys_from_table(torch.from_numpy(slots).cuda(), table)
+    torch.cuda.synchronize()
+    got = keys.cpu().numpy().view(np.uint32)
+    for b, slot in enumerate(slots):
+        s_eff = max(0, int(slot))
+        exp = jr.engine_key(s_eff, int(before[min(s_eff, 63)]))
+        assert tuple(int(x) for x in got[b]) == (int(exp[0]), int(exp[1])), b
+    exp_after = before.copy()
+    for slot in set(max(0, int(s)) for s in slots):
+        if slot < 64:
+            exp_after[slot] = before[slot] + 1
+    assert np.array_equal(table.cpu().numpy(), exp_after)
+
+
+def _bench_inputs(name):
+    import bench
+
+    return bench.make_inputs(torch, name, torch.device("cuda:0"))
+
+
+@pytest.mark.parametrize("name", ["c2", "c3", "c5"])
+def test_bench_workload_at_full_batch(name):
+    """The exact inputs bench.py times (its seeded builders, same per-row
+    parameter draws): C2 [8, 248320] f32, C3 [64, 248320] f32 (k=50, p=0.9,
+    T=0.8) and C5 [256, 248320] bf16 with mixed per-row T / k / p -- every
+    row checked against the oracle."""
+    d = _bench_inputs(name)
+    B = d["batch"]
+    print(f"case {name} B={B}", flush=True)
+    out = nvjsel.sample_token_ids(d["logits"], d["temperature"], d["keys"], top_k=d["top_k"], top_p=d["top_p"])
+    torch.cuda.synchronize()
+    used = d["logits"].float().cpu().numpy()
+    keys = d["keys"].cpu().numpy().view(np.uint32)
+    T = d["temperature"].cpu().numpy()
+    K = d["top_k"].cpu().numpy() if d["top_k"] is not None else np.zeros(B, np.int32)
+    P = d["top_p"].cpu().numpy() if d["top_p"] is not None else np.ones(B, np.float32)
+    namb = check_sampled(out.cpu().numpy(), used, T, K, P, keys, ctx=name)
+    assert namb <= max(1, B // 16)
+    # the same call again on the reused workspace gives the same ids
+    out2 = nvjsel.sample_token_ids(d["logits"], d["temperature"], d["keys"], top_k=d["top_k"], top_p=d["top_p"])
+    assert torch.equal(out, out2)

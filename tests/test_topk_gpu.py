@@ -100,3 +100,15 @@ def test_lm_head_token_ids_and_topk_width(top_k):
     assert np.array_equal(idx.cpu().numpy().reshape(-1, top_k), ei)
     assert np.array_equal(vals.cpu().numpy().reshape(-1, top_k), ev)
     assert np.array_equal(ids.cpu().numpy().reshape(-1), ei[:, 0])
+
+
+def test_topk_bench_workload_x2():
+    """bench.py's x2 inputs (k=50 over [64, 248320] f32 Zipf rows), bitwise."""
+    import bench
+
+    d = bench.make_inputs(torch, "x2", torch.device("cuda:0"))
+    vals, idx = nvjsel.topk_hip(d["logits"], d["k"])
+    torch.cuda.synchronize()
+    ev, ei = sel.topk(d["logits"].cpu().numpy(), d["k"])
+    assert np.array_equal(idx.cpu().numpy(), ei)
+    assert np.array_equal(vals.cpu().numpy().view(np.uint32), ev.view(np.uint32))
