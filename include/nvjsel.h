@@ -85,6 +85,23 @@ int nvjsel_lm_head_top1(const void* hidden, int hidden_dtype,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The same greedy LM-head top-1 for callers that cannot allocate (no
+ * counterpart in the reference): code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  It takes no workspace; the
+ * library keeps the per-row keys and ticket in a fixed device array of its
+ * own (one per GPU, held until the process ends) and calls no allocating
+ * routine.  batch <= 4096 (NVJSEL_EUNSUPPORTED above).  Every call on a GPU
+ * shares that GPU's array, so calls that overlap in time on one GPU (other
+ * streams, other threads) race; calls ordered on a stream do not.  The first
+ * call on a device looks up the array's address and zero-fills it on
+ * `stream`.
+ */
+int nvjsel_lm_head_top1_noalloc(const void* hidden, int hidden_dtype,
+                                const void* weight, int weight_dtype, int weight_layout,
+                                int batch, int hidden_dim, int vocab, int reduce_cast,
+                                int32_t* out_ids, float* out_best, void* stream);
+
+/*
  * Fused LM-head + temperature sampling without writing logits.
  *
  * Replaces lm_head_sample_token_ids (nanovllm_jax/model.py:901-938): per row,

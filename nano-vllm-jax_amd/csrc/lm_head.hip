@@ -23,6 +23,7 @@
 //     and re-zeroes the workspace -- a single launch per call.
 // Any other dtype/layout/shape goes through a generic VALU kernel with the same
 // reduction and epilogue.
+#include <mutex>
 #include <type_traits>
 
 #include "nvjsel_device.h"
@@ -1299,9 +1300,66 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   return NVJSEL_OK;
 }
 
+// ------------------------------------------------------------------ fixed scratch (no allocation)
+// For callers that cannot allocate (code under graph capture, tight serving
+// loops): the workspace of nvjsel_lm_head_top1 -- per-row argmax keys and the
+// last-block ticket -- lives in a file-scope device array.  Each device holds
+// its own copy for the life of the process; host code reaches it only through
+// the address hipGetSymbolAddress returns for that device.  It is zeroed once
+// per device at set-up and every successful call leaves it zeroed again.
+static constexpr int kNoAllocMaxBatch = 4096;
+static constexpr size_t kNoAllocScratchBytes = (size_t)kNoAllocMaxBatch * 8 + 256;  // keys + ticket line
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64] = {};
+
+// The current device's scratch address, set up (address lookup + one zero
+// fill on `stream`) on the first call on that device.
+static int noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = 0;
+  NVJSEL_CHECK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return fail(NVJSEL_EUNSUPPORTED, "lm_head_top1_noalloc: device id >= 64");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    NVJSEL_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(NVJSEL_EHIP, "lm_head_top1_noalloc: no device address for the scratch array");
+    // a fill kernel rather than hipMemsetAsync: safe under graph capture
+    const size_t words = kNoAllocScratchBytes / 4;
+    hipLaunchKernelGGL(lm_zero_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream, (uint32_t*)p,
+                       words);
+    NVJSEL_CHECK_LAUNCH("lm_zero_kernel");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NVJSEL_OK;
+}
+
 }  // namespace nvjsel
 
 using namespace nvjsel;
+
+extern "C" int nvjsel_lm_head_top1_noalloc(const void* hidden, int hidden_dtype, const void* weight,
+                                           int weight_dtype, int weight_layout, int batch, int hidden_dim,
+                                           int vocab, int reduce_cast, int32_t* out_ids, float* out_best,
+                                           void* stream) {
+  clear_error();
+  if (batch > kNoAllocMaxBatch) {
+    set_error("lm_head_top1_noalloc: batch %d exceeds the fixed scratch's maximum of %d rows", batch,
+              kNoAllocMaxBatch);
+    return NVJSEL_EUNSUPPORTED;
+  }
+  if (batch <= 0) {
+    set_error("lm_head_top1_noalloc requires non-empty dimensions (batch=%d)", batch);
+    return NVJSEL_EINVAL;
+  }
+  void* ws = nullptr;
+  const int rc = noalloc_scratch((hipStream_t)stream, &ws);
+  if (rc != NVJSEL_OK) return rc;
+  return lm_head_entry(MODE_GREEDY, hidden, hidden_dtype, weight, weight_dtype, weight_layout, batch, hidden_dim,
+                       vocab, reduce_cast, nullptr, nullptr, out_ids, out_best, ws, kNoAllocScratchBytes, stream);
+}
 
 extern "C" size_t nvjsel_lm_head_workspace_size(int batch) {
   if (batch <= 0) return 0;

@@ -1,0 +1,54 @@
+"""GPU: the allocation-free greedy LM-head entry point against the regular one.
+
+nvjsel_lm_head_top1_noalloc keeps its workspace in a fixed device array
+instead of a caller workspace; its ids (and winning logits) must equal
+nvjsel_lm_head_top1's on the same inputs -- on two calls in a row, the second
+with a smaller batch (the array keeps the first call's state between calls),
+across the streaming (B <= 2), tile (3..64) and chunked (> 64) paths."""
+import numpy as np
+import pytest
+import torch
+
+from nvjsel import _lib
+
+pytestmark = pytest.mark.gpu
+
+def _noalloc(lib):
+    return lib.nvjsel_lm_head_top1_noalloc  # argtypes from nvjsel._lib.SIGNATURES
+
+
+def _run_both(lib, h, W, B, H, V):
+    stream = torch.cuda.current_stream().cuda_stream
+    ids_a = torch.full((B,), -1, dtype=torch.int32, device="cuda")
+    best_a = torch.zeros(B, dtype=torch.float32, device="cuda")
+    ws = torch.zeros(lib.nvjsel_lm_head_workspace_size(B), dtype=torch.uint8, device="cuda")
+    _lib.call("nvjsel_lm_head_top1", h.data_ptr(), _lib.BF16, W.data_ptr(), _lib.BF16, _lib.W_VH, B, H, V, 1,
+              ids_a.data_ptr(), best_a.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    ids_b = torch.full((B,), -1, dtype=torch.int32, device="cuda")
+    best_b = torch.zeros(B, dtype=torch.float32, device="cuda")
+    rc = _noalloc(lib)(h.data_ptr(), _lib.BF16, W.data_ptr(), _lib.BF16, _lib.W_VH, B, H, V, 1, ids_b.data_ptr(),
+                       best_b.data_ptr(), stream)
+    assert rc == 0, lib.nvjsel_last_error()
+    torch.cuda.synchronize()
+    return ids_a.cpu().numpy(), best_a.cpu().numpy(), ids_b.cpu().numpy(), best_b.cpu().numpy()
+
+
+@pytest.mark.parametrize("batches", [(64, 8), (1, 1), (200, 2), (33, 3)])
+def test_noalloc_matches_workspace_entry(batches):
+    lib = _lib.load()
+    rng = np.random.default_rng(sum(batches))
+    H, V = 1024, 50_000
+    W = torch.from_numpy(rng.standard_normal((V, H)).astype(np.float32) * 0.02).cuda().to(torch.bfloat16)
+    for B in batches:  # second call smaller
+        h = torch.from_numpy(rng.standard_normal((B, H)).astype(np.float32)).cuda().to(torch.bfloat16)
+        ia, ba, ib, bb = _run_both(lib, h, W, B, H, V)
+        assert np.array_equal(ia, ib), (B, ia[:8], ib[:8])
+        assert np.array_equal(ba.view(np.uint32), bb.view(np.uint32)), B
+        assert np.all((ia >= 0) & (ia < V))
+
+
+def test_noalloc_rejects_batch_beyond_scratch():
+    lib = _lib.load()
+    rc = _noalloc(lib)(0x1000, _lib.BF16, 0x1000, _lib.BF16, _lib.W_VH, 4097, 1024, 1000, 1, 0x1000, None, None)
+    assert rc == -2
+    assert b"4096" in lib.nvjsel_last_error()
