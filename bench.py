@@ -220,13 +220,13 @@ def build_configs(torch, which, with_cpu):
         dt = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[d["logits"].dtype]
         out = torch.empty(B, dtype=torch.int32, device=dev)
         w = ws(lib.nvjsel_sample_workspace_size(B, V_FULL))
+        # the closure holds every tensor it passes by pointer, so none is freed and reused
         t, k, p, keys = d["temperature"], d["top_k"], d["top_p"], d["keys"]
-        kp = k.data_ptr() if k is not None else None
-        pp = p.data_ptr() if p is not None else None
 
-        def launch(i):
-            ck(lib.nvjsel_sample(Ls[i].data_ptr(), dt, B, V_FULL, V_FULL, t.data_ptr(), kp, pp, keys.data_ptr(),
-                                 None, out.data_ptr(), w.data_ptr(), w.numel(), stream()))
+        def launch(i, Ls=Ls, t=t, k=k, p=p, keys=keys, out=out, w=w):
+            ck(lib.nvjsel_sample(Ls[i].data_ptr(), dt, B, V_FULL, V_FULL, t.data_ptr(),
+                                 k.data_ptr() if k is not None else None, p.data_ptr() if p is not None else None,
+                                 keys.data_ptr(), None, out.data_ptr(), w.data_ptr(), w.numel(), stream()))
 
         cpu = (lambda secs, d=d: cpu_sampler(d, secs)) if with_cpu else None
         return Cfg(name, B, d["logits"].numel() * d["logits"].element_size(), launch, n, kernel, desc, cpu)
