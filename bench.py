@@ -36,9 +36,10 @@ for _p in (ROOT, os.path.join(ROOT, "nano-vllm-jax_amd")):
 HBM_PEAK = 8.0e12  # bytes/s, MI355X
 MALL_BYTES = 256 * 1024 * 1024
 V_FULL, H_FULL = 248320, 1024
-ALL_CONFIGS = "c1,c2,c3,c4,c5,x1,x2"
+ALL_CONFIGS = "c1,c2,c3,c4,c5,x1,x2,x3,x4,x5"
 # per-config generator seeds: each config's inputs depend only on its own seed
-SEEDS = {"c1": 101, "c2": 102, "c3": 103, "c4": 104, "c5": 105, "x1": 201, "x2": 202}
+SEEDS = {"c1": 101, "c2": 102, "c3": 103, "c4": 104, "c5": 105, "x1": 201, "x2": 202, "x3": 203, "x4": 204,
+         "x5": 205}
 
 
 def _parse():
@@ -171,6 +172,10 @@ def make_inputs(torch, name, dev):
         return {"batch": B, "logits": l, "temperature": choice([0.0, 0.6, 1.0], torch.float32),
                 "top_k": choice([0, 20, 100], torch.int32), "top_p": choice([1.0, 0.95, 0.8], torch.float32),
                 "keys": _engine_keys(torch, B, dev)}
+    if name in ("x3", "x4", "x5"):
+        B = 1 if name == "x3" else 8
+        h = torch.randn(B, H_FULL, device=dev, generator=gen)
+        return {"batch": B, "hidden": h if name == "x5" else h.to(torch.bfloat16)}
     raise KeyError(name)
 
 
@@ -199,6 +204,7 @@ def build_configs(torch, which, with_cpu):
     stream = lambda: torch.cuda.current_stream(dev).cuda_stream  # noqa: E731
     cfgs = []
     Wcache = []
+    Whv = []  # [H, V] copies of the weight copies
 
     def weights():
         # two copies, alternated per step, so the 508 MB table cannot sit in the 256 MB MALL
@@ -303,6 +309,34 @@ def build_configs(torch, which, with_cpu):
 
         cfgs.append(Cfg("x2_topk50_b64", B, B * V_FULL * 4, launch, n, "sample_scan_kernel",
                         "top-k values+indices k=50, f32 logits [64,248320] Zipf(1.1)"))
+    # the reference's other operating points: the materialised [H, V] lm_head
+    # (B = 1 and 8) and fp32 activations at B = 8 on the [V, H] table
+    for name in ("x3", "x4", "x5"):
+        if name not in which:
+            continue
+        d = make_inputs(torch, name, dev)
+        B, h = d["batch"], d["hidden"]
+        if name == "x5":
+            Ws, layout = weights(), 0
+        else:
+            if not Whv:
+                Whv.extend([W.T.contiguous() for W in weights()])
+            Ws, layout = Whv, 1
+        hdt = 0 if h.dtype == torch.float32 else 1
+        rc = 1 if hdt == 1 else 0
+        out = torch.empty(B, dtype=torch.int32, device=dev)
+        w = ws(lib.nvjsel_lm_head_workspace_size(B))
+
+        def launch(i, Ws=Ws, h=h, out=out, w=w, B=B, layout=layout, hdt=hdt, rc=rc):
+            ck(lib.nvjsel_lm_head_top1(h.data_ptr(), hdt, Ws[i].data_ptr(), 1, layout, B, H_FULL, V_FULL, rc,
+                                       out.data_ptr(), None, w.data_ptr(), w.numel(), stream()))
+
+        desc = {"x3": "greedy LM-head top-1, B=1, W [1024,248320] bf16 ([H,V], the materialised lm_head)",
+                "x4": "greedy LM-head top-1, B=8, W [1024,248320] bf16 ([H,V])",
+                "x5": "greedy LM-head top-1, B=8, fp32 activations x W [248320,1024] bf16 (one W pass)"}[name]
+        kern = "lm_head_tile_kernel" if name == "x5" else "lm_head_hv_kernel"
+        cfgs.append(Cfg(f"{name}_{'hv' if layout else 'f32act'}_greedy_b{B}", B,
+                        V_FULL * H_FULL * 2 + B * H_FULL * h.element_size(), launch, 2, kern, desc))
     torch.cuda.synchronize()
     del np
     return cfgs

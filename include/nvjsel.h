@@ -119,6 +119,22 @@ int nvjsel_lm_head_sample(const void* hidden, int hidden_dtype,
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Dense LM-head logits, for the routes that need them: the top-k verifier
+ * route of lm_head_token_ids_and_topk(top_k > 0) (nanovllm_jax/model.py:
+ * 866-898: jnp.dot(hidden_norm, W) then lax.top_k / radix_topk) and sampling
+ * with top-k / top-p from the hidden state.  out_logits[b, v] (rows
+ * out_row_stride elements apart, out_dtype f32 or bf16) = sum_k hidden[b,k] *
+ * W(v,k) accumulated in fp32 and rounded per reduce_cast (the reference's dot
+ * output: bf16 for bf16 x bf16), then stored as out_dtype (bf16: round to
+ * nearest even).  Same kernels as nvjsel_lm_head_top1, with a store epilogue;
+ * no workspace.
+ */
+int nvjsel_lm_head_logits(const void* hidden, int hidden_dtype,
+                          const void* weight, int weight_dtype, int weight_layout,
+                          int batch, int hidden_dim, int vocab, int reduce_cast,
+                          void* out_logits, int out_dtype, int64_t out_row_stride, void* stream);
+
+/*
  * Final-RMSNorm prologue variants: the same as nvjsel_lm_head_top1 /
  * nvjsel_lm_head_sample, but `hidden` is the pre-norm hidden state and the
  * library first forms, per row, the LM-head input of

@@ -29,57 +29,27 @@
 #include "nvjsel_device.h"
 #include "nvjsel_host.h"
 
-// Launch shape; overridable at build time for tuning sweeps.
-#ifndef NVJSEL_LM_WAVES
-#define NVJSEL_LM_WAVES 8  // waves per block
-#endif
-#ifndef NVJSEL_LM_MT1
-#define NVJSEL_LM_MT1 4  // 16-row vocab tiles per wave when B <= 16
-#endif
-#ifndef NVJSEL_LM_MTN
-#define NVJSEL_LM_MTN 2  // ... when B > 16
-#endif
-#ifndef NVJSEL_LM_KU
-#define NVJSEL_LM_KU 4  // 32-wide k-steps per prefetch chunk
-#endif
-#ifndef NVJSEL_LM_NT
-#define NVJSEL_LM_NT 1  // non-temporal (streaming) loads of W
-#endif
-#ifndef NVJSEL_LM_DEPTH
-#define NVJSEL_LM_DEPTH 3  // k-chunks of W in flight per wave
-#endif
-#ifndef NVJSEL_LM_BPC
-#define NVJSEL_LM_BPC 0  // blocks per CU (0 = as many as occupancy allows)
-#endif
+// Launch shapes (chosen by measurement on MI355X).
+static constexpr int kLmWaves = 8;  // waves per block
+static constexpr int kLmMt1 = 4;  // 16-row vocab tiles per wave when B <= 16
+static constexpr int kLmMtn = 2;  // ... when B > 16
+static constexpr int kLmKu = 4;  // 32-wide k-steps per prefetch chunk
+static constexpr int kLmNt = 1;  // non-temporal (streaming) loads of W
+static constexpr int kLmDepth = 3;  // k-chunks of W in flight per wave
+static constexpr int kLmBpc = 0;  // blocks per CU (0 = as many as occupancy allows)
 
-#ifndef NVJSEL_USE_TILE
-#define NVJSEL_USE_TILE 1  // LDS-staged MFMA kernel for bf16 x bf16, H = 1024, B >= 3
-#endif
-#ifndef NVJSEL_GEMV_WAVES
-#define NVJSEL_GEMV_WAVES 4  // waves per block of the streaming GEMV
-#endif
-#ifndef NVJSEL_GEMV_DEPTH
-#define NVJSEL_GEMV_DEPTH 3  // row groups in flight per wave (measured: 3 > 4, 5 > 2)
-#endif
-#ifndef NVJSEL_GEMV_BPC
-#define NVJSEL_GEMV_BPC 1  // blocks per CU for the streaming GEMV (0 = occupancy)
-#endif
-#ifndef NVJSEL_TILE_QCAP
-#define NVJSEL_TILE_QCAP 768  // queue entries per epilogue wave (sample mode)
-#endif
-#ifndef NVJSEL_GEMV_R
-#define NVJSEL_GEMV_R 4  // rows per wave step of the streaming GEMV
-#endif
+static constexpr int kGemvWaves = 4;  // waves per block of the streaming GEMV
+static constexpr int kGemvDepth = 3;  // row groups in flight per wave (measured: 3 > 4, 5 > 2)
+static constexpr int kGemvBpc = 1;  // blocks per CU for the streaming GEMV (0 = occupancy)
+static constexpr int kTileQcap = 768;  // queue entries per epilogue wave (sample mode)
+static constexpr int kGemvR = 4;  // rows per wave step of the streaming GEMV
 
 namespace nvjsel {
 
 template <typename T>
 __device__ __forceinline__ T stream_load(const T* p) {
-#if NVJSEL_LM_NT
-  return __builtin_nontemporal_load(p);
-#else
-  return *p;
-#endif
+  if constexpr (kLmNt) return __builtin_nontemporal_load(p);
+  else return *p;
 }
 
 // Lambdas that take a register array by reference must inline, or the array
@@ -134,7 +104,9 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-enum { MODE_GREEDY = 0, MODE_SAMPLE = 1 };
+// GREEDY: argmax id per row; SAMPLE: Gumbel-max id per row; LOGITS: the
+// (REDUCE_CAST-rounded) logits themselves, written to out_logits.
+enum { MODE_GREEDY = 0, MODE_SAMPLE = 1, MODE_LOGITS = 2 };
 
 struct LmArgs {
   const void* W;
@@ -159,7 +131,17 @@ struct LmArgs {
   unsigned int* counter;
   int32_t* out_ids;
   float* out_best;
+  void* out_logits;      // MODE_LOGITS: [B, out_stride] of out_dtype, offset to this launch's first row
+  int out_dtype;         // DT_F32 or DT_BF16
+  long long out_stride;  // elements between output rows
 };
+
+// MODE_LOGITS store of logit (b, v): f32 as is, bf16 rounded to nearest even.
+__device__ __forceinline__ void store_logit(const LmArgs& a, int b, int v, float val) {
+  const size_t i = (size_t)b * (size_t)a.out_stride + (size_t)v;
+  if (a.out_dtype == DT_F32) ((float*)a.out_logits)[i] = val;
+  else ((__bf16*)a.out_logits)[i] = (__bf16)val;
+}
 
 template <int WT>
 __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
@@ -456,16 +438,21 @@ lm_head_mfma_kernel(LmArgs a) {
           const int v = v0 + t * 16 + g * 4 + i;
           if (v < V && b < B) {
             float val = apply_cast(acc[t][nb][i], a.reduce_cast);
-            if constexpr (MODE == MODE_SAMPLE) {
-              if (!greedy_row[nb]) val = val / tp[nb] + gumbel_at(key[nb], (uint32_t)v);
+            if constexpr (MODE == MODE_LOGITS) {
+              store_logit(a, b, v, val);
+            } else {
+              if constexpr (MODE == MODE_SAMPLE) {
+                if (!greedy_row[nb]) val = val / tp[nb] + gumbel_at(key[nb], (uint32_t)v);
+              }
+              best[nb] = max_u64(best[nb], argmax_key(val, (uint32_t)v));
             }
-            best[nb] = max_u64(best[nb], argmax_key(val, (uint32_t)v));
           }
         }
         acc[t][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
   }
 
+  if constexpr (MODE == MODE_LOGITS) return;
   // ---- reduce the four k-groups, then the waves, then across blocks
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -492,8 +479,8 @@ lm_head_mfma_kernel(LmArgs a) {
 // lanes with the full dot of one row (log2(64) shuffle rounds, halving the
 // values carried at each of the first log2(R) rounds).
 template <int NB, int R, int KJ, int MODE>
-__global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(LmArgs a) {
-  constexpr int WAVES = NVJSEL_GEMV_WAVES;
+__global__ void __launch_bounds__(kGemvWaves * 64) lm_head_gemv_kernel(LmArgs a) {
+  constexpr int WAVES = kGemvWaves;
   __shared__ unsigned long long red[WAVES * NB];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int H = KJ * 512, V = a.V, B = a.B;
@@ -614,13 +601,19 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
       for (int b = 0; b < NB; ++b) p[b][0] += __shfl_xor(p[b][0], mask, 64);
     const int v = v0 + sel;
     if (v < V) {
+      // every lane of a row group (64 / R lanes) holds the same totals; in
+      // sample and logits mode lane j of the group handles batch row j
+      const int gl = lane & (64 / R - 1);
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         if (b >= B) continue;
         float val = apply_cast(p[b][0], a.reduce_cast);
+        if constexpr (MODE == MODE_LOGITS) {
+          if (gl == b) store_logit(a, b, v, val);
+          continue;
+        }
         if constexpr (MODE == MODE_SAMPLE) {
-          // every lane of a row group holds the same total; one draws the noise
-          if ((lane & (64 / R - 1)) != 0) continue;
+          if (gl != b) continue;
           if (!greedy_row[b]) val = val / tp[b] + gumbel_at(key[b], (uint32_t)v);
         }
         best[b] = max_u64(best[b], argmax_key(val, (uint32_t)v));
@@ -630,7 +623,7 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
 
   // ring of DEPTH row groups in flight: group i+DEPTH-1 is requested before i is reduced
   // ring of DEPTH * R * KJ 16-byte loads per lane
-  constexpr int DEPTH = MODE == MODE_SAMPLE ? (KJ >= 4 ? 2 : 3) : NVJSEL_GEMV_DEPTH;
+  constexpr int DEPTH = MODE == MODE_SAMPLE ? (KJ >= 4 || NB > 2 ? 2 : 3) : (NB > 2 ? 2 : kGemvDepth);
   const int n_mine = g_end > g_begin ? (g_end - g_begin + g_step - 1) / g_step : 0;
   auto gid = [&](int i) { return g_begin + i * g_step; };
   u32x4_t ring[DEPTH][R][KJ];
@@ -657,6 +650,7 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
           for (int j = 0; j < KJ; ++j) ring[d][r][j] = ring[d + 1][r][j];
     }
   }
+  if constexpr (MODE == MODE_LOGITS) return;
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     best[b] = wave_max_u64(best[b]);
@@ -664,6 +658,149 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
   }
   block_commit<WAVES, NB>(red, B, a.row_keys);
   finish_rows(a.row_keys, a.counter, B, a.out_ids, a.out_best);
+}
+
+// ------------------------------------------------------------------ [H, V] streaming kernel
+// Weight stored [H, V] bf16, vocabulary contiguous: the reference's
+// materialised lm_head operand (nanovllm_jax/load_weights.py:256-258; the
+// layout lm_head_triton.py:51-55 reads), B <= 8, activations of any dtype
+// (fp32 activations multiply exactly: every product and sum is fp32).
+// A block owns a 512-column vocabulary strip; wave w of WAVES takes the
+// k-slice [w * H / WAVES, (w + 1) * H / WAVES).  Lane l loads 16 bytes
+// (columns 8 l .. 8 l + 7) of every W row of its slice, so each load
+// instruction of a wave reads 1 KB of one row, contiguous, and (DEPTH - 1) *
+// KU rows are in flight per wave; acc[b][c] += h[b][k] * W[k][col + c] in
+// fp32, with h broadcast from LDS.  The slices' partial sums meet in LDS,
+// summed in slice order, and each thread then scores two columns of every row.
+template <int NB, int WAVES, int MODE>
+__global__ void __launch_bounds__(WAVES * 64) lm_head_hv_kernel(LmArgs a) {
+  constexpr int KU = 4;
+  constexpr int DEPTH = NB <= 2 ? 6 : 4;
+  constexpr int STRIP = 512;
+  extern __shared__ float lds_f[];  // hidden [H][NB], then partial sums [WAVES][NB][STRIP]
+  __shared__ unsigned long long red[WAVES * NB];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int H = a.H, V = a.V, B = a.B;
+  const int vb = blockIdx.x * STRIP;
+  const int col = min(vb + lane * 8, V - 8);  // clamped loads past the row end (V % 8 == 0)
+  for (int i = threadIdx.x; i < H * NB; i += WAVES * 64) {
+    const int k = i / NB, b = i - k * NB;
+    lds_f[i] = b < B ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * H + k) : 0.0f;
+  }
+  float tp[NB];
+  bool greedy_row[NB];
+  TfKey key[NB];
+  if constexpr (MODE == MODE_SAMPLE) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float t = (b < B) ? a.temperature[b] : 0.0f;
+      greedy_row[b] = (t <= 0.0f);
+      tp[b] = temp_floor(t);
+      key[b] = (b < B) ? tf_key(a.keys[2 * b], a.keys[2 * b + 1]) : tf_key(0u, 0u);
+    }
+  }
+  __syncthreads();
+  const int kper = (H + WAVES - 1) / WAVES;
+  const int k0 = min(H, wave * kper), k1 = min(H, k0 + kper);
+  const int nsteps = (k1 - k0 + KU - 1) / KU;
+  const uint16_t* W = (const uint16_t*)a.W;
+  float acc[NB][8];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[b][c] = 0.0f;
+  u32x4_t ring[DEPTH][KU];
+  ring_pipeline<DEPTH>(
+      nsteps,
+      [&](auto S, int j) NVJSEL_INLINE {
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+          const int k = min(k0 + j * KU + u, k1 - 1);
+          ring[decltype(S)::value][u] = stream_load((const u32x4_t*)(W + (size_t)k * V + col));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      },
+      [&](auto S, int i) NVJSEL_INLINE {
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+          const int k = k0 + i * KU + u;
+          if (k >= k1) continue;  // wave-uniform (last step of the slice)
+          const u32x4_t w = ring[decltype(S)::value][u];
+          const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+          float wf[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            wf[2 * e] = __uint_as_float(q[e] << 16);
+            wf[2 * e + 1] = __uint_as_float(q[e] & 0xFFFF0000u);
+          }
+          const float* hk = lds_f + k * NB;
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            const float h = hk[b];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[b][c] = fmaf(h, wf[c], acc[b][c]);
+          }
+        }
+      });
+  __syncthreads();  // the hidden is dead: the LDS takes the partial sums
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) lds_f[(wave * NB + b) * STRIP + lane * 8 + c] = acc[b][c];
+  __syncthreads();
+  unsigned long long best[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) best[b] = 0;
+  for (int cc = threadIdx.x; cc < STRIP; cc += WAVES * 64) {
+    const int v = vb + cc;
+    if (v >= V) continue;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (b >= B) continue;
+      float sum = lds_f[b * STRIP + cc];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) sum += lds_f[(w * NB + b) * STRIP + cc];
+      float val = apply_cast(sum, a.reduce_cast);
+      if constexpr (MODE == MODE_LOGITS) {
+        store_logit(a, b, v, val);
+        continue;
+      }
+      if constexpr (MODE == MODE_SAMPLE) {
+        if (!greedy_row[b]) val = val / tp[b] + gumbel_at(key[b], (uint32_t)v);
+      }
+      best[b] = max_u64(best[b], argmax_key(val, (uint32_t)v));
+    }
+  }
+  if constexpr (MODE == MODE_LOGITS) return;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    best[b] = wave_max_u64(best[b]);
+    if (lane == 0) red[wave * NB + b] = best[b];
+  }
+  block_commit<WAVES, NB>(red, B, a.row_keys);
+  finish_rows(a.row_keys, a.counter, B, a.out_ids, a.out_best);
+}
+
+// Packs eight values into NS bf16 B-fragment words per term: NS = 1 rounds
+// each value to bf16 (exact for bf16 activations); NS = 3 splits an fp32 value
+// exactly into three bf16 terms (hi + mid + lo = v: 8 + 8 + 8 significand bits),
+// so that three bf16 x bf16 products, each exact in fp32, give an fp32-accurate dot.
+template <int NS, int KPW>
+__device__ __forceinline__ void split_terms(const float (&v)[8], u32x4_t (&hb)[NS][KPW], int kk) {
+  float r[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = v[e];
+#pragma unroll
+  for (int t = 0; t < NS; ++t) {
+    uint32_t bits[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      bits[e] = bf16_bits_rne(r[e]);
+      r[e] = r[e] - __uint_as_float(bits[e] << 16);
+    }
+    hb[t][kk] = u32x4_t{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16), bits[4] | (bits[5] << 16),
+                        bits[6] | (bits[7] << 16)};
+  }
 }
 
 // ------------------------------------------------------------------ LDS-staged MFMA tile kernel
@@ -686,7 +823,7 @@ __global__ void __launch_bounds__(NVJSEL_GEMV_WAVES * 64) lm_head_gemv_kernel(Lm
 // beside the GEMM waves' LDS, MFMA and memory waits on the same SIMDs.
 // PN: the final RMSNorm prologue is compiled in (a.prenorm set); kept out of
 // the plain kernel so its registers do not constrain the main loops.
-template <int NB, int GW, int MODE, int DEPTH, int EPM, bool PN>
+template <int NB, int GW, int MODE, int DEPTH, int EPM, bool PN, int NS>
 __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmArgs a) {
   constexpr int EW = NB * EPM;     // epilogue waves
   constexpr int EPL = 4 / EPM;     // vocabulary rows per epilogue lane per tile
@@ -704,7 +841,7 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
   // per-epilogue-wave queue of entries that may be their row's maximum; it is
   // filtered against the rows' current approximate maxima when it fills and
   // at the end, and only the survivors are rescored exactly
-  constexpr int QCAP = NVJSEL_TILE_QCAP * 4 / (EW > 4 ? EW : 4);  // LDS: 12 B per entry
+  constexpr int QCAP = kTileQcap * 4 / (EW > 4 ? EW : 4);  // LDS: 12 B per entry
   static_assert(QCAP >= 2 * 64 * EPL, "room for a filtered queue plus one tile");
   __shared__ u32x4_t wt[2][16 * 128];
   __shared__ f32x4_t part[2][KSPLIT * NB * 64];
@@ -724,7 +861,7 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
   // ---- GEMM-wave state
   const int g = lane >> 4, r = lane & 15;
   const int nb = wave % NB, ks = wave / NB;  // meaningful for GEMM waves
-  u32x4_t hb[KPW];
+  u32x4_t hb[NS][KPW];  // hidden fragments: NS bf16 terms (3 split an fp32 value exactly)
   u32x4_t ring[DEPTH][LPT];
   // ---- epilogue-wave state
   const int ew = wave - GW;                      // epilogue wave index
@@ -801,12 +938,22 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
   __shared__ float pre_ss[KSPLIT][ROWS];
   if (gemm) {
     const int brow = nb * 16 + r;
-    if constexpr (!PN) {
+    if constexpr (!PN && NS == 1) {
       const uint16_t* hp = (const uint16_t*)a.hidden + (size_t)(brow < B ? brow : 0) * 1024;
 #pragma unroll
       for (int kk = 0; kk < KPW; ++kk) {
         const int kb = ks * KPW + kk;
-        hb[kk] = brow < B ? *(const u32x4_t*)(hp + kb * 32 + g * 8) : u32x4_t{0u, 0u, 0u, 0u};
+        hb[0][kk] = brow < B ? *(const u32x4_t*)(hp + kb * 32 + g * 8) : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    } else if constexpr (!PN) {
+#pragma unroll
+      for (int kk = 0; kk < KPW; ++kk) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          v[e] = brow < B ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)brow * 1024 + (ks * KPW + kk) * 32 + g * 8 + e)
+                          : 0.0f;
+        split_terms<NS>(v, hb, kk);
       }
     } else {
       // RMSNorm prologue, pass 1: this lane's sum of squares; the four lanes
@@ -852,15 +999,14 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
     const float inv = prenorm_inv(a, tot);
 #pragma unroll
     for (int kk = 0; kk < KPW; ++kk) {
-      uint32_t bits[8];
+      float v[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int k = (ks * KPW + kk) * 32 + g * 8 + e;
         const float x = brow < B ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)brow * 1024 + k) : 0.0f;
-        bits[e] = brow < B ? bf16_bits_rne(prenorm_apply(a, x, inv, k)) : 0u;
+        v[e] = brow < B ? prenorm_apply(a, x, inv, k) : 0.0f;
       }
-      hb[kk] = u32x4_t{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16), bits[4] | (bits[5] << 16),
-                       bits[6] | (bits[7] << 16)};
+      split_terms<NS>(v, hb, kk);
     }
   };
 
@@ -879,7 +1025,9 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
 #pragma unroll
       for (int kk = 0; kk < KPW; ++kk) {
         const int q = (ks * KPW + kk) * 4 + g;
-        acc = mfma16x16x32<DT_BF16>(buf[q * 16 + (r ^ (q & 15))], hb[kk], acc);
+        const u32x4_t af = buf[q * 16 + (r ^ (q & 15))];
+#pragma unroll
+        for (int t = 0; t < NS; ++t) acc = mfma16x16x32<DT_BF16>(af, hb[t][kk], acc);
       }
       part[i & 1][(ks * NB + nb) * 64 + lane] = acc;
     }, finish_prenorm);
@@ -920,7 +1068,13 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
         float raw[EPL];
 #pragma unroll
         for (int e = 0; e < EPL; ++e) raw[e] = EPL == 4 ? s[e] : (c0 == 0 ? s[e] : s[e + 2]);
-        score_run<MODE, EPL>(raw, v0, V, a.reduce_cast, greedy_row, unit_tp, tp, key, amax, best, q, xq, aq);
+        if constexpr (MODE == MODE_LOGITS) {
+#pragma unroll
+          for (int e = 0; e < EPL; ++e)
+            if (v0 + e < V) store_logit(a, erow, v0 + e, apply_cast(raw[e], a.reduce_cast));
+        } else {
+          score_run<MODE, EPL>(raw, v0, V, a.reduce_cast, greedy_row, unit_tp, tp, key, amax, best, q, xq, aq);
+        }
       }
       if constexpr (MODE == MODE_SAMPLE) {
         // queue the marked entries with the whole wave active: slots from a
@@ -945,6 +1099,7 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
       }
     }
   }
+  if constexpr (MODE == MODE_LOGITS) return;
   if (!gemm) {
     if constexpr (MODE == MODE_SAMPLE) {
       compact();
@@ -963,30 +1118,20 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
   finish_rows(a.row_keys, a.counter, B, a.out_ids, a.out_best);
 }
 
-#ifndef NVJSEL_TILE_DEPTH
-#define NVJSEL_TILE_DEPTH 2  // W tiles in flight per block (registers)
-#endif
-#ifndef NVJSEL_TILE_W1
-#define NVJSEL_TILE_W1 4  // waves per block by batch tiles: 1, 2, 4
-#endif
-#ifndef NVJSEL_TILE_W2
-#define NVJSEL_TILE_W2 8
-#endif
-#ifndef NVJSEL_TILE_W4
-#define NVJSEL_TILE_W4 8
-#endif
-#ifndef NVJSEL_TILE_BPC
-#define NVJSEL_TILE_BPC 1  // blocks per CU of the tile kernel
-#endif
+static constexpr int kTileDepth = 2;  // W tiles in flight per block (registers)
+static constexpr int kTileW1 = 4;  // waves per block by batch tiles: 1, 2, 4
+static constexpr int kTileW2 = 8;
+static constexpr int kTileW4 = 8;
+static constexpr int kTileBpc = 1;  // blocks per CU of the tile kernel
 
-template <int NB, int GW, int MODE>
+template <int NB, int GW, int MODE, int NS>
 static int launch_tile(const LmArgs& a, hipStream_t stream) {
   // a second epilogue wave per batch tile (sample mode; measured B=32 91 ->
   // 81 us, B=64 125 -> 118 us): two waves per SIMD issue the draws
   constexpr int EPM = (MODE == MODE_SAMPLE && NB >= 2) ? 2 : 1;
-  auto kern = a.prenorm ? lm_head_tile_kernel<NB, GW, MODE, NVJSEL_TILE_DEPTH, EPM, true>
-                        : lm_head_tile_kernel<NB, GW, MODE, NVJSEL_TILE_DEPTH, EPM, false>;
-  int grid = NVJSEL_TILE_BPC * device_cu_count();
+  auto kern = a.prenorm ? lm_head_tile_kernel<NB, GW, MODE, kTileDepth, EPM, true, NS>
+                        : lm_head_tile_kernel<NB, GW, MODE, kTileDepth, EPM, false, NS>;
+  int grid = kTileBpc * device_cu_count();
   const int ntiles = (a.V + 15) / 16;
   if (grid > ntiles) grid = ntiles;
   hipLaunchKernelGGL(kern, dim3(grid), dim3((GW + NB * EPM) * 64), 0, stream, a);
@@ -994,11 +1139,15 @@ static int launch_tile(const LmArgs& a, hipStream_t stream) {
   return NVJSEL_OK;
 }
 
+// Activations other than bf16 (a.act_dtype f32 / f16) take three bf16 terms
+// per value, in launches of at most 16 rows (the terms' registers: 32 rows
+// per block would spill).
 template <int MODE>
 static int dispatch_tile(const LmArgs& a, hipStream_t s) {
-  if (a.B <= 16) return launch_tile<1, NVJSEL_TILE_W1, MODE>(a, s);
-  if (a.B <= 32) return launch_tile<2, NVJSEL_TILE_W2, MODE>(a, s);
-  return launch_tile<4, NVJSEL_TILE_W4, MODE>(a, s);
+  if (a.act_dtype != DT_BF16) return launch_tile<1, kTileW1, MODE, 3>(a, s);
+  if (a.B <= 16) return launch_tile<1, kTileW1, MODE, 1>(a, s);
+  if (a.B <= 32) return launch_tile<2, kTileW2, MODE, 1>(a, s);
+  return launch_tile<4, kTileW4, MODE, 1>(a, s);
 }
 
 // ------------------------------------------------------------------ generic kernel
@@ -1008,19 +1157,27 @@ __global__ void __launch_bounds__(256) lm_head_generic_kernel(LmArgs a) {
   __shared__ unsigned long long red[4 * 64];
   const int v = blockIdx.x * blockDim.x + threadIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  auto logit = [&](int b) {
+    float acc = 0.0f;
+    for (int kk = 0; kk < a.H; ++kk) {
+      size_t wi = (a.layout == NVJSEL_W_VH) ? (size_t)v * a.H + kk : (size_t)kk * a.V + v;
+      acc = fmaf(load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * a.H + kk), load_as_f32(a.W, a.weight_dtype, wi),
+                 acc);
+    }
+    return apply_cast(acc, a.reduce_cast);
+  };
+  if constexpr (MODE == MODE_LOGITS) {
+    if (v < a.V)
+      for (int b = 0; b < a.B; ++b) store_logit(a, b, v, logit(b));
+    return;
+  }
   for (int b0 = 0; b0 < a.B; b0 += 64) {
     const int nb = min(64, a.B - b0);
     for (int bb = 0; bb < nb; ++bb) {
       const int b = b0 + bb;
       unsigned long long k = 0;
       if (v < a.V) {
-        float acc = 0.0f;
-        for (int kk = 0; kk < a.H; ++kk) {
-          size_t wi = (a.layout == NVJSEL_W_VH) ? (size_t)v * a.H + kk : (size_t)kk * a.V + v;
-          acc = fmaf(load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * a.H + kk),
-                     load_as_f32(a.W, a.weight_dtype, wi), acc);
-        }
-        float val = apply_cast(acc, a.reduce_cast);
+        float val = logit(b);
         if constexpr (MODE == MODE_SAMPLE) {
           float t = a.temperature[b];
           if (!(t <= 0.0f))
@@ -1074,14 +1231,14 @@ __global__ void __launch_bounds__(256) lm_zero_kernel(uint32_t* p, size_t n) {
 }
 
 // ------------------------------------------------------------------ host side
-static constexpr int kWaves = NVJSEL_LM_WAVES;
+static constexpr int kWaves = kLmWaves;
 // LDS reserved for the kernel's static shared variables (finish_rows flag).
 static constexpr size_t kStaticLdsSlack = 256;
 
 template <int WT, int NSPLIT, int NB, int KU, int MODE>
 static int launch_mfma_ku(const LmArgs& a, hipStream_t stream) {
-  constexpr int MT = (NB == 1) ? NVJSEL_LM_MT1 : NVJSEL_LM_MTN;
-  auto kern = lm_head_mfma_kernel<WT, NSPLIT, NB, MT, kWaves, KU, NVJSEL_LM_DEPTH, MODE>;
+  constexpr int MT = (NB == 1) ? kLmMt1 : kLmMtn;
+  auto kern = lm_head_mfma_kernel<WT, NSPLIT, NB, MT, kWaves, KU, kLmDepth, MODE>;
   size_t lds = (size_t)a.H * NSPLIT * NB * 16 * 2;
   size_t red = (size_t)kWaves * NB * 16 * 8;
   if (lds < red) lds = red;
@@ -1092,7 +1249,7 @@ static int launch_mfma_ku(const LmArgs& a, hipStream_t stream) {
   int per_cu = 0;
   NVJSEL_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kWaves * 64, lds));
   if (per_cu < 1) per_cu = 1;
-  if (NVJSEL_LM_BPC > 0 && per_cu > NVJSEL_LM_BPC) per_cu = NVJSEL_LM_BPC;
+  if (kLmBpc > 0 && per_cu > kLmBpc) per_cu = kLmBpc;
   const int rows = 16 * MT * kWaves;
   const int need = (a.V + rows - 1) / rows;
   int grid = per_cu * device_cu_count();
@@ -1105,19 +1262,19 @@ static int launch_mfma_ku(const LmArgs& a, hipStream_t stream) {
 // KU must divide the number of 32-wide k-steps; odd hidden sizes use KU = 1.
 template <int WT, int NSPLIT, int NB, int MODE>
 static int launch_mfma(const LmArgs& a, hipStream_t stream) {
-  if (((a.H >> 5) % NVJSEL_LM_KU) == 0) return launch_mfma_ku<WT, NSPLIT, NB, NVJSEL_LM_KU, MODE>(a, stream);
+  if (((a.H >> 5) % kLmKu) == 0) return launch_mfma_ku<WT, NSPLIT, NB, kLmKu, MODE>(a, stream);
   return launch_mfma_ku<WT, NSPLIT, NB, 1, MODE>(a, stream);
 }
 
 template <int NB, int KJ, int MODE>
 static int launch_gemv(const LmArgs& a, hipStream_t stream) {
-  constexpr int R = NVJSEL_GEMV_R;
+  constexpr int R = kGemvR;
   auto kern = lm_head_gemv_kernel<NB, R, KJ, MODE>;
   int per_cu = 0;
-  constexpr int WAVES = NVJSEL_GEMV_WAVES;
+  constexpr int WAVES = kGemvWaves;
   NVJSEL_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, WAVES * 64, 0));
   if (per_cu < 1) per_cu = 1;
-  if (NVJSEL_GEMV_BPC > 0 && per_cu > NVJSEL_GEMV_BPC) per_cu = NVJSEL_GEMV_BPC;
+  if (kGemvBpc > 0 && per_cu > kGemvBpc) per_cu = kGemvBpc;
   const int need = (a.V + R * WAVES - 1) / (R * WAVES);
   int grid = per_cu * device_cu_count();
   if (grid < 1) grid = 1;
@@ -1151,7 +1308,9 @@ static int dispatch_nb(const LmArgs& a, hipStream_t s) {
   }
 }
 
+
 static size_t lm_ws_keys_bytes(int batch) { return align_up((size_t)batch * 8, 256); }
+
 
 // Final-RMSNorm prologue request (norm_w == nullptr: hidden is already normed).
 struct Prenorm {
@@ -1163,16 +1322,56 @@ struct Prenorm {
 
 static size_t lm_prenorm_bytes(int batch, int H) { return align_up((size_t)batch * H * 4, 256); }
 
+// Dynamic LDS of lm_head_hv_kernel with NB rows: the hidden [H][NB] f32, then
+// the partial sums [WAVES][NB][512] f32 (the same bytes, reused).
+static size_t hv_lds_bytes(int nb, int H) {
+  const int p2 = nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 4 ? 4 : 8;
+  const size_t waves = p2 >= 8 ? 4 : 8;
+  const size_t a = (size_t)H * p2, b = waves * p2 * 512;
+  return (a > b ? a : b) * 4;
+}
+
+// MODE_LOGITS destination.
+struct LogitsOut {
+  void* ptr = nullptr;
+  int dtype = DT_F32;
+  long long stride = 0;
+};
+
+template <int NB, int MODE>
+static int launch_hv(const LmArgs& a, hipStream_t stream) {
+  constexpr int WAVES = NB >= 8 ? 4 : 8;
+  auto kern = lm_head_hv_kernel<NB, WAVES, MODE>;
+  const size_t lds = hv_lds_bytes(NB, a.H);
+  if (lds > 48 * 1024)
+    NVJSEL_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  hipLaunchKernelGGL(kern, dim3((a.V + 511) / 512), dim3(WAVES * 64), lds, stream, a);
+  NVJSEL_CHECK_LAUNCH("lm_head_hv_kernel");
+  return NVJSEL_OK;
+}
+
+template <int MODE>
+static int dispatch_hv(const LmArgs& a, hipStream_t s) {
+  if (a.B == 1) return launch_hv<1, MODE>(a, s);
+  if (a.B == 2) return launch_hv<2, MODE>(a, s);
+  if (a.B <= 4) return launch_hv<4, MODE>(a, s);
+  return launch_hv<8, MODE>(a, s);
+}
+
 static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const void* weight,
                          int weight_dtype, int layout, int batch, int H, int V, int reduce_cast,
                          const float* temperature, const uint32_t* keys, int32_t* out_ids,
                          float* out_best, void* workspace, size_t ws_bytes, void* stream,
-                         const Prenorm& pn = Prenorm()) {
+                         const Prenorm& pn = Prenorm(), const LogitsOut& lo = LogitsOut()) {
   clear_error();
   const bool prenorm = pn.norm_w != nullptr;
-  const char* who = mode == MODE_GREEDY ? (prenorm ? "lm_head_top1_prenorm" : "lm_head_top1")
-                                        : (prenorm ? "lm_head_sample_prenorm" : "lm_head_sample");
-  if (!hidden || !weight || !out_ids) { set_error("%s: null hidden/weight/out_ids", who); return NVJSEL_EINVAL; }
+  const char* who = mode == MODE_LOGITS ? "lm_head_logits"
+                    : mode == MODE_GREEDY ? (prenorm ? "lm_head_top1_prenorm" : "lm_head_top1")
+                                          : (prenorm ? "lm_head_sample_prenorm" : "lm_head_sample");
+  if (!hidden || !weight || (mode != MODE_LOGITS && !out_ids) || (mode == MODE_LOGITS && !lo.ptr)) {
+    set_error("%s: null hidden/weight/output", who);
+    return NVJSEL_EINVAL;
+  }
   if (batch <= 0 || H <= 0 || V <= 0) {
     set_error("%s requires non-empty dimensions (batch=%d hidden=%d vocab=%d)", who, batch, H, V);
     return NVJSEL_EINVAL;
@@ -1185,6 +1384,10 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   if (layout != NVJSEL_W_VH && layout != NVJSEL_W_HV) { set_error("%s: bad weight layout %d", who, layout); return NVJSEL_EINVAL; }
   if (reduce_cast < 0 || reduce_cast > 2) { set_error("%s: reduce_cast must be 0, 1 or 2", who); return NVJSEL_EINVAL; }
   if (mode == MODE_SAMPLE && (!temperature || !keys)) { set_error("%s: null temperature/keys", who); return NVJSEL_EINVAL; }
+  if (mode == MODE_LOGITS) {
+    if (lo.dtype != DT_F32 && lo.dtype != DT_BF16) { set_error("%s: out dtype must be f32 or bf16", who); return NVJSEL_EINVAL; }
+    if (lo.stride < V) { set_error("%s: out row stride < vocab", who); return NVJSEL_EINVAL; }
+  }
   if (prenorm) {
     if (!valid_dtype(pn.norm_dtype) || !valid_dtype(pn.act_dtype)) {
       set_error("%s: unsupported dtype (norm=%d act=%d)", who, pn.norm_dtype, pn.act_dtype);
@@ -1192,14 +1395,14 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     }
     if (!(pn.eps >= 0.0f)) { set_error("%s: eps must be >= 0", who); return NVJSEL_EINVAL; }
   }
-  const size_t need = nvjsel_lm_head_workspace_size(batch) + (prenorm ? lm_prenorm_bytes(batch, H) : 0);
-  if (!workspace || ws_bytes < need) {
+  const size_t need = mode == MODE_LOGITS ? 0 : nvjsel_lm_head_workspace_size(batch) + (prenorm ? lm_prenorm_bytes(batch, H) : 0);
+  if (need && (!workspace || ws_bytes < need)) {
     set_error("%s: workspace %zu bytes < required %zu", who, ws_bytes, need);
     return NVJSEL_EWORKSPACE;
   }
   hipStream_t s = (hipStream_t)stream;
   unsigned long long* row_keys = (unsigned long long*)workspace;
-  unsigned int* counter = (unsigned int*)((char*)workspace + lm_ws_keys_bytes(batch));
+  unsigned int* counter = need ? (unsigned int*)((char*)workspace + lm_ws_keys_bytes(batch)) : nullptr;
 
   // Paths with a fused prologue: the streaming GEMV and the bf16 tile kernel.
   // Elsewhere the prologue kernel writes the normalised hidden into the
@@ -1210,8 +1413,12 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   const bool f16_mfma = layout == NVJSEL_W_VH && weight_dtype == NVJSEL_F16 &&
                         eff_dtype == NVJSEL_F16 && (H % 32) == 0 && aligned;
   const int nsplit = (bf16_mfma && eff_dtype != NVJSEL_BF16) ? 3 : 1;
+  // streaming GEMV ([V, H] bf16): B <= 2, any activation (fp32 products on the VALU)
   const bool gemv = layout == NVJSEL_W_VH && weight_dtype == NVJSEL_BF16 && aligned && batch <= 2 &&
                     (H == 512 || H == 1024 || H == 2048);
+  // [H, V] bf16 streaming kernel, up to 8 rows per launch
+  const bool hv = layout == NVJSEL_W_HV && weight_dtype == NVJSEL_BF16 && aligned && (V % 8) == 0 &&
+                  hv_lds_bytes(batch < 8 ? batch : 8, H) + kStaticLdsSlack <= device_max_lds_per_block();
   // rows per launch: LDS holds H * nsplit * rows bf16 values
   int chunk = 0;
   if ((bf16_mfma || f16_mfma) && (size_t)H * nsplit * 16 * 2 + kStaticLdsSlack <= device_max_lds_per_block()) {
@@ -1223,8 +1430,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     if (nsplit == 3 && tiles > 1) tiles = 1;
     chunk = tiles * 16;
   }
-  const bool tile = !gemv && bf16_mfma && eff_dtype == NVJSEL_BF16 && H == 1024 &&
-                    (prenorm || (((uintptr_t)hidden) & 15) == 0) && NVJSEL_USE_TILE;
+  const bool tile = !gemv && bf16_mfma && H == 1024 && (prenorm || (((uintptr_t)hidden) & 15) == 0);
   const bool fused_prenorm = prenorm && (gemv || tile);
   if (prenorm && !fused_prenorm) {
     LmArgs p{};
@@ -1241,10 +1447,16 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     hidden = normed;
     hidden_dtype = pn.act_dtype;
   }
-  if (tile) chunk = 64;
+  if (tile) chunk = eff_dtype == NVJSEL_BF16 ? 64 : 16;
   if (gemv) chunk = 0;
+  if (hv) chunk = 8;
+  auto by_mode = [&](auto fn) -> int {
+    if (mode == MODE_GREEDY) return fn(std::integral_constant<int, MODE_GREEDY>{});
+    if (mode == MODE_SAMPLE) return fn(std::integral_constant<int, MODE_SAMPLE>{});
+    return fn(std::integral_constant<int, MODE_LOGITS>{});
+  };
   for (int b0 = 0; b0 < batch; b0 += (chunk > 0 ? chunk : batch)) {
-    LmArgs a;
+    LmArgs a{};
     const int nb = chunk > 0 ? (batch - b0 < chunk ? batch - b0 : chunk) : batch;
     a.W = weight;
     a.hidden = (const char*)hidden + (size_t)b0 * H * dtype_size(hidden_dtype);
@@ -1262,31 +1474,34 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     a.reduce_cast = reduce_cast;
     a.temperature = temperature ? temperature + b0 : nullptr;
     a.keys = keys ? keys + 2 * (size_t)b0 : nullptr;
-    a.row_keys = row_keys + b0;
+    a.row_keys = row_keys ? row_keys + b0 : nullptr;
     a.counter = counter;
-    a.out_ids = out_ids + b0;
+    a.out_ids = out_ids ? out_ids + b0 : nullptr;
     a.out_best = out_best ? out_best + b0 : nullptr;
+    a.out_logits = lo.ptr ? (char*)lo.ptr + (size_t)b0 * (size_t)lo.stride * (lo.dtype == DT_F32 ? 4 : 2) : nullptr;
+    a.out_dtype = lo.dtype;
+    a.out_stride = lo.stride;
     int rc;
     if (gemv) {
-      rc = mode == MODE_GREEDY ? dispatch_gemv<MODE_GREEDY>(a, s) : dispatch_gemv<MODE_SAMPLE>(a, s);
+      rc = by_mode([&](auto M) { return dispatch_gemv<decltype(M)::value>(a, s); });
+    } else if (hv) {
+      rc = by_mode([&](auto M) { return dispatch_hv<decltype(M)::value>(a, s); });
     } else if (tile) {
-      rc = mode == MODE_GREEDY ? dispatch_tile<MODE_GREEDY>(a, s) : dispatch_tile<MODE_SAMPLE>(a, s);
+      rc = by_mode([&](auto M) { return dispatch_tile<decltype(M)::value>(a, s); });
     } else if (chunk > 0) {
       if (f16_mfma)
-        rc = mode == MODE_GREEDY ? dispatch_nb<DT_F16, 1, MODE_GREEDY>(a, s) : dispatch_nb<DT_F16, 1, MODE_SAMPLE>(a, s);
+        rc = by_mode([&](auto M) { return dispatch_nb<DT_F16, 1, decltype(M)::value>(a, s); });
       else if (nsplit == 1)
-        rc = mode == MODE_GREEDY ? dispatch_nb<DT_BF16, 1, MODE_GREEDY>(a, s) : dispatch_nb<DT_BF16, 1, MODE_SAMPLE>(a, s);
+        rc = by_mode([&](auto M) { return dispatch_nb<DT_BF16, 1, decltype(M)::value>(a, s); });
       else
-        rc = mode == MODE_GREEDY ? launch_mfma<DT_BF16, 3, 1, MODE_GREEDY>(a, s)
-                                 : launch_mfma<DT_BF16, 3, 1, MODE_SAMPLE>(a, s);
+        rc = by_mode([&](auto M) { return launch_mfma<DT_BF16, 3, 1, decltype(M)::value>(a, s); });
     } else {
       const int grid = (V + 255) / 256;
-      if (mode == MODE_GREEDY)
-        hipLaunchKernelGGL(lm_head_generic_kernel<MODE_GREEDY>, dim3(grid), dim3(256), 0, s, a);
-      else
-        hipLaunchKernelGGL(lm_head_generic_kernel<MODE_SAMPLE>, dim3(grid), dim3(256), 0, s, a);
-      NVJSEL_CHECK_LAUNCH("lm_head_generic_kernel");
-      rc = NVJSEL_OK;
+      rc = by_mode([&](auto M) -> int {
+        hipLaunchKernelGGL(lm_head_generic_kernel<decltype(M)::value>, dim3(grid), dim3(256), 0, s, a);
+        NVJSEL_CHECK_LAUNCH("lm_head_generic_kernel");
+        return (int)NVJSEL_OK;
+      });
     }
     if (rc != NVJSEL_OK) return rc;
   }
@@ -1373,6 +1588,17 @@ extern "C" int nvjsel_lm_head_top1(const void* hidden, int hidden_dtype, const v
   return lm_head_entry(MODE_GREEDY, hidden, hidden_dtype, weight, weight_dtype, weight_layout, batch,
                        hidden_dim, vocab, reduce_cast, nullptr, nullptr, out_ids, out_best, workspace,
                        workspace_bytes, stream);
+}
+
+extern "C" int nvjsel_lm_head_logits(const void* hidden, int hidden_dtype, const void* weight, int weight_dtype,
+                                     int weight_layout, int batch, int hidden_dim, int vocab, int reduce_cast,
+                                     void* out_logits, int out_dtype, int64_t out_row_stride, void* stream) {
+  LogitsOut lo;
+  lo.ptr = out_logits;
+  lo.dtype = out_dtype;
+  lo.stride = out_row_stride;
+  return lm_head_entry(MODE_LOGITS, hidden, hidden_dtype, weight, weight_dtype, weight_layout, batch, hidden_dim,
+                       vocab, reduce_cast, nullptr, nullptr, nullptr, nullptr, nullptr, 0, stream, Prenorm(), lo);
 }
 
 extern "C" size_t nvjsel_lm_head_prenorm_workspace_size(int batch, int hidden_dim) {

@@ -55,9 +55,6 @@ static constexpr int kRowPad8 = 32;  // uint64 words
 
 enum { STATE_DONE = 1, STATE_HEAVY = 2, STATE_NEEDS_GUMBEL = 3, STATE_TOPP = 4 };
 
-#ifndef NVJSEL_SAMPLE_ONEPASS
-#define NVJSEL_SAMPLE_ONEPASS 1  // calls without top-k/top-p arrays: one-pass Gumbel-max
-#endif
 static constexpr int kThreads = 256;
 static constexpr int kEPT = 32;                    // elements per thread in chunk kernels
 static constexpr int kChunk = kThreads * kEPT;     // 8192 elements per block
@@ -1963,7 +1960,7 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   // round on the device (8 per CU): a latency-bound call saves the scan and
   // select launches; larger ones keep the seeded, pruned Gumbel pass
   const int nsub = (vocab + kThreads * kGumbelEPT - 1) / (kThreads * kGumbelEPT);
-  if (!top_k && !top_p && NVJSEL_SAMPLE_ONEPASS && (long long)batch * nsub <= 8LL * device_cu_count()) {
+  if (!top_k && !top_p && (long long)batch * nsub <= 8LL * device_cu_count()) {
     NVJSEL_LAUNCH_CHUNK(sample_onepass_kernel, dim3(nsub, batch));
     hipLaunchKernelGGL(sample_onepass_finish_kernel, dim3(batch), dim3(64), 0, s, a, nsub);
     NVJSEL_CHECK_LAUNCH("sample_onepass_finish_kernel");

@@ -16,6 +16,7 @@ from .selection import (
     derive_rng_keys,
     derive_rng_keys_from_table,
     lm_head_greedy_top1_hip,
+    lm_head_logits_hip,
     lm_head_sample_token_ids,
     lm_head_token_ids_and_topk,
     mtp_greedy_top1_token_ids,
@@ -36,6 +37,7 @@ __all__ = [
     "load",
     "lm_head_greedy_top1_hip",
     "lm_head_greedy_top1_impl",
+    "lm_head_logits_hip",
     "lm_head_sample_token_ids",
     "lm_head_token_ids_and_topk",
     "mtp_greedy_top1_token_ids",

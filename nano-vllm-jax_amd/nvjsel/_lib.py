@@ -29,6 +29,7 @@ SIGNATURES = {
     "nvjsel_lm_head_top1": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "nvjsel_lm_head_top1_noalloc": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
     "nvjsel_lm_head_sample": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "nvjsel_lm_head_logits": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _i64, _vp]),
     "nvjsel_lm_head_prenorm_workspace_size": (_sz, [_i, _i]),
     "nvjsel_rms_norm": (_i, [_vp, _i, _vp, _i, _f, _i, _i, _i, _vp, _vp]),
     "nvjsel_lm_head_top1_prenorm": (_i, [_vp, _i, _vp, _i, _f, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp,

@@ -243,8 +243,9 @@ def lm_head_sample_token_ids(hidden_norm: torch.Tensor, output_weight: torch.Ten
     """Sample token ids from the LM head (model.py:901-938).
 
     Without top-k/top-p the projection and the Gumbel-max are fused and no
-    logits are written.  With them, the logits are formed once (a library
-    GEMM, rounded as the reference's dot) and handed to the sampler.
+    logits are written.  With them, the logits are formed once by the
+    library's LM-head kernels (rounded as the reference's dot) and handed to
+    the sampler.
     ``norm_weight`` selects the pre-norm input as in lm_head_greedy_top1_hip."""
     x = _flatten_hidden(hidden_norm, require_3d=False)
     batch, hidden_dim = int(x.shape[0]), int(x.shape[1])
@@ -263,11 +264,7 @@ def lm_head_sample_token_ids(hidden_norm: torch.Tensor, output_weight: torch.Ten
         x = rms_norm_hip(x, norm_weight, rms_norm_eps, act)
         norm_weight = None
     if top_k is not None or top_p is not None:
-        wt = w.T if layout == _lib.W_VH else w
-        if rc:
-            logits = torch.matmul(x, wt).float()
-        else:
-            logits = torch.matmul(x.float(), wt.float())
+        logits = _dense_logits(x, w, layout, vocab, rc)
         return sample_token_ids(logits, temperatures, rng_keys, top_k=top_k, top_p=top_p)
     temps = temperatures.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
     if temps.numel() != batch:
@@ -288,6 +285,38 @@ def lm_head_sample_token_ids(hidden_norm: torch.Tensor, output_weight: torch.Ten
                   w.data_ptr(), wd, layout, batch, hidden_dim, vocab, rc, temps.data_ptr(), keys.data_ptr(),
                   out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
     return out
+
+
+def _dense_logits(x: torch.Tensor, w: torch.Tensor, layout: int, vocab: int, rc: int) -> torch.Tensor:
+    """Logits ``[B, V]`` of ``x [B, H]`` against the weight operand, from the
+    library's LM-head kernels (nvjsel_lm_head_logits): fp32 accumulation
+    rounded as the reference's dot (``rc``); stored bf16 when they are
+    bf16-rounded, f32 otherwise."""
+    batch, hidden_dim = int(x.shape[0]), int(x.shape[1])
+    dev = _require_cuda(x, w)
+    x = x.contiguous()
+    out_dtype = torch.bfloat16 if rc == 1 else torch.float32
+    out = torch.empty((batch, vocab), dtype=out_dtype, device=dev)
+    _lib.call("nvjsel_lm_head_logits", x.data_ptr(), _dtype_code(x, "hidden"), w.data_ptr(),
+              _dtype_code(w, "weight"), layout, batch, hidden_dim, vocab, rc, out.data_ptr(),
+              _TORCH_DTYPES[out_dtype], vocab, _stream_handle(dev))
+    return out
+
+
+def lm_head_logits_hip(hidden_norm: torch.Tensor, output_weight: torch.Tensor, *,
+                       weight_layout: str | None = None, reduce_cast: int | None = None) -> torch.Tensor:
+    """Dense LM-head logits ``[B, V]`` (``jnp.dot(hidden_norm, W)``,
+    model.py:765-780): fp32 accumulation; bf16 x bf16 gives bf16 logits (the
+    reference's dot output), other operand types f32 logits."""
+    x = _flatten_hidden(hidden_norm, require_3d=False)
+    batch, hidden_dim = int(x.shape[0]), int(x.shape[1])
+    if batch <= 0 or hidden_dim <= 0 or output_weight.numel() == 0:
+        raise ValueError("LM-head logits require non-empty dimensions")
+    _dtype_code(x, "hidden")
+    _dtype_code(output_weight, "weight")
+    w, layout, vocab = _weight_operand(output_weight, weight_layout, hidden_dim)
+    rc = reference_reduce_cast(x.dtype, w.dtype) if reduce_cast is None else int(reduce_cast)
+    return _dense_logits(x, w, layout, vocab, rc)
 
 
 def rms_norm_hip(hidden: torch.Tensor, norm_weight: torch.Tensor, eps: float = 1e-6,
@@ -386,11 +415,7 @@ def lm_head_token_ids_and_topk(hidden: torch.Tensor, output_weight: torch.Tensor
     w, layout, vocab = _weight_operand(output_weight, weight_layout, hidden_dim)
     x = flat if norm_weight is None else rms_norm_hip(flat, norm_weight, rms_norm_eps, act_dtype)
     rc = reference_reduce_cast(x.dtype, w.dtype) if reduce_cast is None else int(reduce_cast)
-    wt = w.T if layout == _lib.W_VH else w
-    if rc:
-        logits = torch.matmul(x.contiguous(), wt)
-    else:
-        logits = torch.matmul(x.float(), wt.float())
+    logits = _dense_logits(x.contiguous(), w, layout, vocab, rc)
     values, indices = topk_hip(logits, int(top_k))
     ids = indices[:, 0].reshape(batch, width)
     return ids, values.reshape(batch, width, -1), indices.reshape(batch, width, -1)

@@ -1,0 +1,222 @@
+"""GPU parity of the LM-head paths added for the reference's other operating
+points, against the float64 oracle:
+
+* the [H, V] weight layout (the reference's materialised lm_head,
+  configs/server/gpu_optimal.yaml:56, load_weights.py:256-258; the layout
+  lm_head_triton.py:51-55 reads) -- the streaming [H, V] kernel, B <= 8 per
+  launch;
+* fp32 activations (lm_head_decode_act_dtype's default, config.py:120;
+  model.py:277-285) at 3 <= B <= 8 on the [V, H] table -- one W pass, exact
+  fp32 products;
+* dense logits (nvjsel_lm_head_logits) on every path, and the routes built on
+  them: top-k values / indices (model.py:866-898) and top-k / top-p sampling
+  from the hidden state -- no vendor GEMM.
+"""
+import numpy as np
+import pytest
+import torch
+
+import nvjsel
+from oracle import selection as sel
+from tests.gpu_helpers import (as_f32, bf16_tensor, check_fused_sampled, check_greedy, check_sampled,
+                               engine_keys, keys_tensor)
+
+pytestmark = pytest.mark.gpu
+
+
+def _hidden(rng, B, H, dtype):
+    h = torch.from_numpy(rng.standard_normal((B, H)).astype(np.float32)).cuda()
+    return h.to(dtype)
+
+
+def _check_logits(got: torch.Tensor, h: np.ndarray, w_vh: np.ndarray, rc: int, ctx: str):
+    """Logits against the float64 dot z = h . w.  An fp32 accumulation of H
+    products (any order) is within H * 2^-24 * A of z, A = sum |h_k w_k|
+    (the standard summation bound); the rounding (rc) adds at most half an
+    ulp of the rounded value.  Almost every value must also equal the
+    rounded exact logit."""
+    h64, w64 = np.asarray(h, np.float64), np.asarray(w_vh, np.float64)
+    z64 = h64 @ w64.T
+    A = np.abs(h64) @ np.abs(w64).T
+    H = h64.shape[1]
+    g = got.float().cpu().numpy().astype(np.float64)
+    assert g.shape == z64.shape, ctx
+    acc = H * 2.0 ** -24 * A
+    if rc == 0:
+        err = np.abs(g - z64)
+        assert np.all(err <= acc + 1e-30), (ctx, float((err / (acc + 1e-30)).max()))
+        return
+    rnd = sel.round_bf16 if rc == 1 else sel.round_f16
+    half_ulp = (2.0 ** -8 if rc == 1 else 2.0 ** -11) * np.abs(g)
+    err = np.abs(g - z64)
+    assert np.all(err <= acc + half_ulp + 1e-30), (ctx, float((err / (acc + half_ulp + 1e-30)).max()))
+    exp = rnd(z64.astype(np.float32)).astype(np.float64)
+    frac = float(np.mean(g == exp))
+    assert frac > 0.995, (ctx, frac)
+
+
+@pytest.mark.parametrize("B", [1, 2, 3, 5, 8, 13])
+@pytest.mark.parametrize("act", [torch.bfloat16, torch.float32])
+def test_hv_layout_greedy(B, act):
+    rng = np.random.default_rng(100 + B)
+    H, V = 1024, 20008
+    Wvh = (rng.standard_normal((V, H)) * 0.03).astype(np.float32)
+    Whv = torch.from_numpy(Wvh.T.copy()).cuda().to(torch.bfloat16)  # [H, V] contiguous
+    h = _hidden(rng, B, H, act)
+    ids = nvjsel.lm_head_greedy_top1_hip(h, Whv, weight_layout="hv")
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(h.float().cpu().numpy(), Whv.float().cpu().numpy(), weight_layout="hv")
+    rc = 1 if act == torch.bfloat16 else 0
+    check_greedy(ids.cpu().numpy().reshape(-1), z, rc, f"hv B={B} {act}")
+
+
+@pytest.mark.parametrize("H", [256, 512, 100])
+def test_hv_layout_other_hidden_sizes(H):
+    rng = np.random.default_rng(H)
+    B, V = 4, 3000
+    Whv = bf16_tensor(rng.standard_normal((H, V)) * 0.05)
+    h = _hidden(rng, B, H, torch.bfloat16)
+    ids = nvjsel.lm_head_greedy_top1_hip(h, Whv, weight_layout="hv")
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(as_f32(h), as_f32(Whv), weight_layout="hv")
+    check_greedy(ids.cpu().numpy().reshape(-1), z, 1, f"hv H={H}")
+
+
+def test_hv_layout_sample():
+    rng = np.random.default_rng(7)
+    B, H, V = 6, 1024, 20008
+    Whv = bf16_tensor(rng.standard_normal((H, V)) * 0.05)
+    h = _hidden(rng, B, H, torch.bfloat16)
+    T = [0.0, 0.7, 1.0, 1.5, 0.0, 1.0]
+    keys = engine_keys(B, 9)
+    ids = nvjsel.lm_head_sample_token_ids(h, Whv, temperatures=torch.tensor(T).cuda(), rng_keys=keys_tensor(keys),
+                                          weight_layout="hv")
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(as_f32(h), as_f32(Whv), weight_layout="hv")
+    assert check_fused_sampled(ids.cpu().numpy(), z, T, keys, 1, "hv sample") <= 1
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_hv_layout_full_vocab(B):
+    """The promoted serving layout at the BASELINE shape: W [1024, 248320] bf16."""
+    import bench
+
+    dev = torch.device("cuda:0")
+    Whv = bench.lm_weight(torch, dev).T.contiguous()
+    g = torch.Generator(device=dev)
+    g.manual_seed(50 + B)
+    h = torch.randn(B, 1024, device=dev, generator=g).to(torch.bfloat16)
+    ids = nvjsel.lm_head_greedy_top1_hip(h, Whv, weight_layout="hv")
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(as_f32(h), as_f32(Whv), weight_layout="hv")
+    check_greedy(ids.cpu().numpy().reshape(-1), z, 1, f"hv full B={B}")
+
+
+@pytest.mark.parametrize("B", [3, 4, 6, 8])
+def test_fp32_activations_one_pass(B):
+    """fp32 hidden x bf16 [V, H] (the reference's default decode activation):
+    fp32 logits, no rounding."""
+    rng = np.random.default_rng(200 + B)
+    H, V = 1024, 30011
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.03)
+    h = _hidden(rng, B, H, torch.float32)
+    ids = nvjsel.lm_head_greedy_top1_hip(h, W, weight_layout="vh")
+    torch.cuda.synchronize()
+    check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(as_f32(h), as_f32(W)), 0, f"f32 act B={B}")
+
+
+def test_fp32_activations_full_vocab_b8():
+    import bench
+
+    dev = torch.device("cuda:0")
+    W = bench.lm_weight(torch, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    h = torch.randn(8, 1024, device=dev, generator=g)
+    ids = nvjsel.lm_head_greedy_top1_hip(h, W, weight_layout="vh")
+    torch.cuda.synchronize()
+    check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(as_f32(h), as_f32(W)), 0, "f32 act full B=8")
+
+
+def test_fp32_activations_sample():
+    rng = np.random.default_rng(3)
+    B, H, V = 7, 1024, 20011
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    h = _hidden(rng, B, H, torch.float32)
+    T = [1.0, 0.0, 0.6, 1.0, 2.0, 0.8, 1.0]
+    keys = engine_keys(B, 4)
+    ids = nvjsel.lm_head_sample_token_ids(h, W, temperatures=torch.tensor(T).cuda(), rng_keys=keys_tensor(keys),
+                                          weight_layout="vh")
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(as_f32(h), as_f32(W))
+    assert check_fused_sampled(ids.cpu().numpy(), z, T, keys, 0, "f32 act sample") <= 1
+
+
+# (B, H, layout, act, weight dtype): streaming [V,H] B<=2, fp32 B<=8, tile 3..64 and
+# 64-row chunks, [H,V], f16 MFMA, generic (H not a multiple of 32)
+LOGIT_CASES = [
+    (1, 1024, "vh", torch.bfloat16, torch.bfloat16),
+    (2, 512, "vh", torch.float32, torch.bfloat16),
+    (6, 1024, "vh", torch.float32, torch.bfloat16),
+    (40, 1024, "vh", torch.bfloat16, torch.bfloat16),
+    (70, 1024, "vh", torch.bfloat16, torch.bfloat16),
+    (5, 1024, "hv", torch.bfloat16, torch.bfloat16),
+    (11, 1024, "hv", torch.float32, torch.bfloat16),
+    (20, 1024, "vh", torch.float32, torch.bfloat16),
+    (9, 256, "vh", torch.float16, torch.float16),
+    (3, 40, "vh", torch.bfloat16, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("B,H,layout,act,wdt", LOGIT_CASES)
+def test_dense_logits_match_float64(B, H, layout, act, wdt):
+    rng = np.random.default_rng(B * 1000 + H)
+    V = 5008
+    Wvh = torch.from_numpy((rng.standard_normal((V, H)) * 0.05).astype(np.float32)).to(wdt).cuda()
+    W = Wvh if layout == "vh" else Wvh.T.contiguous()
+    h = _hidden(rng, B, H, act)
+    logits = nvjsel.lm_head_logits_hip(h, W, weight_layout=layout)
+    torch.cuda.synchronize()
+    rc = nvjsel.reference_reduce_cast(act, wdt)
+    assert logits.dtype == (torch.bfloat16 if rc == 1 else torch.float32)
+    _check_logits(logits, h.float().cpu().numpy(), Wvh.float().cpu().numpy(), rc, f"{B},{H},{layout},{act},{wdt}")
+
+
+@pytest.mark.parametrize("top_k", [1, 8, 50])
+@pytest.mark.parametrize("layout", ["vh", "hv"])
+def test_lm_head_topk_route_native(top_k, layout):
+    """lm_head_token_ids_and_topk(top_k > 0): the library's logits (checked
+    against float64) and lax.top_k order over them, bitwise."""
+    rng = np.random.default_rng(top_k)
+    B, H, V = 6, 1024, 30008
+    Wvh = bf16_tensor(rng.standard_normal((V, H)) * 0.03)
+    W = Wvh if layout == "vh" else Wvh.T.contiguous()
+    h = _hidden(rng, B, H, torch.bfloat16)
+    ids, vals, idx = nvjsel.lm_head_token_ids_and_topk(h[:, None, :], W, top_k=top_k, weight_layout=layout)
+    logits = nvjsel.lm_head_logits_hip(h, W, weight_layout=layout)
+    torch.cuda.synchronize()
+    _check_logits(logits, as_f32(h), as_f32(Wvh), 1, "topk route logits")
+    ev, ei = sel.topk(logits.float().cpu().numpy(), top_k)
+    assert np.array_equal(idx.cpu().numpy().reshape(B, top_k), ei)
+    assert np.array_equal(vals.cpu().numpy().reshape(B, top_k).view(np.uint32), ev.view(np.uint32))
+    assert np.array_equal(ids.cpu().numpy().reshape(-1), ei[:, 0])
+
+
+def test_hidden_to_filtered_sampling_native():
+    """lm_head_sample_token_ids with top_k / top_p: library logits, then the
+    sampler; ids against the oracle over the same logits."""
+    rng = np.random.default_rng(11)
+    B, H, V = 8, 1024, 30008
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    h = _hidden(rng, B, H, torch.bfloat16)
+    T = [0.0, 0.7, 1.0, 1.0, 0.9, 1.2, 0.5, 1.0]
+    K = [0, 20, 0, 100, 5, 0, 50, 0]
+    P = [1.0, 1.0, 0.9, 0.8, 1.0, 0.95, 0.7, 1.0]
+    keys = engine_keys(B, 2)
+    ids = nvjsel.lm_head_sample_token_ids(h, W, temperatures=torch.tensor(T).cuda(), rng_keys=keys_tensor(keys),
+                                          top_k=torch.tensor(K, dtype=torch.int32).cuda(),
+                                          top_p=torch.tensor(P).cuda(), weight_layout="vh")
+    logits = nvjsel.lm_head_logits_hip(h, W, weight_layout="vh")
+    torch.cuda.synchronize()
+    _check_logits(logits, as_f32(h), as_f32(W), 1, "filtered sampling logits")
+    check_sampled(ids.cpu().numpy(), logits.float().cpu().numpy(), T, K, P, keys, ctx="hidden->filtered")

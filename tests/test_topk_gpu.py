@@ -95,7 +95,9 @@ def test_lm_head_token_ids_and_topk_width(top_k):
         check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(h.reshape(-1, H), E), 1, "width")
         return
     assert tuple(vals.shape) == (B, Wd, top_k) and tuple(idx.shape) == (B, Wd, top_k)
-    logits = torch.matmul(ht.reshape(-1, H), Et.T).float().cpu().numpy()  # the route's own dense logits
+    # the route's dense logits come from the library (checked against float64
+    # in test_lm_head_paths_gpu.py); top-k over them is bitwise
+    logits = nvjsel.lm_head_logits_hip(ht.reshape(-1, H), Et, weight_layout="vh").float().cpu().numpy()
     ev, ei = sel.topk(logits, top_k)
     assert np.array_equal(idx.cpu().numpy().reshape(-1, top_k), ei)
     assert np.array_equal(vals.cpu().numpy().reshape(-1, top_k), ev)
