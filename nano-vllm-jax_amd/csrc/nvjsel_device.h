@@ -15,7 +15,57 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace nvjsel {
+
+// ---------------------------------------------------------------- software pipelining
+// Lambdas that take a register array by reference must inline, or the array
+// is placed in scratch memory.
+#define NVJSEL_INLINE __attribute__((always_inline))
+
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
+// Software pipeline over items 0..n-1 with a DEPTH-slot register ring:
+// load(slot, j) requests item j into ring slot `slot`; body(slot, i) consumes
+// item i.  The loop is unrolled by DEPTH so every slot index is a compile-time
+// constant and no register holding an in-flight load is ever copied (a copy
+// would wait for the load, collapsing the ring to one item in flight).  The
+// main loop issues its loads unconditionally, so the compiler's wait counts
+// keep DEPTH - 1 items in flight; only the tail tests bounds.  pre() runs
+// once the first loads are issued, so set-up work overlaps them.
+struct NoPrologue {
+  __device__ void operator()() const {}
+};
+
+template <int DEPTH, typename Load, typename Body, typename Pre = NoPrologue>
+__device__ __forceinline__ void ring_pipeline(int n, Load&& load, Body&& body, Pre&& pre = Pre()) {
+  static_for<DEPTH - 1>([&](auto D) NVJSEL_INLINE {
+    if (decltype(D)::value < n) load(D, (int)decltype(D)::value);
+  });
+  pre();  // work that can overlap the first loads
+  int i = 0;
+  for (; i + 2 * DEPTH - 2 < n; i += DEPTH)
+    static_for<DEPTH>([&](auto D) NVJSEL_INLINE {
+      constexpr int d = decltype(D)::value;
+      load(std::integral_constant<int, (d + DEPTH - 1) % DEPTH>{}, i + d + DEPTH - 1);
+      body(D, i + d);
+    });
+  for (; i < n; i += DEPTH)
+    static_for<DEPTH>([&](auto D) NVJSEL_INLINE {
+      constexpr int d = decltype(D)::value;
+      if (i + d < n) {
+        if (i + d + DEPTH - 1 < n) load(std::integral_constant<int, (d + DEPTH - 1) % DEPTH>{}, i + d + DEPTH - 1);
+        body(D, i + d);
+      }
+    });
+}
 
 // ---------------------------------------------------------------- Threefry-2x32-20
 __device__ __forceinline__ uint32_t rotl32(uint32_t v, int r) {

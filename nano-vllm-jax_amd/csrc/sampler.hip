@@ -27,9 +27,11 @@
 //                 queues the chunks that can hold its winner.
 //   3. gumbel     one block per queued chunk quarter: Gumbel-max over
 //                 x >= tau; top-p-only rows score x above the crossing bin and
-//                 collect the bin's elements.  The row's last block writes its id.
-//   4. topp finish grid (B), top-p-only rows: exact threshold inside the
-//                 crossing bin and the final id.
+//                 collect the bin's elements.  Each block folds its best
+//                 into the row's best key (one atomic max).
+//   4. finish     grid (B): rows the gumbel pass scored take their id from
+//                 the row's best key; top-p-only rows first find the exact
+//                 threshold inside the crossing bin.
 //
 // Top-k survivors' masses are exp(x - max) in 2^-40 fixed point summed in
 // 64-bit integers; top-p-only rows use integer weights per grid bin combined
@@ -48,9 +50,8 @@
 namespace nvjsel {
 
 enum { ROW_GREEDY = 0, ROW_FULL = 1, ROW_FILTER = 2 };
-// Per-row words hit by same-address atomics from many blocks (best key,
-// finished-item counter) each get a 256-byte line of their own.
-static constexpr int kRowPad = 64;   // uint32 words
+// The per-row best key, hit by same-address atomics from many blocks, gets a
+// 256-byte line of its own.
 static constexpr int kRowPad8 = 32;  // uint64 words
 
 enum { STATE_DONE = 1, STATE_HEAVY = 2, STATE_NEEDS_GUMBEL = 3, STATE_TOPP = 4 };
@@ -94,8 +95,6 @@ struct SampleArgs {
   uint32_t* topp_n;                // [B]
   uint32_t* list_n;                // [2]   rows queued for gumbel, for top-p
   uint32_t* list_gumbel;           // [B * nchunks] gumbel items: row << 16 | chunk
-  uint32_t* row_done;              // [B * kRowPad] gumbel items finished per row
-  uint32_t* row_items;             // [B * kRowPad] gumbel items queued per row
   int32_t* out_ids;
   float* lane_tops;                // [B, nchunks, 4 waves, kTopsPub] largest raw-logit lane maxima
   int topk;  // > 0: top-k selection (nvjsel_topk): every row FILTER with this k on raw logits
@@ -732,23 +731,34 @@ __device__ __forceinline__ float decode16(uint32_t h) {
   return DT == DT_BF16 ? __uint_as_float(h << 16) : f16_to_f32((uint16_t)h);
 }
 
-template <int DT, int VEC>
-__device__ __forceinline__ void scan_load(const char* row, int base, int V, ChunkRegs<DT, VEC>& r) {
-  constexpr int Q = ChunkRegs<DT, VEC>::Q;
+// Issues the loads of a thread's raw chunk words (no use of them): vectors
+// past the row's end re-read its last vector -- duplicates of row elements,
+// harmless to the maximum and masked everywhere else.  Streaming loads: the
+// logits are read once.
+template <int DT, int VEC, int Q, int W>
+__device__ __forceinline__ void scan_issue(const char* row, int base, int V, uint32_t (&w)[Q][W]) {
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
     const int i0 = base + (q * kThreads + (int)threadIdx.x) * VEC;
-    r.vok[q] = i0 < V;
-    // vectors past the row's end re-read its last vector: duplicates of row
-    // elements, harmless to the maximum and masked everywhere else
-    const int j = r.vok[q] ? i0 : V - VEC;
+    const int j = i0 < V ? i0 : V - VEC;
     if constexpr (VEC == 1) {
-      r.w[q][0] = DT == DT_F32 ? ((const uint32_t*)row)[j] : (uint32_t)((const uint16_t*)row)[j];
+      w[q][0] = DT == DT_F32 ? __builtin_nontemporal_load((const uint32_t*)row + j)
+                             : (uint32_t)__builtin_nontemporal_load((const uint16_t*)row + j);
     } else {
-      const uint4 v = DT == DT_F32 ? *(const uint4*)((const float*)row + j) : *(const uint4*)((const uint16_t*)row + j);
-      r.w[q][0] = v.x; r.w[q][1] = v.y; r.w[q][2] = v.z; r.w[q][3] = v.w;
+      const u32x4v v = __builtin_nontemporal_load(DT == DT_F32 ? (const u32x4v*)((const float*)row + j)
+                                                               : (const u32x4v*)((const uint16_t*)row + j));
+      w[q][0] = v.x; w[q][1] = v.y; w[q][2] = v.z; w[q][3] = v.w;
     }
   }
+}
+
+// The per-vector summaries of loaded raw words (r.w filled).
+template <int DT, int VEC>
+__device__ __forceinline__ void scan_finish(int base, int V, ChunkRegs<DT, VEC>& r) {
+  constexpr int Q = ChunkRegs<DT, VEC>::Q;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) r.vok[q] = base + (q * kThreads + (int)threadIdx.x) * VEC < V;
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
     if constexpr (VEC == 1) {
@@ -828,19 +838,17 @@ __device__ __forceinline__ uint32_t wave_kth_prefix(float v, bool ok, uint32_t k
   return p;
 }
 
+// One (row b, chunk c) item of the scan; r holds its raw words.  Block-uniform.
 template <int DT, int VEC>
-__global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
+__device__ __forceinline__ void scan_item(const SampleArgs& a, int b, int c, ChunkRegs<DT, VEC>& r,
+                                          ScanShared& sh) {
   constexpr int Q = kEPT / VEC;
-  __shared__ ScanShared sh;
-  const int b = blockIdx.y, c = blockIdx.x;
   const RowParams rp = row_params(a, b);
-  const char* row = row_ptr(a, b);
   const int base = c * kChunk;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // Raw logits: x = l / T' is monotone in l, so maxima and the candidate test
   // run on l and only candidates pay for the division.
-  ChunkRegs<DT, VEC> r;
-  scan_load<DT, VEC>(row, base, a.V, r);
+  scan_finish<DT, VEC>(base, a.V, r);
   float tm = r.vmax[0];
   bool tn = r.vnan[0];
 #pragma unroll
@@ -898,7 +906,6 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   }
   if (threadIdx.x == 0) {
     a.chunk_max[(size_t)b * a.nchunks + c] = cbest;
-    if (c == 0) a.row_done[(size_t)b * kRowPad] = 0;
     if (b == 0 && c == 0) a.list_n[0] = 0;  // this call's work list
   }
   if (topp_row) {
@@ -1004,6 +1011,17 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
       a.cand_floor_a[(size_t)b * a.nchunks + c] = th_a;
     }
   }
+}
+
+// One block per (chunk, row) item: every load of the chunk is issued at once,
+// then the item is processed.
+template <int DT, int VEC>
+__global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
+  __shared__ ScanShared sh;
+  const int b = blockIdx.y, c = blockIdx.x;
+  ChunkRegs<DT, VEC> r;
+  scan_issue<DT, VEC>(row_ptr(a, b), c * kChunk, a.V, r.w);
+  scan_item<DT, VEC>(a, b, c, r, sh);
 }
 
 // ------------------------------------------------------------------ 2. select
@@ -1315,6 +1333,7 @@ __global__ void __launch_bounds__(kThreads) topk_select_kernel(SampleArgs a, flo
 // of the scan, for the VALU-heavy noise.
 static constexpr int kGumbelEPT = 8;
 static constexpr int kGumbelSplit = kEPT / kGumbelEPT;
+static constexpr int kGumbelBlocksPerCu = 16;  // gumbel-pass grid: blocks per CU (measured: 16 > 8, uncapped)
 
 // Scratch of queue_chunks.
 struct QueueShared {
@@ -1345,7 +1364,6 @@ __device__ __forceinline__ void queue_chunks(const SampleArgs& a, int b, const R
   (void)block_exclusive_scan<uint32_t>(mine, q.wsum, total);
   if (threadIdx.x == 0) {
     q.base = total ? atomicAdd(&a.list_n[0], total) : 0u;
-    a.row_items[(size_t)b * kRowPad] = total * (uint32_t)kGumbelSplit;
     if (total == 0) a.out_ids[b] = (int32_t)(~(uint32_t)best);
   }
   __syncthreads();
@@ -1546,7 +1564,7 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
   }
   mk = block_max_u64(mk, s.red);
   if (rp.mode == ROW_GREEDY) {  // the row's first maximum
-    if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)mk);
+    if (threadIdx.x == 0) { a.out_ids[b] = (int32_t)(~(uint32_t)mk); a.row_state[b] = STATE_DONE; }
     return;
   }
   const float ml = unord_f32((uint32_t)(mk >> 32));
@@ -1687,24 +1705,22 @@ __device__ __forceinline__ void gumbel_item(const SampleArgs& a, uint32_t item, 
       }
   }
   const unsigned long long best = block_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, act, s_cur, sh);
-  // The row's last item writes its id.  A block whose best does not exceed
-  // the value it read skips the max (the row's best only grows), halving the
-  // same-address atomics; each row's counters sit on their own cache lines.
-  if (threadIdx.x == 0) {
-    const unsigned long long prev = best > seen ? atomicMax(rk, best) : 0ull;
-    uint32_t* done = &a.row_done[(size_t)b * kRowPad];
-    if (atomicAdd(done + after(prev), 1u) == a.row_items[(size_t)b * kRowPad] - 1u)
-      a.out_ids[b] = (int32_t)(~(uint32_t)load_row_best(rk));
-  }
+  // The finish kernel turns the row's best into its id.  A block whose best
+  // does not exceed the value it read skips the max (the row's best only
+  // grows); each row's best sits on a cache line of its own.
+  if (threadIdx.x == 0 && best > seen) atomicMax(rk, best);
 }
 
-// One block per possible item quarter; blocks past the queued items exit at once.
+// The queued item quarters, grid-stride: a grid of one round of resident
+// blocks (dispatching a block that exits at once still costs the dispatcher).
 template <int DT, int VEC>
 __global__ void __launch_bounds__(kThreads) sample_gumbel_kernel(SampleArgs a) {
   __shared__ GumbelShared sh;
-  const uint32_t it = blockIdx.x / kGumbelSplit;
-  if (it >= a.list_n[0]) return;
-  gumbel_item<DT, VEC>(a, a.list_gumbel[it], (int)(blockIdx.x % kGumbelSplit), sh);
+  const uint32_t n = a.list_n[0] * (uint32_t)kGumbelSplit;
+  for (uint32_t q = blockIdx.x; q < n; q += gridDim.x) {
+    gumbel_item<DT, VEC>(a, a.list_gumbel[q / kGumbelSplit], (int)(q % kGumbelSplit), sh);
+    __syncthreads();  // the next item reuses the LDS
+  }
 }
 
 // ------------------------------------------------------------------ one pass (no top-k, no top-p)
@@ -1760,8 +1776,10 @@ __global__ void __launch_bounds__(64) sample_onepass_finish_kernel(SampleArgs a,
   if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)m);
 }
 
-// ------------------------------------------------------------------ 5. top-p rows: finish
-// After the gumbel pass: the exact threshold tau inside the crossing bin (the
+// ------------------------------------------------------------------ 5. finish
+// After the gumbel pass (a kernel boundary orders its atomic maxima before
+// these reads): rows it scored take the id of their best key.  Top-p-only
+// rows first find the exact threshold tau inside the crossing bin (the
 // largest key whose weight from the top of the bin reaches the row's target),
 // then the best of the row's score above the bin (the gumbel pass's result)
 // and the exact scores of the collected bin elements >= tau.  A bin too
@@ -1775,14 +1793,19 @@ struct ToppFinishShared {
   };
 };
 
-__global__ void __launch_bounds__(kThreads) sample_topp_finish_kernel(SampleArgs a) {
+__global__ void __launch_bounds__(kThreads) sample_finish_kernel(SampleArgs a) {
   __shared__ ToppFinishShared sh;
   const int b = blockIdx.x;
+  const int state = a.row_state[b];
+  unsigned long long* rk = &a.row_key[(size_t)b * kRowPad8];
+  if (state == STATE_NEEDS_GUMBEL) {  // the gumbel pass left the row's best key
+    if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)load_row_best(rk));
+    return;
+  }
+  if (state != STATE_TOPP) return;
   const RowParams rp = row_params(a, b);
-  if (rp.mode != ROW_FILTER || rp.k != 0 || a.row_state[b] != STATE_TOPP) return;
   const int ib = a.row_ib[b];
   const uint32_t n = a.topp_n[b];
-  unsigned long long* rk = &a.row_key[(size_t)b * kRowPad8];
   const unsigned long long above = load_row_best(rk);
   const float s_cur = prune_level(above);
   const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
@@ -1834,7 +1857,7 @@ __global__ void __launch_bounds__(kThreads) sample_topp_finish_kernel(SampleArgs
 
 struct WsLayout {
   size_t lane_tops, topp_chunk_hist, topp_chunk_tb, row_ib, row_target, row_key, row_tau, row_state, chunk_max, cand_count, cand_count_a, cand_floor_a, cand_floor, cand, topp_cand, topp_n;
-  size_t list_n, list_gumbel, row_done, row_items, total;
+  size_t list_n, list_gumbel, total;
 };
 
 static WsLayout ws_layout(int B, int V) {
@@ -1859,8 +1882,6 @@ static WsLayout ws_layout(int B, int V) {
   w.topp_n = o;     o += align_up((size_t)B * 4, 256);
   w.list_n = o;     o += 256;
   w.list_gumbel = o; o += align_up((size_t)B * nc * 4, 256);
-  w.row_done = o;   o += (size_t)B * kRowPad * 4;
-  w.row_items = o;  o += (size_t)B * kRowPad * 4;
   w.total = o;
   return w;
 }
@@ -1898,8 +1919,6 @@ static SampleArgs make_args(const void* logits, int dtype, int batch, int vocab,
   a.topp_n = (uint32_t*)(ws + w.topp_n);
   a.list_n = (uint32_t*)(ws + w.list_n);
   a.list_gumbel = (uint32_t*)(ws + w.list_gumbel);
-  a.row_done = (uint32_t*)(ws + w.row_done);
-  a.row_items = (uint32_t*)(ws + w.row_items);
   return a;
 }
 
@@ -1938,7 +1957,6 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   a.noise = noise;
   a.out_ids = out_ids;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid_chunks(a.nchunks, batch);
   const size_t esz = dtype_size(dtype);
   const int vec = (int)(16 / esz);
   const bool vec_ok = (vocab % vec) == 0 && (row_stride % vec) == 0 && (((uintptr_t)logits) & 15) == 0;
@@ -1966,15 +1984,15 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
     NVJSEL_CHECK_LAUNCH("sample_onepass_finish_kernel");
     return NVJSEL_OK;
   }
-  NVJSEL_LAUNCH_CHUNK(sample_scan_kernel, grid_chunks);
+  NVJSEL_LAUNCH_CHUNK(sample_scan_kernel, dim3(a.nchunks, batch));
   hipLaunchKernelGGL(sample_select_kernel, dim3(batch), dim3(kThreads), 0, s, a);
   NVJSEL_CHECK_LAUNCH("sample_select_kernel");
-  const dim3 grid_items((unsigned)((long long)batch * a.nchunks * kGumbelSplit));
+  const long long max_items = (long long)batch * a.nchunks * kGumbelSplit;
+  const long long cap = (long long)kGumbelBlocksPerCu * device_cu_count();
+  const dim3 grid_items((unsigned)(max_items < cap ? max_items : cap));
   NVJSEL_LAUNCH_CHUNK(sample_gumbel_kernel, grid_items);
-  if (top_p) {
-    hipLaunchKernelGGL(sample_topp_finish_kernel, dim3(batch), dim3(kThreads), 0, s, a);
-    NVJSEL_CHECK_LAUNCH("sample_topp_finish_kernel");
-  }
+  hipLaunchKernelGGL(sample_finish_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+  NVJSEL_CHECK_LAUNCH("sample_finish_kernel");
 #undef NVJSEL_LAUNCH_CHUNK
   return NVJSEL_OK;
 }
@@ -2001,10 +2019,10 @@ extern "C" int nvjsel_topk(const void* logits, int dtype, int batch, int vocab, 
   SampleArgs a = make_args(logits, dtype, batch, vocab, row_stride, workspace);
   a.topk = k;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid_chunks(a.nchunks, batch);
   const size_t esz = dtype_size(dtype);
   const int vec = (int)(16 / esz);
   const bool vec_ok = (vocab % vec) == 0 && (row_stride % vec) == 0 && (((uintptr_t)logits) & 15) == 0;
+  const dim3 grid_chunks(a.nchunks, batch);
   if (dtype == NVJSEL_F32) {
     if (vec_ok) hipLaunchKernelGGL((sample_scan_kernel<DT_F32, 4>), grid_chunks, dim3(kThreads), 0, s, a);
     else hipLaunchKernelGGL((sample_scan_kernel<DT_F32, 1>), grid_chunks, dim3(kThreads), 0, s, a);
