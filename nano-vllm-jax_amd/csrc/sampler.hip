@@ -472,6 +472,94 @@ __device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v) {
   return v;
 }
 
+// The same Gumbel-max per wave, with no block barrier: the wave's elements
+// that can beat s_cur are packed densely into the wave's own LDS slice
+// (dx/di, 64 * EPT entries; only this wave reads it back), drawn fast four
+// chains at a time, and the few within the error margin of the wave's fast
+// maximum rescored exactly.  Returns the wave's exact best key (0: nothing
+// could beat s_cur), the same value in every lane.
+template <int EPT, int VEC>
+__device__ __forceinline__ unsigned long long wave_gumbel(const SampleArgs& a, int b, const TfKey& key,
+                                                          const float (&x)[EPT], int base, uint32_t act, float s_cur,
+                                                          float* dx, uint32_t* di) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j)
+    if (x[j] + NVJSEL_GUMBEL_MAX < s_cur) act &= ~(1u << j);  // cannot beat a score found; NaN stays
+  const uint32_t cnt = (uint32_t)__popc(act);
+  const uint32_t incl = wave_incl_sum(cnt);
+  const uint32_t n = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+  if (n == 0) return 0;
+  uint32_t pos = incl - cnt;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j)
+    if ((act >> j) & 1u) {
+      dx[pos] = x[j];
+      di[pos] = (uint32_t)elem_index<VEC>(base, j);
+      ++pos;
+    }
+  // the wave's own LDS writes before its reads (no other wave touches the slice)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+  // dense entry e = 256 g + 4 lane + j
+  constexpr int G = EPT / 4;
+  float st[EPT];
+  uint32_t tmax = 0;  // ord of the fast maximum
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int e0 = 256 * g + 4 * lane;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) st[4 * g + j] = -INFINITY;
+    if (256 * g < (int)n) {  // wave-uniform
+      uint32_t idx[4];
+      float xv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool in = e0 + j < (int)n;
+        idx[j] = in ? di[e0 + j] : 0u;
+        xv[j] = in ? dx[e0 + j] : -INFINITY;
+      }
+      float t[4];
+      if (a.noise) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t[j] = xv[j] + a.noise[(size_t)b * a.V + idx[j]];
+      } else {
+        uint32_t bits[4];
+        random_bits32_n<4>(key, idx, bits);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t[j] = xv[j] + gumbel_fast_from_bits(bits[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool in = e0 + j < (int)n;
+        const float v = (t[j] != t[j]) ? INFINITY : t[j];  // NaN only from a NaN logit
+        st[4 * g + j] = in ? v : -INFINITY;
+        const uint32_t o = in ? ord_f32(v) : 0u;
+        tmax = o > tmax ? o : tmax;
+      }
+    }
+  }
+  const float m = unord_f32(wave_max_u32(tmax));
+  // |fast - exact| <= 1.91e-6 on the draw (measured over all 2^23 draws),
+  // plus one ulp of the sum: the margin keeps ample room
+  const float margin = 1e-3f + fabsf(m) * 4.8e-7f;
+  if (m + margin < s_cur) return 0;  // nothing here can beat the score already reached
+  const float thr = m - margin;
+  unsigned long long best = 0;
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 256 * g + 4 * lane + j;
+      if (e < (int)n && st[4 * g + j] >= thr) {
+        const uint32_t i = di[e];
+        best = max_u64(best, argmax_key(dx[e] + exact_noise(a, b, key, (int)i), i));
+      }
+    }
+  return wave_max_u64(best);
+}
+
 // ------------------------------------------------------------------ top-k rows from candidates
 // A FILTER row with k <= 256: the row floor is the larger of the largest chunk
 // floor and the k-th largest lane maximum the scan published (four per wave);
@@ -1704,11 +1792,14 @@ __device__ __forceinline__ void gumbel_item(const SampleArgs& a, uint32_t item, 
         ++pos;
       }
   }
-  const unsigned long long best = block_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, act, s_cur, sh);
-  // The finish kernel turns the row's best into its id.  A block whose best
-  // does not exceed the value it read skips the max (the row's best only
-  // grows); each row's best sits on a cache line of its own.
-  if (threadIdx.x == 0 && best > seen) atomicMax(rk, best);
+  const int wave = threadIdx.x >> 6;
+  constexpr int WS = 64 * kGumbelEPT;  // each wave's slice of the dense lists
+  const unsigned long long best =
+      wave_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, act, s_cur, sh.dx + wave * WS, sh.di + wave * WS);
+  // The finish kernel turns the row's best into its id.  A wave whose best
+  // does not exceed the value its block read skips the max (the row's best
+  // only grows); each row's best sits on a cache line of its own.
+  if ((threadIdx.x & 63) == 0 && best > seen) atomicMax(rk, best);
 }
 
 // The queued item quarters, grid-stride: a grid of one round of resident
@@ -1729,23 +1820,25 @@ __global__ void __launch_bounds__(kThreads) sample_gumbel_kernel(SampleArgs a) {
 // so the scan / select / seed stages buy little.  One block per
 // (2048-element sub-chunk, row) scores its elements directly -- greedy rows
 // by argmax key of the raw logit, temperature rows by the block Gumbel-max
-// (fast draws, exact rescoring near the block maximum) -- and leaves one key
-// per block; a per-row kernel takes the maximum.
+// (fast draws, exact rescoring near the wave maximum) -- and leaves one key
+// per wave; a per-row kernel takes the maximum.
 template <int DT, int VEC>
 __global__ void __launch_bounds__(kThreads) sample_onepass_kernel(SampleArgs a) {
   __shared__ GumbelShared sh;
   const int b = blockIdx.y;
   const int base = blockIdx.x * (kThreads * kGumbelEPT);
+  const int wave = threadIdx.x >> 6;
   const RowParams rp = row_params(a, b);
   float x[kGumbelEPT];
   uint32_t valid;
   load_chunk_elems<DT, VEC, kGumbelEPT>(row_ptr(a, b), base, a.V, true, 1.0f, x, valid);
   unsigned long long best = 0;
+  // every wave settles its own 512 elements (no block barrier)
   if (rp.mode == ROW_GREEDY) {  // block-uniform
 #pragma unroll
     for (int j = 0; j < kGumbelEPT; ++j)
       if ((valid >> j) & 1u) best = max_u64(best, argmax_key(x[j], (uint32_t)elem_index<VEC>(base, j)));
-    best = block_max_u64(best, sh.red);
+    best = wave_max_u64(best);
   } else {
     // a NaN or +inf scaled logit scores NaN / +inf whatever its draw: the
     // first NaN, else the first +inf, is the row's argmax (jnp.argmax); their
@@ -1757,15 +1850,16 @@ __global__ void __launch_bounds__(kThreads) sample_onepass_kernel(SampleArgs a) 
       if (((valid >> j) & 1u) && (x[j] != x[j] || x[j] == INFINITY))
         nf = max_u64(nf, argmax_key(x[j], (uint32_t)elem_index<VEC>(base, j)));
     }
-    nf = block_max_u64(nf, sh.red);
+    nf = wave_max_u64(nf);
     if (nf) {
       best = nf;
     } else {
       const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
-      best = block_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, valid, -INFINITY, sh);
+      constexpr int WS = 64 * kGumbelEPT;
+      best = wave_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, valid, -INFINITY, sh.dx + wave * WS, sh.di + wave * WS);
     }
   }
-  if (threadIdx.x == 0) a.cand[(size_t)b * gridDim.x + blockIdx.x] = best;
+  if ((threadIdx.x & 63) == 0) a.cand[((size_t)b * gridDim.x + blockIdx.x) * (kThreads / 64) + wave] = best;
 }
 
 __global__ void __launch_bounds__(64) sample_onepass_finish_kernel(SampleArgs a, int nsub) {
@@ -1980,7 +2074,7 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   const int nsub = (vocab + kThreads * kGumbelEPT - 1) / (kThreads * kGumbelEPT);
   if (!top_k && !top_p && (long long)batch * nsub <= 8LL * device_cu_count()) {
     NVJSEL_LAUNCH_CHUNK(sample_onepass_kernel, dim3(nsub, batch));
-    hipLaunchKernelGGL(sample_onepass_finish_kernel, dim3(batch), dim3(64), 0, s, a, nsub);
+    hipLaunchKernelGGL(sample_onepass_finish_kernel, dim3(batch), dim3(64), 0, s, a, nsub * (kThreads / 64));
     NVJSEL_CHECK_LAUNCH("sample_onepass_finish_kernel");
     return NVJSEL_OK;
   }
