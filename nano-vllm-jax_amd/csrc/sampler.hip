@@ -57,8 +57,14 @@ static constexpr int kRowPad8 = 32;  // uint64 words
 enum { STATE_DONE = 1, STATE_HEAVY = 2, STATE_NEEDS_GUMBEL = 3, STATE_TOPP = 4 };
 
 static constexpr int kThreads = 256;
-static constexpr int kEPT = 32;                    // elements per thread in chunk kernels
-static constexpr int kChunk = kThreads * kEPT;     // 8192 elements per block
+// Elements per thread in the scan: 64 for 16-bit logits read as 16-byte
+// vectors, else 32 -- 32 KB per block either way (measured: 16-bit chunks of
+// 16384 elements beat 8192; f32 chunks of 16384 lose).  chunk = 256 * EPT.
+template <int DT, int VEC>
+struct ChunkShape {
+  static constexpr int EPT = (DT != 0 && VEC == 8) ? 64 : 32;
+};
+static constexpr int kChunkMin = 256 * 32;  // the smallest chunk (workspace sizing)
 static constexpr int kFastK = 256;                 // top-k resolved from candidates
 static constexpr int kCandCap = 512;               // candidates kept per chunk
 static constexpr int kSelCap = 8192;               // candidates per row held in LDS
@@ -72,6 +78,7 @@ struct SampleArgs {
   int B;
   int V;
   int nchunks;
+  int chunk;  // elements per scan chunk (256 * EPT)
   long long stride;  // elements between rows
   const float* temperature;
   const int32_t* top_k;
@@ -780,7 +787,7 @@ typedef unsigned short nvjsel_u16x2 __attribute__((ext_vector_type(2)));
 // for f32) instead of decoding every element.
 template <int DT, int VEC>
 struct ChunkRegs {
-  static constexpr int Q = kEPT / VEC;
+  static constexpr int Q = ChunkShape<DT, VEC>::EPT / VEC;
   static constexpr int W = VEC == 1 ? 1 : 4;  // dwords per vector
   uint32_t w[Q][W];
   float vmax[Q];  // max of each vector (NaN ignored)
@@ -930,9 +937,9 @@ __device__ __forceinline__ uint32_t wave_kth_prefix(float v, bool ok, uint32_t k
 template <int DT, int VEC>
 __device__ __forceinline__ void scan_item(const SampleArgs& a, int b, int c, ChunkRegs<DT, VEC>& r,
                                           ScanShared& sh) {
-  constexpr int Q = kEPT / VEC;
+  constexpr int Q = ChunkShape<DT, VEC>::EPT / VEC;
   const RowParams rp = row_params(a, b);
-  const int base = c * kChunk;
+  const int base = c * a.chunk;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // Raw logits: x = l / T' is monotone in l, so maxima and the candidate test
   // run on l and only candidates pay for the division.
@@ -956,7 +963,7 @@ __device__ __forceinline__ void scan_item(const SampleArgs& a, int b, int c, Chu
   uint32_t wfloor = 0xFFFFFFFFu;
   if (topk && !wnan) {
     // lane t holds an element iff its first vector (index t) lies in the row
-    const int nv = (min(a.V - base, kChunk) + VEC - 1) / VEC;
+    const int nv = (min(a.V - base, a.chunk) + VEC - 1) / VEC;
     const int Lw = max(0, min(64, nv - 64 * wave)), L = min(nv, kThreads);
     const uint32_t kk = (uint32_t)(((long long)rp.k * Lw + L - 1) / L);
     float tv = r.vmax[0];  // the lane's maximum over its vectors inside the row
@@ -1108,7 +1115,7 @@ __global__ void __launch_bounds__(kThreads) sample_scan_kernel(SampleArgs a) {
   __shared__ ScanShared sh;
   const int b = blockIdx.y, c = blockIdx.x;
   ChunkRegs<DT, VEC> r;
-  scan_issue<DT, VEC>(row_ptr(a, b), c * kChunk, a.V, r.w);
+  scan_issue<DT, VEC>(row_ptr(a, b), c * a.chunk, a.V, r.w);
   scan_item<DT, VEC>(a, b, c, r, sh);
 }
 
@@ -1420,7 +1427,7 @@ __global__ void __launch_bounds__(kThreads) topk_select_kernel(SampleArgs a, flo
 // A gumbel block covers a quarter chunk (2048 elements): four times the blocks
 // of the scan, for the VALU-heavy noise.
 static constexpr int kGumbelEPT = 8;
-static constexpr int kGumbelSplit = kEPT / kGumbelEPT;
+static constexpr int kGumbelSub = kThreads * kGumbelEPT;  // elements per gumbel item
 static constexpr int kGumbelBlocksPerCu = 16;  // gumbel-pass grid: blocks per CU (measured: 16 > 8, uncapped)
 
 // Scratch of queue_chunks.
@@ -1756,7 +1763,7 @@ __device__ __forceinline__ void gumbel_item(const SampleArgs& a, uint32_t item, 
   const int b = (int)(item >> 16), c = (int)(item & 0xFFFFu);
   const RowParams rp = row_params(a, b);
   const char* row = row_ptr(a, b);
-  const int base = (c * kGumbelSplit + sub) * (kThreads * kGumbelEPT);
+  const int base = c * a.chunk + sub * kGumbelSub;
   float x[kGumbelEPT];
   uint32_t valid;
   load_chunk_elems<DT, VEC, kGumbelEPT>(row, base, a.V, true, 1.0f, x, valid);
@@ -1807,9 +1814,10 @@ __device__ __forceinline__ void gumbel_item(const SampleArgs& a, uint32_t item, 
 template <int DT, int VEC>
 __global__ void __launch_bounds__(kThreads) sample_gumbel_kernel(SampleArgs a) {
   __shared__ GumbelShared sh;
-  const uint32_t n = a.list_n[0] * (uint32_t)kGumbelSplit;
+  const uint32_t split = (uint32_t)(a.chunk / kGumbelSub);
+  const uint32_t n = a.list_n[0] * split;
   for (uint32_t q = blockIdx.x; q < n; q += gridDim.x) {
-    gumbel_item<DT, VEC>(a, a.list_gumbel[q / kGumbelSplit], (int)(q % kGumbelSplit), sh);
+    gumbel_item<DT, VEC>(a, a.list_gumbel[q / split], (int)(q % split), sh);
     __syncthreads();  // the next item reuses the LDS
   }
 }
@@ -1955,7 +1963,7 @@ struct WsLayout {
 };
 
 static WsLayout ws_layout(int B, int V) {
-  const size_t nc = (size_t)((V + kChunk - 1) / kChunk);
+  const size_t nc = (size_t)((V + kChunkMin - 1) / kChunkMin);
   WsLayout w;
   size_t o = 0;
   w.lane_tops = o;  o += align_up((size_t)B * nc * (kThreads / 64) * kTopsPub * 4, 256);
@@ -1993,7 +2001,12 @@ static SampleArgs make_args(const void* logits, int dtype, int batch, int vocab,
   a.dtype = dtype;
   a.B = batch;
   a.V = vocab;
-  a.nchunks = (vocab + kChunk - 1) / kChunk;
+  // the chunk of the scan instance that will run (ChunkShape)
+  const int vec = (int)(16 / dtype_size(dtype));
+  const bool vec_ok = (vocab % vec) == 0 && (row_stride % vec) == 0 && (((uintptr_t)logits) & 15) == 0;
+  a.chunk = kThreads * ((dtype != NVJSEL_F32 && vec_ok) ? 64 : 32);
+  a.nchunks = (vocab + a.chunk - 1) / a.chunk;
+
   a.stride = row_stride;
   a.lane_tops = (float*)(ws + w.lane_tops);
   a.topp_chunk_hist = (unsigned long long*)(ws + w.topp_chunk_hist);
@@ -2042,7 +2055,7 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   }
   if (batch > 65535) return fail(NVJSEL_EUNSUPPORTED, "sample: batch > 65535");
   // the select kernel reads up to 1024 chunk counts per row
-  if ((vocab + kChunk - 1) / kChunk > 1024) return fail(NVJSEL_EUNSUPPORTED, "sample: vocab > 2^23");
+  if ((vocab + kChunkMin - 1) / kChunkMin > 1024) return fail(NVJSEL_EUNSUPPORTED, "sample: vocab > 2^23");
   SampleArgs a = make_args(logits, dtype, batch, vocab, row_stride, workspace);
   a.temperature = temperature;
   a.top_k = top_k;
@@ -2081,7 +2094,7 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   NVJSEL_LAUNCH_CHUNK(sample_scan_kernel, dim3(a.nchunks, batch));
   hipLaunchKernelGGL(sample_select_kernel, dim3(batch), dim3(kThreads), 0, s, a);
   NVJSEL_CHECK_LAUNCH("sample_select_kernel");
-  const long long max_items = (long long)batch * a.nchunks * kGumbelSplit;
+  const long long max_items = (long long)batch * a.nchunks * (a.chunk / kGumbelSub);
   const long long cap = (long long)kGumbelBlocksPerCu * device_cu_count();
   const dim3 grid_items((unsigned)(max_items < cap ? max_items : cap));
   NVJSEL_LAUNCH_CHUNK(sample_gumbel_kernel, grid_items);
@@ -2109,7 +2122,7 @@ extern "C" int nvjsel_topk(const void* logits, int dtype, int batch, int vocab, 
   if (!workspace || workspace_bytes < nvjsel_topk_workspace_size(batch, vocab))
     return fail(NVJSEL_EWORKSPACE, "topk: workspace smaller than nvjsel_topk_workspace_size");
   if (batch > 65535) return fail(NVJSEL_EUNSUPPORTED, "topk: batch > 65535");
-  if ((vocab + kChunk - 1) / kChunk > 1024) return fail(NVJSEL_EUNSUPPORTED, "topk: vocab > 2^23");
+  if ((vocab + kChunkMin - 1) / kChunkMin > 1024) return fail(NVJSEL_EUNSUPPORTED, "topk: vocab > 2^23");
   SampleArgs a = make_args(logits, dtype, batch, vocab, row_stride, workspace);
   a.topk = k;
   hipStream_t s = (hipStream_t)stream;
