@@ -22,16 +22,26 @@ class KernelBackendUnavailable(RuntimeError):
 class KernelBackendSpec:
     name: str
     aliases: tuple[str, ...]
+    required_modules: tuple[str, ...]
     provided_kernels: tuple[str, ...]
+    implemented: bool
     description: str
 
 
 @dataclass(frozen=True)
 class KernelBackendStatus:
+    """The reference's status record (kernels/registry.py:30-52), field for
+    field.  ``missing_modules`` names the native library when it cannot load;
+    ``fallback`` is always None: this backend never falls back."""
+
     requested: str
     selected: str
     available: bool
+    implemented: bool
+    external_kernels_enabled: bool
+    missing_modules: tuple[str, ...] = ()
     provided_kernels: tuple[str, ...] = ()
+    fallback: str | None = None
     reason: str = ""
 
     def as_dict(self) -> dict[str, object]:
@@ -39,7 +49,11 @@ class KernelBackendStatus:
             "requested": self.requested,
             "selected": self.selected,
             "available": self.available,
+            "implemented": self.implemented,
+            "external_kernels_enabled": self.external_kernels_enabled,
+            "missing_modules": list(self.missing_modules),
             "provided_kernels": list(self.provided_kernels),
+            "fallback": self.fallback,
             "reason": self.reason,
         }
 
@@ -48,6 +62,7 @@ _SPECS = {
     "hip": KernelBackendSpec(
         name="hip",
         aliases=("hip", "rocm", "nvjsel", "mi355x", "gfx950", "auto"),
+        required_modules=(),
         provided_kernels=(
             "lm_head_greedy_top1",
             "lm_head_greedy_top1_prenorm",
@@ -56,7 +71,9 @@ _SPECS = {
             "mtp_greedy_top1",
             "sample_topk_topp",
             "derive_rng_keys",
+            "lm_head_logits",
         ),
+        implemented=True,
         description="Hand-written HIP kernels for gfx950 behind the libnvjsel C ABI.",
     ),
 }
@@ -107,11 +124,12 @@ def backend_status(name: str | None = None) -> KernelBackendStatus:
     spec = _SPECS[n]
     try:
         _lib.load()
-        return KernelBackendStatus(requested=name or n, selected=n, available=True,
-                                   provided_kernels=spec.provided_kernels,
+        return KernelBackendStatus(requested=name or n, selected=n, available=True, implemented=spec.implemented,
+                                   external_kernels_enabled=True, provided_kernels=spec.provided_kernels,
                                    reason=f"{n} backend selected")
     except Exception as exc:  # library missing or ABI mismatch
-        return KernelBackendStatus(requested=name or n, selected=n, available=False,
+        return KernelBackendStatus(requested=name or n, selected=n, available=False, implemented=spec.implemented,
+                                   external_kernels_enabled=False, missing_modules=(_lib.LIB_PATH.name,),
                                    provided_kernels=spec.provided_kernels, reason=str(exc))
 
 

@@ -85,6 +85,10 @@ def test_registry_semantics():
         registry.lm_head_greedy_top1_impl("bogus")
     st = registry.select_token_selection_backend("auto")
     assert st.selected == "hip" and st.available
+    # the reference's status record, field for field (kernels/registry.py:30-52)
+    assert list(st.as_dict()) == ["requested", "selected", "available", "implemented", "external_kernels_enabled",
+                                  "missing_modules", "provided_kernels", "fallback", "reason"]
+    assert st.implemented and st.external_kernels_enabled and st.fallback is None and st.missing_modules == ()
     with pytest.raises(ValueError):
         registry.select_token_selection_backend("nope")
 
@@ -94,7 +98,9 @@ def test_registry_strict_raises_when_library_missing(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "missing.so")
     with pytest.raises(registry.KernelBackendUnavailable):
         registry.select_token_selection_backend("hip")
-    assert not registry.select_token_selection_backend("hip", strict=False).available
+    st = registry.select_token_selection_backend("hip", strict=False)
+    assert not st.available and not st.external_kernels_enabled and st.missing_modules == ("missing.so",)
+    assert st.fallback is None  # never a silent fallback
 
 
 def test_host_api_rejects_bad_shapes_before_launch():
