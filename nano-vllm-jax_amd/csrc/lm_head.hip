@@ -1279,7 +1279,7 @@ static size_t lm_prenorm_bytes(int batch, int H) { return align_up((size_t)batch
 // the partial sums [WAVES][NB][512] f32 (the same bytes, reused).
 static size_t hv_lds_bytes(int nb, int H) {
   const int p2 = nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 4 ? 4 : 8;
-  const size_t waves = p2 >= 8 ? 4 : 8;
+  const size_t waves = 4;
   const size_t a = (size_t)H * p2, b = waves * p2 * 512;
   return (a > b ? a : b) * 4;
 }
@@ -1293,7 +1293,7 @@ struct LogitsOut {
 
 template <int NB, int MODE>
 static int launch_hv(const LmArgs& a, hipStream_t stream) {
-  constexpr int WAVES = NB >= 8 ? 4 : 8;
+  constexpr int WAVES = 4;  // measured: 4 waves per block beat 8 and 16 at B = 1 and 8
   auto kern = lm_head_hv_kernel<NB, WAVES, MODE>;
   const size_t lds = hv_lds_bytes(NB, a.H);
   if (lds > 48 * 1024)
