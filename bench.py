@@ -36,10 +36,10 @@ for _p in (ROOT, os.path.join(ROOT, "nano-vllm-jax_amd")):
 HBM_PEAK = 8.0e12  # bytes/s, MI355X
 MALL_BYTES = 256 * 1024 * 1024
 V_FULL, H_FULL = 248320, 1024
-ALL_CONFIGS = "c1,c2,c3,c4,c5,x1,x2,x3,x4,x5"
+ALL_CONFIGS = "c1,c2,c3,c4,c5,x1,x2,x3,x4,x5,x6"
 # per-config generator seeds: each config's inputs depend only on its own seed
 SEEDS = {"c1": 101, "c2": 102, "c3": 103, "c4": 104, "c5": 105, "x1": 201, "x2": 202, "x3": 203, "x4": 204,
-         "x5": 205}
+         "x5": 205, "x6": 206}
 
 
 def _parse():
@@ -172,8 +172,8 @@ def make_inputs(torch, name, dev):
         return {"batch": B, "logits": l, "temperature": choice([0.0, 0.6, 1.0], torch.float32),
                 "top_k": choice([0, 20, 100], torch.int32), "top_p": choice([1.0, 0.95, 0.8], torch.float32),
                 "keys": _engine_keys(torch, B, dev)}
-    if name in ("x3", "x4", "x5"):
-        B = 1 if name == "x3" else 8
+    if name in ("x3", "x4", "x5", "x6"):
+        B = {"x3": 1, "x4": 8, "x5": 8, "x6": 256}[name]
         h = torch.randn(B, H_FULL, device=dev, generator=gen)
         return {"batch": B, "hidden": h if name == "x5" else h.to(torch.bfloat16)}
     raise KeyError(name)
@@ -311,12 +311,12 @@ def build_configs(torch, which, with_cpu):
                         "top-k values+indices k=50, f32 logits [64,248320] Zipf(1.1)"))
     # the reference's other operating points: the materialised [H, V] lm_head
     # (B = 1 and 8) and fp32 activations at B = 8 on the [V, H] table
-    for name in ("x3", "x4", "x5"):
+    for name in ("x3", "x4", "x5", "x6"):
         if name not in which:
             continue
         d = make_inputs(torch, name, dev)
         B, h = d["batch"], d["hidden"]
-        if name == "x5":
+        if name in ("x5", "x6"):
             Ws, layout = weights(), 0
         else:
             if not Whv:
@@ -333,9 +333,11 @@ def build_configs(torch, which, with_cpu):
 
         desc = {"x3": "greedy LM-head top-1, B=1, W [1024,248320] bf16 ([H,V], the materialised lm_head)",
                 "x4": "greedy LM-head top-1, B=8, W [1024,248320] bf16 ([H,V])",
-                "x5": "greedy LM-head top-1, B=8, fp32 activations x W [248320,1024] bf16 (one W pass)"}[name]
-        kern = "lm_head_tile_kernel" if name == "x5" else "lm_head_hv_kernel"
-        cfgs.append(Cfg(f"{name}_{'hv' if layout else 'f32act'}_greedy_b{B}", B,
+                "x5": "greedy LM-head top-1, B=8, fp32 activations x W [248320,1024] bf16 (one W pass)",
+                "x6": "greedy LM-head top-1, B=256, bf16 x W [248320,1024] bf16 (one W pass, blocked GEMM)"}[name]
+        kern = {"x5": "lm_head_tile_kernel", "x6": "lm_head_gemm_kernel"}.get(name, "lm_head_hv_kernel")
+        tag = "hv" if layout else {"x5": "f32act", "x6": "gemm"}[name]
+        cfgs.append(Cfg(f"{name}_{tag}_greedy_b{B}", B,
                         V_FULL * H_FULL * 2 + B * H_FULL * h.element_size(), launch, 2, kern, desc))
     torch.cuda.synchronize()
     del np

@@ -1103,6 +1103,166 @@ static int dispatch_tile(const LmArgs& a, hipStream_t s) {
   return launch_tile<4, kTileW4, MODE, 1>(a, s);
 }
 
+// ------------------------------------------------------------------ blocked GEMM, 64 < B <= 256
+// bf16 hidden x bf16 W [V, H], H % 64 == 0, up to 256 rows in ONE pass over
+// W.  The hidden of 256 rows (512 KB at H = 1024) is a CU's whole register
+// file, so unlike the tile kernel nothing is held for the whole call: a block
+// tile is 128 vocabulary rows x all 256 batch rows, and K is streamed in
+// chunks of 64 -- the W chunk (128 x 64, 16 KB, from HBM) and the hidden
+// chunk (256 x 64, 32 KB, L2-resident) both staged in LDS, the next chunk
+// prefetched into registers while the current one is multiplied.  Wave w of
+// 8 computes the 64 x 64 sub-tile (vocab half w & 1, batch quarter w >> 1) as
+// 4 x 4 v_mfma_f32_16x16x32_bf16 tiles (64 accumulators per lane), reading
+// 4 A and 4 B fragments per 32-wide k-step: every W and hidden element is
+// read from LDS by 4 and 2 waves.  LDS rows are XOR-swizzled by the 16-byte
+// column (q) index: conflict-free fragment reads and stores.
+// Blocks are persistent over the vocabulary tiles (round robin) and keep, per
+// batch row, a running best key; each block finally stores its 256 keys and
+// gemm_reduce_kernel takes the per-row maximum (no same-address atomics).
+// MODE_LOGITS stores the rounded logits instead.
+static constexpr int kGemmBV = 128, kGemmBB = 256, kGemmKC = 64;
+
+template <int MODE>
+__global__ void __launch_bounds__(512) lm_head_gemm_kernel(LmArgs a, unsigned long long* blk_keys) {
+  constexpr int QC = kGemmKC / 8;  // 16-byte columns per chunk row
+  __shared__ u32x4_t As[QC * kGemmBV];
+  __shared__ u32x4_t Bs[QC * kGemmBB];
+  __shared__ unsigned long long kred[2][kGemmBB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int vi = wave & 1, bj = wave >> 1;
+  const int B = a.B, V = a.V, H = a.H;
+  const uint16_t* W = (const uint16_t*)a.W;
+  const uint16_t* X = (const uint16_t*)a.hidden;
+  const int ntiles = (V + kGemmBV - 1) / kGemmBV;
+  const int nchunks = H / kGemmKC;
+  // the thread's load pieces: W 2 x 16 B (rows p >> 3, column p & 7), hidden 4 x 16 B
+  auto wpiece = [&](int i) { return tid + 512 * i; };
+  unsigned long long best[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) best[t] = 0;
+
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int v0 = tile * kGemmBV;
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    u32x4_t pw[2], ph[4];
+    auto load_chunk = [&](int c) NVJSEL_INLINE {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int p = wpiece(i), row = p >> 3, q = p & 7;
+        const int v = min(v0 + row, V - 1);
+        pw[i] = stream_load((const u32x4_t*)(W + (size_t)v * H + c * kGemmKC) + q);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = wpiece(i), row = p >> 3, q = p & 7;
+        ph[i] = row < B ? *((const u32x4_t*)(X + (size_t)row * H + c * kGemmKC) + q) : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    };
+    load_chunk(0);
+    for (int c = 0; c < nchunks; ++c) {
+      __syncthreads();  // every fragment read of the previous chunk is done
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int p = wpiece(i), row = p >> 3, q = p & 7;
+        As[q * kGemmBV + (row ^ q)] = pw[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = wpiece(i), row = p >> 3, q = p & 7;
+        Bs[q * kGemmBB + (row ^ q)] = ph[i];
+      }
+      __syncthreads();
+      if (c + 1 < nchunks) load_chunk(c + 1);  // in flight during the MFMAs
+#pragma unroll
+      for (int ks = 0; ks < kGemmKC / 32; ++ks) {
+        const int q = ks * 4 + g;
+        u32x4_t bf[4];
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) bf[tb] = Bs[q * kGemmBB + ((bj * 64 + tb * 16 + r) ^ q)];
+#pragma unroll
+        for (int tv = 0; tv < 4; ++tv) {
+          const u32x4_t af = As[q * kGemmBV + ((vi * 64 + tv * 16 + r) ^ q)];
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) acc[tv][tb] = mfma16x16x32<DT_BF16>(af, bf[tb], acc[tv][tb]);
+        }
+      }
+    }
+    // epilogue: D[vocab 4 g + i][batch r] of tile (tv, tb)
+#pragma unroll
+    for (int tv = 0; tv < 4; ++tv)
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const int b = bj * 64 + tb * 16 + r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int v = v0 + vi * 64 + tv * 16 + 4 * g + i;
+          if (v >= V || b >= B) continue;
+          const float val = apply_cast(acc[tv][tb][i], a.reduce_cast);
+          if constexpr (MODE == MODE_LOGITS) store_logit(a, b, v, val);
+          else best[tb] = max_u64(best[tb], argmax_key(val, (uint32_t)v));
+        }
+      }
+  }
+  if constexpr (MODE == MODE_LOGITS) return;
+  // the four lane groups (vocab rows 4 g ..) of a column, then the two vocab halves
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    best[tb] = max_u64(best[tb], shfl_xor_u64(best[tb], 16));
+    best[tb] = max_u64(best[tb], shfl_xor_u64(best[tb], 32));
+    if (g == 0) kred[vi][bj * 64 + tb * 16 + r] = best[tb];
+  }
+  __syncthreads();
+  for (int b = tid; b < kGemmBB; b += 512)
+    blk_keys[(size_t)blockIdx.x * kGemmBB + b] = max_u64(kred[0][b], kred[1][b]);
+}
+
+// Per row: the maximum of the blocks' keys -> id (and the winning logit);
+// the keys read are cleared.
+__global__ void __launch_bounds__(256) gemm_reduce_kernel(unsigned long long* __restrict__ blk_keys, int nblk,
+                                                          int B, int32_t* out_ids, float* out_best) {
+  __shared__ unsigned long long red[4];
+  const int b = blockIdx.x;
+  unsigned long long m = 0;
+  for (int i = threadIdx.x; i < nblk; i += 256) {
+    unsigned long long* p = blk_keys + (size_t)i * kGemmBB + b;
+    m = max_u64(m, *p);
+    *p = 0;  // the workspace is zero at rest (the GEMM writes zero keys for rows >= B)
+  }
+  m = wave_max_u64(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    m = max_u64(max_u64(red[0], red[1]), max_u64(red[2], red[3]));
+    out_ids[b] = (int32_t)(~(uint32_t)m);
+    if (out_best) out_best[b] = unord_f32((uint32_t)(m >> 32));
+  }
+}
+
+static constexpr int kGemmBpc = 1;  // blocks per CU of the blocked GEMM
+static constexpr int kGemmMaxBlocks = 1024;  // bounds the per-block key array
+static size_t gemm_keys_bytes() { return (size_t)kGemmMaxBlocks * kGemmBB * 8; }
+
+template <int MODE>
+static int launch_gemm(const LmArgs& a, unsigned long long* blk_keys, hipStream_t stream) {
+  const int ntiles = (a.V + kGemmBV - 1) / kGemmBV;
+  int grid = kGemmBpc * device_cu_count();
+  if (grid > kGemmMaxBlocks) grid = kGemmMaxBlocks;
+  if (grid > ntiles) grid = ntiles;
+  hipLaunchKernelGGL(lm_head_gemm_kernel<MODE>, dim3(grid), dim3(512), 0, stream, a, blk_keys);
+  NVJSEL_CHECK_LAUNCH("lm_head_gemm_kernel");
+  if constexpr (MODE == MODE_GREEDY) {
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3(a.B), dim3(256), 0, stream, blk_keys, grid, a.B, a.out_ids,
+                       a.out_best);
+    NVJSEL_CHECK_LAUNCH("gemm_reduce_kernel");
+  }
+  return NVJSEL_OK;
+}
+
 // ------------------------------------------------------------------ generic kernel
 // One vocabulary entry per thread, every batch row, any dtype/layout.
 template <int MODE>
@@ -1264,6 +1424,13 @@ static int dispatch_nb(const LmArgs& a, hipStream_t s) {
 
 static size_t lm_ws_keys_bytes(int batch) { return align_up((size_t)batch * 8, 256); }
 
+// The workspace every greedy/sample path needs: per-row keys and the ticket
+// line.  Batches past kGemmMinBatch add the blocked GEMM's per-block keys.
+static size_t lm_ws_small_bytes(int batch) {
+  return batch <= 0 ? 0 : lm_ws_keys_bytes(batch) + 256;
+}
+static constexpr int kGemmMinBatch = 64;
+
 
 // Final-RMSNorm prologue request (norm_w == nullptr: hidden is already normed).
 struct Prenorm {
@@ -1348,7 +1515,8 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     }
     if (!(pn.eps >= 0.0f)) { set_error("%s: eps must be >= 0", who); return NVJSEL_EINVAL; }
   }
-  const size_t need = mode == MODE_LOGITS ? 0 : nvjsel_lm_head_workspace_size(batch) + (prenorm ? lm_prenorm_bytes(batch, H) : 0);
+  // the blocked GEMM's key array is optional: without it the tile path runs
+  const size_t need = mode == MODE_LOGITS ? 0 : lm_ws_small_bytes(batch) + (prenorm ? lm_prenorm_bytes(batch, H) : 0);
   if (need && (!workspace || ws_bytes < need)) {
     set_error("%s: workspace %zu bytes < required %zu", who, ws_bytes, need);
     return NVJSEL_EWORKSPACE;
@@ -1384,7 +1552,13 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     chunk = tiles * 16;
   }
   const bool tile = !gemv && bf16_mfma && H == 1024 && (prenorm || (((uintptr_t)hidden) & 15) == 0);
-  const bool fused_prenorm = prenorm && (gemv || tile);
+  // blocked GEMM: 64 < B, bf16 activations, one pass over W per 256 rows (greedy/logits)
+  const size_t gemm_off = lm_ws_small_bytes(batch) + (prenorm ? lm_prenorm_bytes(batch, H) : 0);
+  const bool gemm = mode != MODE_SAMPLE && batch > kGemmMinBatch && bf16_mfma && (H % kGemmKC) == 0 &&
+                    eff_dtype == NVJSEL_BF16 && (prenorm || (((uintptr_t)hidden) & 15) == 0) &&
+                    (mode == MODE_LOGITS || (workspace && ws_bytes >= gemm_off + gemm_keys_bytes()));
+  unsigned long long* gemm_keys = gemm && mode != MODE_LOGITS ? (unsigned long long*)((char*)workspace + gemm_off) : nullptr;
+  const bool fused_prenorm = prenorm && !gemm && (gemv || tile);
   if (prenorm && !fused_prenorm) {
     LmArgs p{};
     p.hidden = hidden;
@@ -1394,7 +1568,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     p.norm_dtype = pn.norm_dtype;
     p.eps = pn.eps;
     p.act_dtype = pn.act_dtype;
-    void* normed = (char*)workspace + nvjsel_lm_head_workspace_size(batch);
+    void* normed = (char*)workspace + lm_ws_small_bytes(batch);
     hipLaunchKernelGGL(lm_prenorm_kernel, dim3(batch), dim3(256), 0, s, p, normed);
     NVJSEL_CHECK_LAUNCH("lm_prenorm_kernel");
     hidden = normed;
@@ -1403,6 +1577,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   if (tile) chunk = eff_dtype == NVJSEL_BF16 ? 64 : 16;
   if (gemv) chunk = 0;
   if (hv) chunk = 8;
+  if (gemm) chunk = kGemmBB;
   auto by_mode = [&](auto fn) -> int {
     if (mode == MODE_GREEDY) return fn(std::integral_constant<int, MODE_GREEDY>{});
     if (mode == MODE_SAMPLE) return fn(std::integral_constant<int, MODE_SAMPLE>{});
@@ -1435,7 +1610,9 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     a.out_dtype = lo.dtype;
     a.out_stride = lo.stride;
     int rc;
-    if (gemv) {
+    if (gemm) {
+      rc = mode == MODE_GREEDY ? launch_gemm<MODE_GREEDY>(a, gemm_keys, s) : launch_gemm<MODE_LOGITS>(a, nullptr, s);
+    } else if (gemv) {
       rc = by_mode([&](auto M) { return dispatch_gemv<decltype(M)::value>(a, s); });
     } else if (hv) {
       rc = by_mode([&](auto M) { return dispatch_hv<decltype(M)::value>(a, s); });
@@ -1462,7 +1639,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     const size_t words = lm_prenorm_bytes(batch, H) / 4;
     const unsigned grid = (unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024);
     hipLaunchKernelGGL(lm_zero_kernel, dim3(grid), dim3(256), 0, s,
-                       (uint32_t*)((char*)workspace + nvjsel_lm_head_workspace_size(batch)), words);
+                       (uint32_t*)((char*)workspace + lm_ws_small_bytes(batch)), words);
     NVJSEL_CHECK_LAUNCH("lm_zero_kernel");
   }
   return NVJSEL_OK;
@@ -1531,7 +1708,7 @@ extern "C" int nvjsel_lm_head_top1_noalloc(const void* hidden, int hidden_dtype,
 
 extern "C" size_t nvjsel_lm_head_workspace_size(int batch) {
   if (batch <= 0) return 0;
-  return lm_ws_keys_bytes(batch) + 256;
+  return lm_ws_small_bytes(batch) + (batch > kGemmMinBatch ? gemm_keys_bytes() : 0);
 }
 
 extern "C" int nvjsel_lm_head_top1(const void* hidden, int hidden_dtype, const void* weight,

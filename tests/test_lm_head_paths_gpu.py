@@ -220,3 +220,41 @@ def test_hidden_to_filtered_sampling_native():
     torch.cuda.synchronize()
     _check_logits(logits, as_f32(h), as_f32(W), 1, "filtered sampling logits")
     check_sampled(ids.cpu().numpy(), logits.float().cpu().numpy(), T, K, P, keys, ctx="hidden->filtered")
+
+
+# Blocked GEMM (64 < B, bf16 activations, [V, H] bf16): one pass over W per
+# 256 rows, greedy and logits; B = 300 takes a 256-row and a 44-row launch.
+@pytest.mark.parametrize("B,H", [(65, 1024), (128, 1024), (256, 1024), (300, 512), (100, 2048), (77, 64)])
+def test_gemm_greedy_and_logits(B, H):
+    rng = np.random.default_rng(7000 + B + H)
+    V = 10000 + (B % 7)  # not a multiple of the 128-row tile
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    h = _hidden(rng, B, H, torch.bfloat16)
+    ids = nvjsel.lm_head_greedy_top1_hip(h, W.T)
+    logits = nvjsel.lm_head_logits_hip(h, W.T)
+    torch.cuda.synchronize()
+    hf, wf = h.float().cpu().numpy(), W.float().cpu().numpy()
+    z = sel.lm_head_logits(hf, wf)
+    check_greedy(ids.cpu().numpy().reshape(-1), z, 1, f"gemm B={B} H={H}")
+    _check_logits(logits, hf, wf, 1, f"gemm logits B={B} H={H}")
+    # a second call on the same workspace (its keys are cleared at rest)
+    ids2 = nvjsel.lm_head_greedy_top1_hip(h, W.T)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ids2)
+
+
+def test_gemm_full_vocab_b256_with_prenorm():
+    """The bench shape (B = 256, V = 151936, H = 1024) through the final-norm
+    entry (prologue kernel into the workspace, then the GEMM), against the
+    oracle's norm + float64 LM head."""
+    rng = np.random.default_rng(4242)
+    B, H, V = 256, 1024, 151936
+    x = sel.round_bf16(rng.normal(0.0, 3.0, (B, H)).astype(np.float32))
+    nw = rng.normal(0.0, 0.2, H).astype(np.float32)
+    W = sel.round_bf16(rng.normal(0.0, 0.02, (V, H)).astype(np.float32))
+    ids = nvjsel.lm_head_greedy_top1_hip(
+        torch.from_numpy(x).to(torch.bfloat16).cuda(), torch.from_numpy(W).to(torch.bfloat16).cuda(),
+        weight_layout="vh", norm_weight=torch.from_numpy(nw).cuda(), rms_norm_eps=1e-6, act_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    xin = sel.lm_head_input(x, nw, 1e-6, hidden_dtype="bf16", act_dtype="bf16")
+    check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(xin, W), 1, "gemm B=256 prenorm")

@@ -34,7 +34,7 @@ def _inputs(rng, batch, H, V, hidden_dtype):
     (1, 512, "bf16", "f32"),     # streaming GEMV, fused, H = 512
     (5, 1024, "bf16", "bf16"),   # tile kernel, fused
     (64, 1024, "f32", "bf16"),   # tile kernel, fused, f32 input
-    (70, 1024, "bf16", "bf16"),  # tile kernel in two launches
+    (70, 1024, "bf16", "bf16"),  # blocked GEMM, prologue kernel
     (8, 1024, "bf16", "f32"),    # exact-split MFMA path, prologue kernel
     (4, 40, "f16", "f32"),       # generic path, prologue kernel
 ])
