@@ -107,6 +107,17 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c)
   }
 }
 
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// v_mfma_f32_32x32x16_bf16: lane l holds A row (l & 31) and B column (l & 31)
+// at k = 8 (l >> 5) .. +7; D element e of lane l is row 8 (e >> 2) +
+// 4 (l >> 5) + (e & 3), column l & 31.  Twice the work of a 16x16x32 in
+// about the same issue time on gfx950 (measured ~2.2 vs ~1.25 PFLOP/s).
+__device__ __forceinline__ f32x16_t mfma32x32x16_bf16(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
+}
+
 __device__ __forceinline__ float apply_cast(float v, int rc) {
   if (rc == 1) return round_bf16(v);
   if (rc == 2) return round_f16(v);
@@ -1107,143 +1118,253 @@ static int dispatch_tile(const LmArgs& a, hipStream_t s) {
 // bf16 hidden x bf16 W [V, H], H % 64 == 0, up to 256 rows in ONE pass over
 // W.  The hidden of 256 rows (512 KB at H = 1024) is a CU's whole register
 // file, so unlike the tile kernel nothing is held for the whole call: a block
-// tile is 128 vocabulary rows x all 256 batch rows, and K is streamed in
-// chunks of 64 -- the W chunk (128 x 64, 16 KB, from HBM) and the hidden
-// chunk (256 x 64, 32 KB, L2-resident) both staged in LDS, the next chunk
-// prefetched into registers while the current one is multiplied.  Wave w of
-// 8 computes the 64 x 64 sub-tile (vocab half w & 1, batch quarter w >> 1) as
-// 4 x 4 v_mfma_f32_16x16x32_bf16 tiles (64 accumulators per lane), reading
-// 4 A and 4 B fragments per 32-wide k-step: every W and hidden element is
-// read from LDS by 4 and 2 waves.  LDS rows are XOR-swizzled by the 16-byte
-// column (q) index: conflict-free fragment reads and stores.
-// Blocks are persistent over the vocabulary tiles (round robin) and keep, per
-// batch row, a running best key; each block finally stores its 256 keys and
-// gemm_reduce_kernel takes the per-row maximum (no same-address atomics).
-// MODE_LOGITS stores the rounded logits instead.
-static constexpr int kGemmBV = 128, kGemmBB = 256, kGemmKC = 64;
+// tile is 256 vocabulary rows x all 256 batch rows, and K is streamed in
+// stages of 32 -- the W stage (256 x 32, 16 KB, from HBM) and the hidden
+// stage (256 x 32, 16 KB, L2-resident) staged through a two-buffer LDS ring.
+// Each thread loads 4 x 16 B per stage into registers; two register sets
+// keep the stages s+2 and s+3 in flight while stage s is multiplied, so every
+// load has two compute phases to land, and the pipeline runs on across the
+// block's vocabulary tiles (round robin) without draining.  One barrier per
+// stage.  Each wave computes a 128 x 64 sub-tile (vocab part, batch quarter)
+// as 4 x 2 v_mfma_f32_32x32x16_bf16 tiles (128 accumulators per lane),
+// reading 4 A and 2 B fragments per 16-wide k-step.
+// LDS layout: 16-byte column q of row `row` at q * ROWS + (row ^ 2q): the 32
+// lanes of a fragment read hit 32 distinct slots of one 512 B window, and the
+// 8 lanes (2 rows x 4 columns) of a store phase hit 8 distinct bank groups.
+// Blocks keep, per batch row, a running best key; each block finally stores
+// its 256 keys and gemm_reduce_kernel takes the per-row maximum (no
+// same-address atomics).  MODE_LOGITS stores the rounded logits instead.
+static constexpr int kGemmBB = 256, kGemmKC = 32;
 
-template <int MODE>
-__global__ void __launch_bounds__(512) lm_head_gemm_kernel(LmArgs a, unsigned long long* blk_keys) {
-  constexpr int QC = kGemmKC / 8;  // 16-byte columns per chunk row
-  __shared__ u32x4_t As[QC * kGemmBV];
-  __shared__ u32x4_t Bs[QC * kGemmBB];
-  __shared__ unsigned long long kred[2][kGemmBB];
+template <int MODE, int BV>
+__global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a, unsigned long long* blk_keys) {
+  constexpr int Q = kGemmKC / 8;  // 16-byte columns per row and stage
+  constexpr int VH = BV / 128;  // 128-row vocabulary parts; 4 batch quarters each
+  constexpr int NT = VH * 4 * 64;  // threads
+  constexpr int PA = Q * BV / NT, PB = Q * kGemmBB / NT;  // 16 B load pieces per thread (W, hidden)
+  static_assert(PA == 2, "two W pieces per thread and stage");
+  __shared__ u32x4_t As[2][Q * BV];
+  __shared__ u32x4_t Bs[2][Q * kGemmBB];
+  __shared__ unsigned long long kred[VH][kGemmBB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 4, r = lane & 15;
-  const int vi = wave & 1, bj = wave >> 1;
+  const int vi = wave % VH, bj = wave / VH;
   const int B = a.B, V = a.V, H = a.H;
   const uint16_t* W = (const uint16_t*)a.W;
   const uint16_t* X = (const uint16_t*)a.hidden;
-  const int ntiles = (V + kGemmBV - 1) / kGemmBV;
-  const int nchunks = H / kGemmKC;
-  // the thread's load pieces: W 2 x 16 B (rows p >> 3, column p & 7), hidden 4 x 16 B
-  auto wpiece = [&](int i) { return tid + 512 * i; };
-  unsigned long long best[4];
+  const int ntiles = (V + BV - 1) / BV;
+  const int nkc = H / kGemmKC;
+  const int my_tiles = blockIdx.x < ntiles ? (ntiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+  const int S = my_tiles * nkc;  // stages of this block
+  // load piece p: row p >> 2, 16-byte column p & 3, LDS slot q * ROWS + (row ^ 2q)
+  int arow[PA], aq[PA], aslot[PA], bslot[PB];
+  const u32x4_t* xp[PB];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) best[t] = 0;
-
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int v0 = tile * kGemmBV;
-    f32x4_t acc[4][4];
+  for (int i = 0; i < PA; ++i) {
+    const int p = tid + NT * i;
+    arow[i] = p >> 2;
+    aq[i] = p & 3;
+    aslot[i] = aq[i] * BV + (arow[i] ^ (aq[i] << 1));
+  }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < PB; ++i) {
+    const int p = tid + NT * i, row = p >> 2, q = p & 3;
+    bslot[i] = q * kGemmBB + (row ^ (q << 1));
+    // rows >= B repeat row B - 1: a fixed count of loads in flight and no
+    // select on the loaded data (which would make the compiler wait for it
+    // early); their batch columns are never read
+    xp[i] = (const u32x4_t*)(X + (size_t)min(row, B - 1) * H) + q;
+  }
+  // Two register sets: stages s+2 and s+3 (W and hidden) are in flight while
+  // stage s is multiplied.  Loads past the last stage re-read it, so every
+  // path has the same loads in flight and each LDS store waits for exactly
+  // its own stage.
+  u32x4_t RA[2][PA], RB[2][PB];
+  auto stage_of = [&](int st, int& v0, int& kc) NVJSEL_INLINE {
+    st = st < S ? st : S - 1;
+    const int t = st / nkc;
+    kc = st - t * nkc;
+    v0 = (blockIdx.x + t * gridDim.x) * BV;
+  };
+  auto gload_a = [&](auto set, int st) NVJSEL_INLINE {
+    constexpr int e = decltype(set)::value;
+    int v0, kc;
+    stage_of(st, v0, kc);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    u32x4_t pw[2], ph[4];
-    auto load_chunk = [&](int c) NVJSEL_INLINE {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int p = wpiece(i), row = p >> 3, q = p & 7;
-        const int v = min(v0 + row, V - 1);
-        pw[i] = stream_load((const u32x4_t*)(W + (size_t)v * H + c * kGemmKC) + q);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int p = wpiece(i), row = p >> 3, q = p & 7;
-        ph[i] = row < B ? *((const u32x4_t*)(X + (size_t)row * H + c * kGemmKC) + q) : u32x4_t{0u, 0u, 0u, 0u};
-      }
-    };
-    load_chunk(0);
-    for (int c = 0; c < nchunks; ++c) {
-      __syncthreads();  // every fragment read of the previous chunk is done
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int p = wpiece(i), row = p >> 3, q = p & 7;
-        As[q * kGemmBV + (row ^ q)] = pw[i];
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int p = wpiece(i), row = p >> 3, q = p & 7;
-        Bs[q * kGemmBB + (row ^ q)] = ph[i];
-      }
-      __syncthreads();
-      if (c + 1 < nchunks) load_chunk(c + 1);  // in flight during the MFMAs
-#pragma unroll
-      for (int ks = 0; ks < kGemmKC / 32; ++ks) {
-        const int q = ks * 4 + g;
-        u32x4_t bf[4];
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) bf[tb] = Bs[q * kGemmBB + ((bj * 64 + tb * 16 + r) ^ q)];
-#pragma unroll
-        for (int tv = 0; tv < 4; ++tv) {
-          const u32x4_t af = As[q * kGemmBV + ((vi * 64 + tv * 16 + r) ^ q)];
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb) acc[tv][tb] = mfma16x16x32<DT_BF16>(af, bf[tb], acc[tv][tb]);
-        }
-      }
+    for (int i = 0; i < PA; ++i) {
+      const int v = min(v0 + arow[i], V - 1);
+      RA[e][i] = *((const u32x4_t*)(W + (size_t)v * H + kc * kGemmKC) + aq[i]);
     }
-    // epilogue: D[vocab 4 g + i][batch r] of tile (tv, tb)
+  };
+  auto gload_b = [&](auto set, int st) NVJSEL_INLINE {
+    constexpr int e = decltype(set)::value;
+    int v0, kc;
+    stage_of(st, v0, kc);
+#pragma unroll
+    for (int i = 0; i < PB; ++i) RB[e][i] = xp[i][kc * Q];
+  };
+  auto lstore = [&](auto set, auto buf) NVJSEL_INLINE {
+    constexpr int e = decltype(set)::value, f = decltype(buf)::value;
+#pragma unroll
+    for (int i = 0; i < PA; ++i) As[f][aslot[i]] = RA[e][i];
+#pragma unroll
+    for (int i = 0; i < PB; ++i) Bs[f][bslot[i]] = RB[e][i];
+  };
+  // 32 x 32 tiles: 4 (vocab) x 2 (batch) per wave
+  const int h = lane >> 5, c32 = lane & 31;
+  f32x16_t acc[4][2];
+  auto zero_acc = [&]() NVJSEL_INLINE {
 #pragma unroll
     for (int tv = 0; tv < 4; ++tv)
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        const int b = bj * 64 + tb * 16 + r;
+      for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int v = v0 + vi * 64 + tv * 16 + 4 * g + i;
-          if (v >= V || b >= B) continue;
-          const float val = apply_cast(acc[tv][tb][i], a.reduce_cast);
-          if constexpr (MODE == MODE_LOGITS) store_logit(a, b, v, val);
-          else best[tb] = max_u64(best[tb], argmax_key(val, (uint32_t)v));
+        for (int e = 0; e < 16; ++e) acc[tv][tb][e] = 0.f;
+  };
+  auto compute = [&](auto buf) NVJSEL_INLINE {
+    constexpr int f = decltype(buf)::value;
+#pragma unroll
+    for (int ks = 0; ks < kGemmKC / 16; ++ks) {
+      const int q = ks * 2 + h, sw = q << 1;
+      u32x4_t bf[2];
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) bf[tb] = Bs[f][q * kGemmBB + ((bj * 64 + tb * 32 + c32) ^ sw)];
+#pragma unroll
+      for (int tv = 0; tv < 4; ++tv) {
+        const u32x4_t af = As[f][q * BV + ((vi * 128 + tv * 32 + c32) ^ sw)];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) acc[tv][tb] = mfma32x32x16_bf16(af, bf[tb], acc[tv][tb]);
+      }
+    }
+  };
+  // D[vocab 8 (e >> 2) + 4 h + (e & 3)][batch c32] of tile (tv, tb), after
+  // the last stage of tile t.  Greedy: per (tile, lane) the maximum of the 16
+  // raw values (v_maximum3: NaN propagates), rounded; only where that beats
+  // the lane's running best is the first element rounding to it looked up.
+  // Rounding is monotone, so max(round(x)) = round(max(x)), and ties keep the
+  // lowest vocabulary row (rows ascend with e and with t).  Rows past V
+  // repeat row V - 1 (clamped loads) and lose its ties.
+  uint32_t bo[2] = {0u, 0u}, bi[2] = {0u, 0u};  // running best: ordered value, row
+  auto epilogue = [&](int t) NVJSEL_INLINE {
+    const int v0 = (blockIdx.x + t * gridDim.x) * BV + vi * 128;
+#pragma unroll
+    for (int tv = 0; tv < 4; ++tv)
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        const f32x16_t& d = acc[tv][tb];
+        if constexpr (MODE == MODE_LOGITS) {
+          const int b = bj * 64 + tb * 32 + c32;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int v = v0 + tv * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (v < V && b < B) store_logit(a, b, v, apply_cast(d[e], a.reduce_cast));
+          }
+        } else {
+          float m = d[0];
+#pragma unroll
+          for (int e = 1; e < 15; e += 2)
+            m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, d[e]), d[e + 1]);
+          m = __builtin_elementwise_maximum(m, d[15]);
+          const float rm = apply_cast(m, a.reduce_cast);
+          const uint32_t om = ord_f32(rm);
+          const bool up = om > bo[tb];
+          if (__builtin_amdgcn_ballot_w64(up)) {
+            int first = 15;
+            const bool nan = rm != rm;
+#pragma unroll
+            for (int e = 14; e >= 0; --e) {
+              const float x = apply_cast(d[e], a.reduce_cast);
+              if (nan ? x != x : x == rm) first = e;
+            }
+            if (up) {
+              bo[tb] = om;
+              bi[tb] = (uint32_t)(v0 + tv * 32 + 8 * (first >> 2) + 4 * h + (first & 3));
+            }
+          }
         }
       }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  if (S > 0) {  // S is even: nkc = H / 32 with H % 64 == 0
+    // prologue: stage 0 in LDS buffer 0, stages 1 and 2 in sets 1 and 0 --
+    // issued in the order the loop's back edge leaves them in flight, so the
+    // wait counts agree at the loop head and no store waits for more than
+    // its own stage
+    gload_b(I0{}, 0);
+    gload_a(I0{}, 0);
+    lstore(I0{}, I0{});
+    gload_b(I1{}, 1);
+    gload_a(I1{}, 1);
+    gload_b(I0{}, 2);
+    gload_a(I0{}, 2);
+    __syncthreads();
+    // stage s: store stage s+1 (set (s+1)&1) to buffer (s+1)&1, load stage
+    // s+3 into that set, multiply buffer s&1
+    auto step = [&](int st, auto cur) NVJSEL_INLINE {
+      constexpr int c = decltype(cur)::value;
+      using N = std::integral_constant<int, 1 - c>;
+      lstore(N{}, N{});
+      gload_b(N{}, st + 3);
+      gload_a(N{}, st + 3);
+      compute(cur);
+      __syncthreads();
+    };
+    // the accumulators are zeroed and read outside the stage loop, so they
+    // stay in place across it
+    for (int t = 0; t < my_tiles; ++t) {
+      zero_acc();
+      for (int kc = 0; kc < nkc; kc += 2) {
+        step(t * nkc + kc, I0{});
+        step(t * nkc + kc + 1, I1{});
+      }
+      epilogue(t);
+    }
   }
   if constexpr (MODE == MODE_LOGITS) return;
-  // the four lane groups (vocab rows 4 g ..) of a column, then the two vocab halves
+  // the two lane halves (vocab rows 4 h ..) of a column, then the vocabulary parts
+  unsigned long long best[2];
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    best[tb] = max_u64(best[tb], shfl_xor_u64(best[tb], 16));
+  for (int tb = 0; tb < 2; ++tb) {
+    best[tb] = ((unsigned long long)bo[tb] << 32) | (unsigned long long)(~bi[tb]);
     best[tb] = max_u64(best[tb], shfl_xor_u64(best[tb], 32));
-    if (g == 0) kred[vi][bj * 64 + tb * 16 + r] = best[tb];
+    if (h == 0) kred[vi][bj * 64 + tb * 32 + c32] = best[tb];
   }
   __syncthreads();
-  for (int b = tid; b < kGemmBB; b += 512)
-    blk_keys[(size_t)blockIdx.x * kGemmBB + b] = max_u64(kred[0][b], kred[1][b]);
+  for (int b = tid; b < kGemmBB; b += NT) {
+    unsigned long long m = kred[0][b];
+#pragma unroll
+    for (int h = 1; h < VH; ++h) m = max_u64(m, kred[h][b]);
+    blk_keys[(size_t)blockIdx.x * kGemmBB + b] = m;
+  }
 }
 
 // Per row: the maximum of the blocks' keys -> id (and the winning logit);
-// the keys read are cleared.
+// the keys read are cleared.  Block x handles 64 rows; its 4 waves stride
+// over the blocks' key rows, so every wave's reads are one contiguous 512 B.
 __global__ void __launch_bounds__(256) gemm_reduce_kernel(unsigned long long* __restrict__ blk_keys, int nblk,
                                                           int B, int32_t* out_ids, float* out_best) {
-  __shared__ unsigned long long red[4];
-  const int b = blockIdx.x;
+  __shared__ unsigned long long red[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int b = blockIdx.x * 64 + lane;
   unsigned long long m = 0;
-  for (int i = threadIdx.x; i < nblk; i += 256) {
+  for (int i = w; i < nblk; i += 4) {
     unsigned long long* p = blk_keys + (size_t)i * kGemmBB + b;
     m = max_u64(m, *p);
-    *p = 0;  // the workspace is zero at rest (the GEMM writes zero keys for rows >= B)
+    *p = 0;  // the workspace is zero at rest
   }
-  m = wave_max_u64(m);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  red[w][lane] = m;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    m = max_u64(max_u64(red[0], red[1]), max_u64(red[2], red[3]));
+  if (w == 0 && b < B) {
+    m = max_u64(max_u64(red[0][lane], red[1][lane]), max_u64(red[2][lane], red[3][lane]));
     out_ids[b] = (int32_t)(~(uint32_t)m);
     if (out_best) out_best[b] = unord_f32((uint32_t)(m >> 32));
   }
 }
 
-static constexpr int kGemmBpc = 1;  // blocks per CU of the blocked GEMM
+// vocabulary rows per block tile: 256 (8 waves, one block per CU; measured
+// 185 us at B = 256, V = 248320) or 128 (4 waves, two blocks per CU: 195 us)
+static constexpr int kGemmBV = 256;
+static constexpr int kGemmBpc = 256 / kGemmBV;  // blocks per CU of the blocked GEMM
 static constexpr int kGemmMaxBlocks = 1024;  // bounds the per-block key array
 static size_t gemm_keys_bytes() { return (size_t)kGemmMaxBlocks * kGemmBB * 8; }
 
@@ -1253,11 +1374,11 @@ static int launch_gemm(const LmArgs& a, unsigned long long* blk_keys, hipStream_
   int grid = kGemmBpc * device_cu_count();
   if (grid > kGemmMaxBlocks) grid = kGemmMaxBlocks;
   if (grid > ntiles) grid = ntiles;
-  hipLaunchKernelGGL(lm_head_gemm_kernel<MODE>, dim3(grid), dim3(512), 0, stream, a, blk_keys);
+  hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a, blk_keys);
   NVJSEL_CHECK_LAUNCH("lm_head_gemm_kernel");
   if constexpr (MODE == MODE_GREEDY) {
-    hipLaunchKernelGGL(gemm_reduce_kernel, dim3(a.B), dim3(256), 0, stream, blk_keys, grid, a.B, a.out_ids,
-                       a.out_best);
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((a.B + 63) / 64), dim3(256), 0, stream, blk_keys, grid, a.B,
+                       a.out_ids, a.out_best);
     NVJSEL_CHECK_LAUNCH("gemm_reduce_kernel");
   }
   return NVJSEL_OK;
@@ -1554,7 +1675,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   const bool tile = !gemv && bf16_mfma && H == 1024 && (prenorm || (((uintptr_t)hidden) & 15) == 0);
   // blocked GEMM: 64 < B, bf16 activations, one pass over W per 256 rows (greedy/logits)
   const size_t gemm_off = lm_ws_small_bytes(batch) + (prenorm ? lm_prenorm_bytes(batch, H) : 0);
-  const bool gemm = mode != MODE_SAMPLE && batch > kGemmMinBatch && bf16_mfma && (H % kGemmKC) == 0 &&
+  const bool gemm = mode != MODE_SAMPLE && batch > kGemmMinBatch && bf16_mfma && (H % (2 * kGemmKC)) == 0 &&
                     eff_dtype == NVJSEL_BF16 && (prenorm || (((uintptr_t)hidden) & 15) == 0) &&
                     (mode == MODE_LOGITS || (workspace && ws_bytes >= gemm_off + gemm_keys_bytes()));
   unsigned long long* gemm_keys = gemm && mode != MODE_LOGITS ? (unsigned long long*)((char*)workspace + gemm_off) : nullptr;
