@@ -272,6 +272,7 @@ __device__ __forceinline__ void load_vec(const char* row, int i0, float* o) {
 template <int DT, int VEC, int EPT>
 __device__ __forceinline__ void load_chunk_elems(const char* row, int base, int V, bool raw, float tp,
                                                  float (&x)[EPT], uint32_t& valid) {
+  static_assert(EPT % VEC == 0, "whole vectors per thread");
   valid = 0;
 #pragma unroll
   for (int q = 0; q < EPT / VEC; ++q) {
@@ -509,43 +510,51 @@ __device__ __forceinline__ unsigned long long wave_gumbel(const SampleArgs& a, i
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-  // dense entry e = 256 g + 4 lane + j
+  // The dense entries are drawn in rounds of up to 256: a round with r
+  // entries left runs C = 4, 2 or 1 interleaved Threefry chains per lane
+  // (entry off + C lane + j, j < C) for r > 128, > 64 or <= 64 -- a wave with a
+  // few survivors pays for one chain per lane, not four.
   constexpr int G = EPT / 4;
-  float st[EPT];
+  float st[G][4];
+  int cr[G];  // chains of each round (0: round not run)
   uint32_t tmax = 0;  // ord of the fast maximum
+  auto round = [&](auto CC, int g) NVJSEL_INLINE {
+    constexpr int C = decltype(CC)::value;
+    const int e0 = 256 * g + C * lane;
+    uint32_t idx[C];
+    float xv[C];
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const bool in = e0 + j < (int)n;
+      idx[j] = in ? di[e0 + j] : 0u;
+      xv[j] = in ? dx[e0 + j] : -INFINITY;
+    }
+    float t[C];
+    if (a.noise) {
+#pragma unroll
+      for (int j = 0; j < C; ++j) t[j] = xv[j] + a.noise[(size_t)b * a.V + idx[j]];
+    } else {
+      uint32_t bits[C];
+      random_bits32_n<C>(key, idx, bits);
+#pragma unroll
+      for (int j = 0; j < C; ++j) t[j] = xv[j] + gumbel_fast_from_bits(bits[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const bool in = e0 + j < (int)n;
+      const float v = (t[j] != t[j]) ? INFINITY : t[j];  // NaN only from a NaN logit
+      st[g][j] = in ? v : -INFINITY;
+      const uint32_t o = in ? ord_f32(v) : 0u;
+      tmax = o > tmax ? o : tmax;
+    }
+  };
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const int e0 = 256 * g + 4 * lane;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) st[4 * g + j] = -INFINITY;
-    if (256 * g < (int)n) {  // wave-uniform
-      uint32_t idx[4];
-      float xv[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bool in = e0 + j < (int)n;
-        idx[j] = in ? di[e0 + j] : 0u;
-        xv[j] = in ? dx[e0 + j] : -INFINITY;
-      }
-      float t[4];
-      if (a.noise) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) t[j] = xv[j] + a.noise[(size_t)b * a.V + idx[j]];
-      } else {
-        uint32_t bits[4];
-        random_bits32_n<4>(key, idx, bits);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) t[j] = xv[j] + gumbel_fast_from_bits(bits[j]);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bool in = e0 + j < (int)n;
-        const float v = (t[j] != t[j]) ? INFINITY : t[j];  // NaN only from a NaN logit
-        st[4 * g + j] = in ? v : -INFINITY;
-        const uint32_t o = in ? ord_f32(v) : 0u;
-        tmax = o > tmax ? o : tmax;
-      }
-    }
+    const int r = (int)n - 256 * g;  // wave-uniform
+    cr[g] = r <= 0 ? 0 : r > 128 ? 4 : r > 64 ? 2 : 1;
+    if (cr[g] == 4) round(std::integral_constant<int, 4>{}, g);
+    else if (cr[g] == 2) round(std::integral_constant<int, 2>{}, g);
+    else if (cr[g] == 1) round(std::integral_constant<int, 1>{}, g);
   }
   const float m = unord_f32(wave_max_u32(tmax));
   // |fast - exact| <= 1.91e-6 on the draw (measured over all 2^23 draws),
@@ -558,8 +567,8 @@ __device__ __forceinline__ unsigned long long wave_gumbel(const SampleArgs& a, i
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int e = 256 * g + 4 * lane + j;
-      if (e < (int)n && st[4 * g + j] >= thr) {
+      const int e = 256 * g + cr[g] * lane + j;
+      if (j < cr[g] && e < (int)n && st[g][j] >= thr) {
         const uint32_t i = di[e];
         best = max_u64(best, argmax_key(dx[e] + exact_noise(a, b, key, (int)i), i));
       }
