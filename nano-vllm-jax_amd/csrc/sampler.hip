@@ -94,7 +94,7 @@ struct SampleArgs {
   float* cand_floor_a;             // [B, nchunks]
   float* cand_floor;               // [B, nchunks] logit floor of each chunk's candidates
   unsigned long long* cand;        // [B, nchunks, kCandCap]; one-pass calls: [B, sub-chunks] block keys
-  unsigned long long* topp_chunk_hist;  // [B, nchunks, kToppBins] chunk histograms (top-p-only rows)
+  uint32_t* topp_chunk_hist;       // [B, nchunks, kToppBins] chunk histograms, 2^-17 units (top-p-only rows)
   int32_t* topp_chunk_tb;          // [B, nchunks] grid bin of each chunk's maximum
   int32_t* row_ib;                 // [B] top-p rows: grid bin of the crossing (INT_MIN: none)
   unsigned long long* row_target;  // [B] top-p rows: weight units needed inside the crossing bin
@@ -186,6 +186,13 @@ __device__ __forceinline__ uint64_t fixed_mass(float x, float m) {
 // weight is formed), and bin ib's weights scale by exp(edge - row edge).
 __device__ __forceinline__ int topp_ibin(float x) { return (int)floorf(x * 32.0f); }
 __device__ __forceinline__ float topp_edge(int ib) { return (float)ib * 0.03125f; }
+// The chunk histograms hold the same weight in 2^-17 units (u32: a 16384-
+// element chunk sums to < 2^31): per element at most 2^-18 of its weight off,
+// so a row's mass sums are within 4e-6 relative of the 2^-40 ones.
+__device__ __forceinline__ uint32_t edge_mass17(float x, int ib) {
+  const float d = x - topp_edge(ib + 1);
+  return (uint32_t)rintf(__builtin_amdgcn_exp2f(d * 1.44269504088896341f) * 131072.0f);
+}
 __device__ __forceinline__ uint64_t edge_mass(float x, int ib) {
   const float d = x - topp_edge(ib + 1);
   return (uint64_t)rintf(__builtin_amdgcn_exp2f(d * 1.44269504088896341f) * 1099511627776.0f);
@@ -781,7 +788,7 @@ struct ScanShared {
   uint32_t wfloor[kThreads / 64];
   float wtop[kThreads / 64];  // each wave's kTops-th largest lane maximum
   uint32_t cnt, cnt_b, waves;
-  unsigned long long topp_h[kToppBins];  // top-p-only rows: the chunk's grid-bin histogram
+  uint32_t topp_h[kToppBins];  // top-p-only rows: the chunk's grid-bin histogram (2^-17 units)
 };
 
 typedef short nvjsel_s16x2 __attribute__((ext_vector_type(2)));
@@ -1028,13 +1035,13 @@ __device__ __forceinline__ void scan_item(const SampleArgs& a, int b, int c, Chu
           const float x = r.elem(q, e) / rp.tp;
           if (x >= lowb) {
             const int ib = topp_ibin(x);
-            atomicAdd(&sh.topp_h[tb - ib], (unsigned long long)edge_mass(x, ib));
+            atomicAdd(&sh.topp_h[tb - ib], edge_mass17(x, ib));
           }
         }
       }
     }
     lds_barrier();
-    unsigned long long* ch = a.topp_chunk_hist + ((size_t)b * a.nchunks + c) * kToppBins;
+    uint32_t* ch = a.topp_chunk_hist + ((size_t)b * a.nchunks + c) * kToppBins;
     for (int d = threadIdx.x; d < kToppBins; d += kThreads) ch[d] = sh.topp_h[d];
     if (threadIdx.x == 0) a.topp_chunk_tb[(size_t)b * a.nchunks + c] = tb;
     return;
@@ -1567,10 +1574,11 @@ struct ToppXShared {
 };
 
 // Crossing bin of a row histogram held as h[q] = bin D = PER * t + q of thread
-// t (grid bin TB - D) and the weight still needed inside it: bins are summed
-// in fp64 with their scales exp(-D / 32), the crossing is the first bin whose
-// cumulative mass exceeds p * Z, and the elements of that bin must reach
-// floor((p * Z - mass above) / scale) + 1 of its integer weight units.
+// t (grid bin TB - D), in 2^-17 weight units, and the weight still needed
+// inside it: bins are summed in fp64 with their scales exp(-D / 32), the
+// crossing is the first bin whose cumulative mass exceeds p * Z, and the
+// elements of that bin must reach floor((p * Z - mass above) / scale) + 1 of
+// the 2^-40 weight units the finish kernel sums them in.
 template <int PER>
 __device__ __forceinline__ void topp_crossing(const unsigned long long (&h)[PER], int tb, float p, ToppXShared& sh) {
   double mq[PER], sc[PER], local = 0.0;
@@ -1578,7 +1586,7 @@ __device__ __forceinline__ void topp_crossing(const unsigned long long (&h)[PER]
   for (int q = 0; q < PER; ++q) {
     const int D = threadIdx.x * PER + q;
     sc[q] = exp2(-(double)D * (1.4426950408889634 / 32.0)) * 0x1p-40;
-    mq[q] = (double)h[q] * sc[q];
+    mq[q] = (double)h[q] * (sc[q] * 0x1p23);
     local += mq[q];
   }
   // exclusive block scan in thread order
@@ -1708,18 +1716,18 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     constexpr int U = 16;
     unsigned long long h[PER] = {};
     for (int c0 = 0; c0 < NC; c0 += U) {
-      unsigned long long v[U][PER];
+      uint32_t v[U][PER];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int c = c0 + u;
         const int tbc = c < NC ? s.tb[c] : INT_MIN;
         const int sft = (tbc == INT_MIN || TB == INT_MIN) ? kToppBins * 2 : TB - tbc;
-        const unsigned long long* ch = a.topp_chunk_hist + ((size_t)b * NC + (c < NC ? c : NC - 1)) * kToppBins;
+        const uint32_t* ch = a.topp_chunk_hist + ((size_t)b * NC + (c < NC ? c : NC - 1)) * kToppBins;
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
           const int d = (int)threadIdx.x * PER + q - sft;  // < kToppBins: sft >= 0
           v[u][q] = ch[d >= 0 ? d : 0];
-          v[u][q] = d >= 0 ? v[u][q] : 0ull;
+          v[u][q] = d >= 0 ? v[u][q] : 0u;
         }
       }
 #pragma unroll
@@ -1976,7 +1984,7 @@ static WsLayout ws_layout(int B, int V) {
   WsLayout w;
   size_t o = 0;
   w.lane_tops = o;  o += align_up((size_t)B * nc * (kThreads / 64) * kTopsPub * 4, 256);
-  w.topp_chunk_hist = o; o += align_up((size_t)B * nc * kToppBins * 8, 256);
+  w.topp_chunk_hist = o; o += align_up((size_t)B * nc * kToppBins * 4, 256);
   w.topp_chunk_tb = o;   o += align_up((size_t)B * nc * 4, 256);
   w.row_ib = o;          o += align_up((size_t)B * 4, 256);
   w.row_target = o;      o += align_up((size_t)B * 8, 256);
@@ -2018,7 +2026,7 @@ static SampleArgs make_args(const void* logits, int dtype, int batch, int vocab,
 
   a.stride = row_stride;
   a.lane_tops = (float*)(ws + w.lane_tops);
-  a.topp_chunk_hist = (unsigned long long*)(ws + w.topp_chunk_hist);
+  a.topp_chunk_hist = (uint32_t*)(ws + w.topp_chunk_hist);
   a.topp_chunk_tb = (int32_t*)(ws + w.topp_chunk_tb);
   a.row_ib = (int32_t*)(ws + w.row_ib);
   a.row_target = (unsigned long long*)(ws + w.row_target);
