@@ -92,9 +92,10 @@ def test_hidden_dim_not_multiple_of_32_uses_generic():
     check_greedy(ids, sel.lm_head_logits(as_f32(h)[:, 0], as_f32(E)), 1, "H=40")
 
 
-@pytest.mark.parametrize("H,B", [(256, 2), (512, 2), (512, 1), (1024, 5)])
+@pytest.mark.parametrize("H,B", [(256, 2), (512, 2), (512, 1), (1024, 5), (1024, 100), (256, 256)])
 def test_ties_resolve_to_lowest_index_across_blocks(H, B):
-    """Identical rows far apart in the vocabulary (different blocks/waves)."""
+    """Identical rows far apart in the vocabulary (different blocks/waves;
+    B > 64: different blocked-GEMM tiles and lanes)."""
     rng = np.random.default_rng(11)
     V = 70000
     Wn = (rng.standard_normal((V, H)) * 0.01).astype(np.float32)
@@ -106,15 +107,15 @@ def test_ties_resolve_to_lowest_index_across_blocks(H, B):
     assert list(ids) == [12345] * B
 
 
-@pytest.mark.parametrize("H", [128, 512, 2048])
-def test_nan_logit_wins_first(H):
+@pytest.mark.parametrize("H,B", [(128, 3), (512, 3), (2048, 3), (512, 80), (1024, 130)])
+def test_nan_logit_wins_first(H, B):
     rng = np.random.default_rng(12)
     V = 5000
     Wn = (rng.standard_normal((V, H)) * 0.01).astype(np.float32)
     Wn[4000, 3] = np.nan
     Wn[2500, 7] = np.nan
-    ids = _run(bf16_tensor(rng.standard_normal((3, H))), bf16_tensor(Wn), weight_layout="vh")
-    assert list(ids) == [2500, 2500, 2500]
+    ids = _run(bf16_tensor(rng.standard_normal((B, H))), bf16_tensor(Wn), weight_layout="vh")
+    assert list(ids) == [2500] * B
 
 
 def test_repeated_calls_reuse_workspace():

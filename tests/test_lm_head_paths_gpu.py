@@ -243,6 +243,22 @@ def test_gemm_greedy_and_logits(B, H):
     assert torch.equal(ids, ids2)
 
 
+@pytest.mark.parametrize("rc", [0, 2])
+def test_gemm_other_roundings(rc):
+    """The blocked GEMM with the caller's reduce_cast: 0 (fp32 logits, f32
+    out) and 2 (f16 rounding), greedy and logits."""
+    rng = np.random.default_rng(880 + rc)
+    B, H, V = 96, 512, 7001
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    h = _hidden(rng, B, H, torch.bfloat16)
+    ids = nvjsel.lm_head_greedy_top1_hip(h, W.T, reduce_cast=rc)
+    logits = nvjsel.lm_head_logits_hip(h, W.T, reduce_cast=rc)
+    torch.cuda.synchronize()
+    hf, wf = h.float().cpu().numpy(), W.float().cpu().numpy()
+    check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(hf, wf), rc, f"gemm rc={rc}")
+    _check_logits(logits, hf, wf, rc, f"gemm logits rc={rc}")
+
+
 def test_gemm_full_vocab_b256_with_prenorm():
     """The bench shape (B = 256, V = 151936, H = 1024) through the final-norm
     entry (prologue kernel into the workspace, then the GEMM), against the
