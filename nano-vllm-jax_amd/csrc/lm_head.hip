@@ -1134,7 +1134,80 @@ static int dispatch_tile(const LmArgs& a, hipStream_t s) {
 // Blocks keep, per batch row, a running best key; each block finally stores
 // its 256 keys and gemm_reduce_kernel takes the per-row maximum (no
 // same-address atomics).  MODE_LOGITS stores the rounded logits instead.
-static constexpr int kGemmBB = 256, kGemmKC = 32;
+static constexpr int kGemmBBRows = 256;  // batch rows per blocked-GEMM pass
+static constexpr int kGemmBB = kGemmBBRows, kGemmKC = 32;
+
+// Epilogue of one block tile of the blocked GEMM for the wave's 128 x 64
+// sub-tile: D[vocab 8 (e >> 2) + 4 h + (e & 3)][batch c32] of 32 x 32 tile
+// (tv, tb), vocabulary rows from v0.  Greedy: per (tile, lane) the maximum of
+// the 16 raw values (v_maximum3: NaN propagates), rounded; only where that
+// beats the lane's running best (bo, bi) is the first element rounding to it
+// looked up.  Rounding is monotone, so max(round(x)) = round(max(x)), and ties
+// keep the lowest vocabulary row (rows ascend with e and with the tiles).
+// Rows past V repeat row V - 1 (clamped loads) and lose its ties.
+template <int MODE>
+__device__ __forceinline__ void gemm_epilogue(const LmArgs& a, const f32x16_t (&acc)[4][2], int v0, int bj, int h,
+                                              int c32, uint32_t (&bo)[2], uint32_t (&bi)[2]) {
+#pragma unroll
+  for (int tv = 0; tv < 4; ++tv)
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      const f32x16_t& d = acc[tv][tb];
+      if constexpr (MODE == MODE_LOGITS) {
+        const int b = bj * 64 + tb * 32 + c32;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int v = v0 + tv * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (v < a.V && b < a.B) store_logit(a, b, v, apply_cast(d[e], a.reduce_cast));
+        }
+      } else {
+        float m = d[0];
+#pragma unroll
+        for (int e = 1; e < 15; e += 2)
+          m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, d[e]), d[e + 1]);
+        m = __builtin_elementwise_maximum(m, d[15]);
+        const float rm = apply_cast(m, a.reduce_cast);
+        const uint32_t om = ord_f32(rm);
+        const bool up = om > bo[tb];
+        if (__builtin_amdgcn_ballot_w64(up)) {
+          int first = 15;
+          const bool nan = rm != rm;
+#pragma unroll
+          for (int e = 14; e >= 0; --e) {
+            const float x = apply_cast(d[e], a.reduce_cast);
+            if (nan ? x != x : x == rm) first = e;
+          }
+          if (up) {
+            bo[tb] = om;
+            bi[tb] = (uint32_t)(v0 + tv * 32 + 8 * (first >> 2) + 4 * h + (first & 3));
+          }
+        }
+      }
+    }
+}
+
+// The blocks' final step: the lanes' best keys of each batch column, reduced
+// over the two lane halves and the vocabulary parts, stored per block.
+template <int VH, int NT>
+__device__ __forceinline__ void gemm_store_keys(const uint32_t (&bo)[2], const uint32_t (&bi)[2], int vi, int bj,
+                                                int h, int c32, unsigned long long (*kred)[kGemmBBRows],
+                                                unsigned long long* blk_keys) {
+  unsigned long long best[2];
+#pragma unroll
+  for (int tb = 0; tb < 2; ++tb) {
+    best[tb] = ((unsigned long long)bo[tb] << 32) | (unsigned long long)(~bi[tb]);
+    best[tb] = max_u64(best[tb], shfl_xor_u64(best[tb], 32));
+    if (h == 0) kred[vi][bj * 64 + tb * 32 + c32] = best[tb];
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < kGemmBBRows; b += NT) {
+    unsigned long long m = kred[0][b];
+#pragma unroll
+    for (int q = 1; q < VH; ++q) m = max_u64(m, kred[q][b]);
+    blk_keys[(size_t)blockIdx.x * kGemmBBRows + b] = m;
+  }
+}
+
 
 template <int MODE, int BV>
 __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a, unsigned long long* blk_keys) {
@@ -1236,52 +1309,9 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
       }
     }
   };
-  // D[vocab 8 (e >> 2) + 4 h + (e & 3)][batch c32] of tile (tv, tb), after
-  // the last stage of tile t.  Greedy: per (tile, lane) the maximum of the 16
-  // raw values (v_maximum3: NaN propagates), rounded; only where that beats
-  // the lane's running best is the first element rounding to it looked up.
-  // Rounding is monotone, so max(round(x)) = round(max(x)), and ties keep the
-  // lowest vocabulary row (rows ascend with e and with t).  Rows past V
-  // repeat row V - 1 (clamped loads) and lose its ties.
   uint32_t bo[2] = {0u, 0u}, bi[2] = {0u, 0u};  // running best: ordered value, row
   auto epilogue = [&](int t) NVJSEL_INLINE {
-    const int v0 = (blockIdx.x + t * gridDim.x) * BV + vi * 128;
-#pragma unroll
-    for (int tv = 0; tv < 4; ++tv)
-#pragma unroll
-      for (int tb = 0; tb < 2; ++tb) {
-        const f32x16_t& d = acc[tv][tb];
-        if constexpr (MODE == MODE_LOGITS) {
-          const int b = bj * 64 + tb * 32 + c32;
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int v = v0 + tv * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-            if (v < V && b < B) store_logit(a, b, v, apply_cast(d[e], a.reduce_cast));
-          }
-        } else {
-          float m = d[0];
-#pragma unroll
-          for (int e = 1; e < 15; e += 2)
-            m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, d[e]), d[e + 1]);
-          m = __builtin_elementwise_maximum(m, d[15]);
-          const float rm = apply_cast(m, a.reduce_cast);
-          const uint32_t om = ord_f32(rm);
-          const bool up = om > bo[tb];
-          if (__builtin_amdgcn_ballot_w64(up)) {
-            int first = 15;
-            const bool nan = rm != rm;
-#pragma unroll
-            for (int e = 14; e >= 0; --e) {
-              const float x = apply_cast(d[e], a.reduce_cast);
-              if (nan ? x != x : x == rm) first = e;
-            }
-            if (up) {
-              bo[tb] = om;
-              bi[tb] = (uint32_t)(v0 + tv * 32 + 8 * (first >> 2) + 4 * h + (first & 3));
-            }
-          }
-        }
-      }
+    gemm_epilogue<MODE>(a, acc, (blockIdx.x + t * gridDim.x) * BV + vi * 128, bj, h, c32, bo, bi);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -1321,21 +1351,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
     }
   }
   if constexpr (MODE == MODE_LOGITS) return;
-  // the two lane halves (vocab rows 4 h ..) of a column, then the vocabulary parts
-  unsigned long long best[2];
-#pragma unroll
-  for (int tb = 0; tb < 2; ++tb) {
-    best[tb] = ((unsigned long long)bo[tb] << 32) | (unsigned long long)(~bi[tb]);
-    best[tb] = max_u64(best[tb], shfl_xor_u64(best[tb], 32));
-    if (h == 0) kred[vi][bj * 64 + tb * 32 + c32] = best[tb];
-  }
-  __syncthreads();
-  for (int b = tid; b < kGemmBB; b += NT) {
-    unsigned long long m = kred[0][b];
-#pragma unroll
-    for (int h = 1; h < VH; ++h) m = max_u64(m, kred[h][b]);
-    blk_keys[(size_t)blockIdx.x * kGemmBB + b] = m;
-  }
+  gemm_store_keys<VH, NT>(bo, bi, vi, bj, h, c32, kred, blk_keys);
 }
 
 // Per row: the maximum of the blocks' keys -> id (and the winning logit);
