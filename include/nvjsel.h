@@ -61,12 +61,8 @@ int nvjsel_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* nvjsel_last_error(void);
 
-/* Workspace bytes for nvjsel_lm_head_top1 / nvjsel_lm_head_sample at `batch`.
- * For batch > 64 this includes 2 MiB of per-block keys that let greedy and
- * logits calls (bf16 x bf16 [V, H], H % 64 == 0) stream W once per 256 rows
- * through the blocked GEMM; a workspace of only the per-row keys and ticket
- * (8 * batch rounded up to 256, plus 256 bytes) is accepted too and takes
- * the 64-rows-per-pass tile kernel instead. */
+/* Workspace bytes for nvjsel_lm_head_top1 / nvjsel_lm_head_sample at `batch`
+ * (per-row keys and a ticket line). */
 size_t nvjsel_lm_head_workspace_size(int batch);
 
 /*

@@ -1131,9 +1131,10 @@ static int dispatch_tile(const LmArgs& a, hipStream_t s) {
 // LDS layout: 16-byte column q of row `row` at q * ROWS + (row ^ 2q): the 32
 // lanes of a fragment read hit 32 distinct slots of one 512 B window, and the
 // 8 lanes (2 rows x 4 columns) of a store phase hit 8 distinct bank groups.
-// Blocks keep, per batch row, a running best key; each block finally stores
-// its 256 keys and gemm_reduce_kernel takes the per-row maximum (no
-// same-address atomics).  MODE_LOGITS stores the rounded logits instead.
+// Blocks keep, per batch row, a running best key, fold it into the row's
+// maximum with one atomicMax per row, and the last block to finish writes the
+// ids (finish_rows; a reduce kernel over stored per-block keys cost ~7 us
+// more).  MODE_LOGITS stores the rounded logits instead.
 static constexpr int kGemmBBRows = 256;  // batch rows per blocked-GEMM pass
 static constexpr int kGemmBB = kGemmBBRows, kGemmKC = 32;
 
@@ -1187,11 +1188,13 @@ __device__ __forceinline__ void gemm_epilogue(const LmArgs& a, const f32x16_t (&
 }
 
 // The blocks' final step: the lanes' best keys of each batch column, reduced
-// over the two lane halves and the vocabulary parts, stored per block.
+// over the two lane halves and the vocabulary parts, folded into the rows'
+// running maxima (one atomicMax per block and row); the last block to finish
+// writes the ids and re-zeroes the keys (finish_rows).
 template <int VH, int NT>
-__device__ __forceinline__ void gemm_store_keys(const uint32_t (&bo)[2], const uint32_t (&bi)[2], int vi, int bj,
-                                                int h, int c32, unsigned long long (*kred)[kGemmBBRows],
-                                                unsigned long long* blk_keys) {
+__device__ __forceinline__ void gemm_finish_rows(const LmArgs& a, const uint32_t (&bo)[2], const uint32_t (&bi)[2],
+                                                 int vi, int bj, int h, int c32,
+                                                 unsigned long long (*kred)[kGemmBBRows]) {
   unsigned long long best[2];
 #pragma unroll
   for (int tb = 0; tb < 2; ++tb) {
@@ -1200,17 +1203,18 @@ __device__ __forceinline__ void gemm_store_keys(const uint32_t (&bo)[2], const u
     if (h == 0) kred[vi][bj * 64 + tb * 32 + c32] = best[tb];
   }
   __syncthreads();
-  for (int b = threadIdx.x; b < kGemmBBRows; b += NT) {
+  for (int b = threadIdx.x; b < a.B; b += NT) {
     unsigned long long m = kred[0][b];
 #pragma unroll
     for (int q = 1; q < VH; ++q) m = max_u64(m, kred[q][b]);
-    blk_keys[(size_t)blockIdx.x * kGemmBBRows + b] = m;
+    if (m) (void)after(atomicMax(&a.row_keys[b], m));
   }
+  finish_rows(a.row_keys, a.counter, a.B, a.out_ids, a.out_best);
 }
 
 
 template <int MODE, int BV>
-__global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a, unsigned long long* blk_keys) {
+__global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a) {
   constexpr int Q = kGemmKC / 8;  // 16-byte columns per row and stage
   constexpr int VH = BV / 128;  // 128-row vocabulary parts; 4 batch quarters each
   constexpr int NT = VH * 4 * 64;  // threads
@@ -1351,52 +1355,21 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
     }
   }
   if constexpr (MODE == MODE_LOGITS) return;
-  gemm_store_keys<VH, NT>(bo, bi, vi, bj, h, c32, kred, blk_keys);
+  gemm_finish_rows<VH, NT>(a, bo, bi, vi, bj, h, c32, kred);
 }
 
-// Per row: the maximum of the blocks' keys -> id (and the winning logit);
-// the keys read are cleared.  Block x handles 64 rows; its 4 waves stride
-// over the blocks' key rows, so every wave's reads are one contiguous 512 B.
-__global__ void __launch_bounds__(256) gemm_reduce_kernel(unsigned long long* __restrict__ blk_keys, int nblk,
-                                                          int B, int32_t* out_ids, float* out_best) {
-  __shared__ unsigned long long red[4][64];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int b = blockIdx.x * 64 + lane;
-  unsigned long long m = 0;
-  for (int i = w; i < nblk; i += 4) {
-    unsigned long long* p = blk_keys + (size_t)i * kGemmBB + b;
-    m = max_u64(m, *p);
-    *p = 0;  // the workspace is zero at rest
-  }
-  red[w][lane] = m;
-  __syncthreads();
-  if (w == 0 && b < B) {
-    m = max_u64(max_u64(red[0][lane], red[1][lane]), max_u64(red[2][lane], red[3][lane]));
-    out_ids[b] = (int32_t)(~(uint32_t)m);
-    if (out_best) out_best[b] = unord_f32((uint32_t)(m >> 32));
-  }
-}
 
 // vocabulary rows per block tile: 256 (8 waves, one block per CU; measured
 // 185 us at B = 256, V = 248320) or 128 (4 waves, two blocks per CU: 195 us)
 static constexpr int kGemmBV = 256;
 static constexpr int kGemmBpc = 256 / kGemmBV;  // blocks per CU of the blocked GEMM
-static constexpr int kGemmMaxBlocks = 1024;  // bounds the per-block key array
-static size_t gemm_keys_bytes() { return (size_t)kGemmMaxBlocks * kGemmBB * 8; }
-
 template <int MODE>
-static int launch_gemm(const LmArgs& a, unsigned long long* blk_keys, hipStream_t stream) {
+static int launch_gemm(const LmArgs& a, hipStream_t stream) {
   const int ntiles = (a.V + kGemmBV - 1) / kGemmBV;
   int grid = kGemmBpc * device_cu_count();
-  if (grid > kGemmMaxBlocks) grid = kGemmMaxBlocks;
   if (grid > ntiles) grid = ntiles;
-  hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a, blk_keys);
+  hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
   NVJSEL_CHECK_LAUNCH("lm_head_gemm_kernel");
-  if constexpr (MODE == MODE_GREEDY) {
-    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((a.B + 63) / 64), dim3(256), 0, stream, blk_keys, grid, a.B,
-                       a.out_ids, a.out_best);
-    NVJSEL_CHECK_LAUNCH("gemm_reduce_kernel");
-  }
   return NVJSEL_OK;
 }
 
@@ -1561,8 +1534,7 @@ static int dispatch_nb(const LmArgs& a, hipStream_t s) {
 
 static size_t lm_ws_keys_bytes(int batch) { return align_up((size_t)batch * 8, 256); }
 
-// The workspace every greedy/sample path needs: per-row keys and the ticket
-// line.  Batches past kGemmMinBatch add the blocked GEMM's per-block keys.
+// The workspace of every greedy/sample path: per-row keys and the ticket line.
 static size_t lm_ws_small_bytes(int batch) {
   return batch <= 0 ? 0 : lm_ws_keys_bytes(batch) + 256;
 }
@@ -1652,7 +1624,6 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     }
     if (!(pn.eps >= 0.0f)) { set_error("%s: eps must be >= 0", who); return NVJSEL_EINVAL; }
   }
-  // the blocked GEMM's key array is optional: without it the tile path runs
   const size_t need = mode == MODE_LOGITS ? 0 : lm_ws_small_bytes(batch) + (prenorm ? lm_prenorm_bytes(batch, H) : 0);
   if (need && (!workspace || ws_bytes < need)) {
     set_error("%s: workspace %zu bytes < required %zu", who, ws_bytes, need);
@@ -1690,11 +1661,8 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   }
   const bool tile = !gemv && bf16_mfma && H == 1024 && (prenorm || (((uintptr_t)hidden) & 15) == 0);
   // blocked GEMM: 64 < B, bf16 activations, one pass over W per 256 rows (greedy/logits)
-  const size_t gemm_off = lm_ws_small_bytes(batch) + (prenorm ? lm_prenorm_bytes(batch, H) : 0);
   const bool gemm = mode != MODE_SAMPLE && batch > kGemmMinBatch && bf16_mfma && (H % (2 * kGemmKC)) == 0 &&
-                    eff_dtype == NVJSEL_BF16 && (prenorm || (((uintptr_t)hidden) & 15) == 0) &&
-                    (mode == MODE_LOGITS || (workspace && ws_bytes >= gemm_off + gemm_keys_bytes()));
-  unsigned long long* gemm_keys = gemm && mode != MODE_LOGITS ? (unsigned long long*)((char*)workspace + gemm_off) : nullptr;
+                    eff_dtype == NVJSEL_BF16 && (prenorm || (((uintptr_t)hidden) & 15) == 0);
   const bool fused_prenorm = prenorm && !gemm && (gemv || tile);
   if (prenorm && !fused_prenorm) {
     LmArgs p{};
@@ -1748,7 +1716,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     a.out_stride = lo.stride;
     int rc;
     if (gemm) {
-      rc = mode == MODE_GREEDY ? launch_gemm<MODE_GREEDY>(a, gemm_keys, s) : launch_gemm<MODE_LOGITS>(a, nullptr, s);
+      rc = mode == MODE_GREEDY ? launch_gemm<MODE_GREEDY>(a, s) : launch_gemm<MODE_LOGITS>(a, s);
     } else if (gemv) {
       rc = by_mode([&](auto M) { return dispatch_gemv<decltype(M)::value>(a, s); });
     } else if (hv) {
@@ -1844,8 +1812,7 @@ extern "C" int nvjsel_lm_head_top1_noalloc(const void* hidden, int hidden_dtype,
 }
 
 extern "C" size_t nvjsel_lm_head_workspace_size(int batch) {
-  if (batch <= 0) return 0;
-  return lm_ws_small_bytes(batch) + (batch > kGemmMinBatch ? gemm_keys_bytes() : 0);
+  return lm_ws_small_bytes(batch);
 }
 
 extern "C" int nvjsel_lm_head_top1(const void* hidden, int hidden_dtype, const void* weight,
