@@ -53,6 +53,7 @@ __device__ __forceinline__ T stream_load(const T* p) {
 }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -636,8 +637,13 @@ __global__ void __launch_bounds__(kGemvWaves * 64) lm_head_gemv_kernel(LmArgs a)
 // KU rows are in flight per wave; acc[b][c] += h[b][k] * W[k][col + c] in
 // fp32, with h broadcast from LDS.  The slices' partial sums meet in LDS,
 // summed in slice order, and each thread then scores two columns of every row.
-template <int NB, int WAVES, int MODE>
+template <int NB, int WAVES, int MODE, bool DOTP>
 __global__ void __launch_bounds__(WAVES * 64) lm_head_hv_kernel(LmArgs a) {
+  // DOT (bf16 hidden, a k-slice of even length): the hidden sits in LDS as
+  // bf16 pairs (k, k+1) and each pair of W rows is packed per column with
+  // v_perm, so one v_dot2c_f32_bf16 does two multiply-adds (products exact,
+  // fp32 sums): half the VALU work per weight element
+  constexpr bool DOT = DOTP;
   constexpr int KU = 4;
   constexpr int DEPTH = NB <= 2 ? 6 : 4;
   constexpr int STRIP = 512;
@@ -647,9 +653,18 @@ __global__ void __launch_bounds__(WAVES * 64) lm_head_hv_kernel(LmArgs a) {
   const int H = a.H, V = a.V, B = a.B;
   const int vb = blockIdx.x * STRIP;
   const int col = min(vb + lane * 8, V - 8);  // clamped loads past the row end (V % 8 == 0)
-  for (int i = threadIdx.x; i < H * NB; i += WAVES * 64) {
-    const int k = i / NB, b = i - k * NB;
-    lds_f[i] = b < B ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * H + k) : 0.0f;
+  if constexpr (DOT) {
+    uint32_t* lds_p = (uint32_t*)lds_f;  // [H / 2][NB] bf16 pairs
+    const uint16_t* hs = (const uint16_t*)a.hidden;
+    for (int i = threadIdx.x; i < (H / 2) * NB; i += WAVES * 64) {
+      const int kp = i / NB, b = i - kp * NB;
+      lds_p[i] = b < B ? ((uint32_t)hs[(size_t)b * H + 2 * kp] | ((uint32_t)hs[(size_t)b * H + 2 * kp + 1] << 16)) : 0u;
+    }
+  } else {
+    for (int i = threadIdx.x; i < H * NB; i += WAVES * 64) {
+      const int k = i / NB, b = i - k * NB;
+      lds_f[i] = b < B ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * H + k) : 0.0f;
+    }
   }
   float tp[NB];
   bool greedy_row[NB];
@@ -685,6 +700,30 @@ __global__ void __launch_bounds__(WAVES * 64) lm_head_hv_kernel(LmArgs a) {
         __builtin_amdgcn_sched_barrier(0);
       },
       [&](auto S, int i) NVJSEL_INLINE {
+        if constexpr (DOT) {
+#pragma unroll
+          for (int u = 0; u < KU; u += 2) {
+            const int k = k0 + i * KU + u;
+            if (k >= k1) continue;  // wave-uniform; the slice length is even
+            const u32x4_t w0 = ring[decltype(S)::value][u], w1 = ring[decltype(S)::value][u + 1];
+            const uint32_t q0[4] = {w0.x, w0.y, w0.z, w0.w}, q1[4] = {w1.x, w1.y, w1.z, w1.w};
+            uint32_t wp[8];  // column c: (W[k][c], W[k+1][c]) as a bf16 pair
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              wp[2 * e] = __builtin_amdgcn_perm(q1[e], q0[e], 0x05040100u);
+              wp[2 * e + 1] = __builtin_amdgcn_perm(q1[e], q0[e], 0x07060302u);
+            }
+            const uint32_t* hk = (const uint32_t*)lds_f + (k >> 1) * NB;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+              const bf16x2_t h = __builtin_bit_cast(bf16x2_t, hk[b]);
+#pragma unroll
+              for (int c = 0; c < 8; ++c)
+                acc[b][c] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wp[c]), h, acc[b][c], false);
+            }
+          }
+          return;
+        }
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
           const int k = k0 + i * KU + u;
@@ -1551,6 +1590,8 @@ struct Prenorm {
 
 static size_t lm_prenorm_bytes(int batch, int H) { return align_up((size_t)batch * H * 4, 256); }
 
+static constexpr bool kHvDot = true;  // bf16 hidden, B >= 2: the v_dot2c_f32_bf16 path
+
 // Dynamic LDS of lm_head_hv_kernel with NB rows: the hidden [H][NB] f32, then
 // the partial sums [WAVES][NB][512] f32 (the same bytes, reused).
 static size_t hv_lds_bytes(int nb, int H) {
@@ -1570,7 +1611,8 @@ struct LogitsOut {
 template <int NB, int MODE>
 static int launch_hv(const LmArgs& a, hipStream_t stream) {
   constexpr int WAVES = 4;  // measured: 4 waves per block beat 8 and 16 at B = 1 and 8
-  auto kern = lm_head_hv_kernel<NB, WAVES, MODE>;
+  const bool dot = kHvDot && NB >= 2 && a.hidden_dtype == DT_BF16 && (a.H % (2 * WAVES)) == 0;
+  auto kern = dot ? lm_head_hv_kernel<NB, WAVES, MODE, NB >= 2> : lm_head_hv_kernel<NB, WAVES, MODE, false>;
   const size_t lds = hv_lds_bytes(NB, a.H);
   if (lds > 48 * 1024)
     NVJSEL_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
