@@ -43,6 +43,7 @@ static constexpr int kGemvDepth = 3;  // row groups in flight per wave (measured
 static constexpr int kGemvBpc = 1;  // blocks per CU for the streaming GEMV (0 = occupancy)
 static constexpr int kTileQcap = 768;  // queue entries per epilogue wave (sample mode)
 static constexpr int kGemvR = 4;  // rows per wave step of the streaming GEMV
+static constexpr bool kGemvDot = true;  // bf16 hidden without prologue: v_dot2c_f32_bf16
 
 namespace nvjsel {
 
@@ -443,20 +444,33 @@ lm_head_mfma_kernel(LmArgs a) {
 // registers, then a butterfly transpose-reduction leaves each group of 64/R
 // lanes with the full dot of one row (log2(64) shuffle rounds, halving the
 // values carried at each of the first log2(R) rounds).
-template <int NB, int R, int KJ, int MODE>
+template <int NB, int R, int KJ, int MODE, bool DOT>
 __global__ void __launch_bounds__(kGemvWaves * 64) lm_head_gemv_kernel(LmArgs a) {
+  // DOT (bf16 activations): the hidden is held as bf16 pairs (k, k+1) --
+  // the pairs of each 32-bit word of W too -- so one v_dot2c_f32_bf16
+  // (exact products, fp32 sums) replaces two convert-and-FMA steps.  Without
+  // the prologue the pairs are the hidden's own words; with it they are
+  // packed from the normalised rows (already rounded to bf16)
   constexpr int WAVES = kGemvWaves;
   __shared__ unsigned long long red[WAVES * NB];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int H = KJ * 512, V = a.V, B = a.B;
   float hv[NB][KJ][8];
+  uint32_t hp[NB][KJ][DOT ? 4 : 1];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int j = 0; j < KJ; ++j)
+    for (int j = 0; j < KJ; ++j) {
+      if (DOT && !a.prenorm) {
+        const u32x4_t v = b < B ? *((const u32x4_t*)((const uint16_t*)a.hidden + (size_t)b * H + j * 512) + lane)
+                                : u32x4_t{0u, 0u, 0u, 0u};
+        hp[b][j][0] = v.x; hp[b][j][1] = v.y; hp[b][j][2] = v.z; hp[b][j][3] = v.w;
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        hv[b][j][e] = (b < B) ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * H + j * 512 + lane * 8 + e) : 0.0f;
+        for (int e = 0; e < 8; ++e)
+          hv[b][j][e] = (b < B) ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * H + j * 512 + lane * 8 + e) : 0.0f;
+      }
+    }
   // RMSNorm prologue: its operands are requested with the hidden, and it runs
   // once the first weight groups are in flight (finish_prenorm below)
   float nwv[KJ][8] = {};
@@ -467,23 +481,32 @@ __global__ void __launch_bounds__(kGemvWaves * 64) lm_head_gemv_kernel(LmArgs a)
       for (int e = 0; e < 8; ++e) nwv[j][e] = load_as_f32(a.norm_w, a.norm_dtype, j * 512 + lane * 8 + e);
   }
   auto finish_prenorm = [&]() NVJSEL_INLINE {
-    if (!a.prenorm) return;
-    // the wave holds whole rows: per-lane sum of squares, then the butterfly
-    // leaves the same total in every lane (and every wave)
+    {
+      if (!a.prenorm) return;
+      // the wave holds whole rows: per-lane sum of squares, then the butterfly
+      // leaves the same total in every lane (and every wave)
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      float ss = 0.0f;
+      for (int b = 0; b < NB; ++b) {
+        float ss = 0.0f;
 #pragma unroll
-      for (int j = 0; j < KJ; ++j)
+        for (int j = 0; j < KJ; ++j)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ss = fmaf(hv[b][j][e], hv[b][j][e], ss);
+          for (int e = 0; e < 8; ++e) ss = fmaf(hv[b][j][e], hv[b][j][e], ss);
 #pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-      const float inv = prenorm_inv(a, ss);
+        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        const float inv = prenorm_inv(a, ss);
 #pragma unroll
-      for (int j = 0; j < KJ; ++j)
+        for (int j = 0; j < KJ; ++j)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) hv[b][j][e] = prenorm_apply_w(a, hv[b][j][e], inv, nwv[j][e]);
+          for (int e = 0; e < 8; ++e) hv[b][j][e] = prenorm_apply_w(a, hv[b][j][e], inv, nwv[j][e]);
+        if constexpr (DOT) {
+#pragma unroll
+          for (int j = 0; j < KJ; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              hp[b][j][e] = (__float_as_uint(hv[b][j][2 * e]) >> 16) | (__float_as_uint(hv[b][j][2 * e + 1]) & 0xFFFF0000u);
+        }
+      }
     }
   };
 
@@ -537,8 +560,13 @@ __global__ void __launch_bounds__(kGemvWaves * 64) lm_head_gemv_kernel(LmArgs a)
           const uint32_t q[4] = {w[r][j].x, w[r][j].y, w[r][j].z, w[r][j].w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            acc = fmaf(__uint_as_float(q[e] << 16), hv[b][j][2 * e], acc);
-            acc = fmaf(__uint_as_float(q[e] & 0xFFFF0000u), hv[b][j][2 * e + 1], acc);
+            if constexpr (DOT) {
+              acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, q[e]),
+                                                    __builtin_bit_cast(bf16x2_t, hp[b][j][e]), acc, false);
+            } else {
+              acc = fmaf(__uint_as_float(q[e] << 16), hv[b][j][2 * e], acc);
+              acc = fmaf(__uint_as_float(q[e] & 0xFFFF0000u), hv[b][j][2 * e + 1], acc);
+            }
           }
         }
         p[b][r] = acc;
@@ -1531,7 +1559,9 @@ static int launch_mfma(const LmArgs& a, hipStream_t stream) {
 template <int NB, int KJ, int MODE>
 static int launch_gemv(const LmArgs& a, hipStream_t stream) {
   constexpr int R = kGemvR;
-  auto kern = lm_head_gemv_kernel<NB, R, KJ, MODE>;
+  const bool dot = kGemvDot && (a.prenorm ? a.act_dtype == DT_BF16
+                                           : a.hidden_dtype == DT_BF16 && (((uintptr_t)a.hidden) & 15) == 0);
+  auto kern = dot ? lm_head_gemv_kernel<NB, R, KJ, MODE, true> : lm_head_gemv_kernel<NB, R, KJ, MODE, false>;
   int per_cu = 0;
   constexpr int WAVES = kGemvWaves;
   NVJSEL_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, WAVES * 64, 0));
