@@ -1620,7 +1620,7 @@ struct Prenorm {
 
 static size_t lm_prenorm_bytes(int batch, int H) { return align_up((size_t)batch * H * 4, 256); }
 
-static constexpr bool kHvDot = true;  // bf16 hidden, B >= 2: the v_dot2c_f32_bf16 path
+static constexpr bool kHvDot = true;  // bf16 hidden: the v_dot2c_f32_bf16 path
 
 // Dynamic LDS of lm_head_hv_kernel with NB rows: the hidden [H][NB] f32, then
 // the partial sums [WAVES][NB][512] f32 (the same bytes, reused).
@@ -1641,8 +1641,8 @@ struct LogitsOut {
 template <int NB, int MODE>
 static int launch_hv(const LmArgs& a, hipStream_t stream) {
   constexpr int WAVES = 4;  // measured: 4 waves per block beat 8 and 16 at B = 1 and 8
-  const bool dot = kHvDot && NB >= 2 && a.hidden_dtype == DT_BF16 && (a.H % (2 * WAVES)) == 0;
-  auto kern = dot ? lm_head_hv_kernel<NB, WAVES, MODE, NB >= 2> : lm_head_hv_kernel<NB, WAVES, MODE, false>;
+  const bool dot = kHvDot && a.hidden_dtype == DT_BF16 && (a.H % (2 * WAVES)) == 0;
+  auto kern = dot ? lm_head_hv_kernel<NB, WAVES, MODE, true> : lm_head_hv_kernel<NB, WAVES, MODE, false>;
   const size_t lds = hv_lds_bytes(NB, a.H);
   if (lds > 48 * 1024)
     NVJSEL_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
