@@ -1828,8 +1828,10 @@ __device__ __forceinline__ void gumbel_item(const SampleArgs& a, uint32_t item, 
 
 // The queued item quarters, grid-stride: a grid of one round of resident
 // blocks (dispatching a block that exits at once still costs the dispatcher).
+// Registers capped for 7 waves per SIMD (95 -> 71 VGPRs, no spill; same-box
+// C5 90.5 -> 88.5 us, 6 waves 89 us).
 template <int DT, int VEC>
-__global__ void __launch_bounds__(kThreads) sample_gumbel_kernel(SampleArgs a) {
+__global__ void __launch_bounds__(kThreads, 7) sample_gumbel_kernel(SampleArgs a) {
   __shared__ GumbelShared sh;
   const uint32_t split = (uint32_t)(a.chunk / kGumbelSub);
   const uint32_t n = a.list_n[0] * split;
