@@ -39,7 +39,7 @@ static constexpr int kLmDepth = 3;  // k-chunks of W in flight per wave
 static constexpr int kLmBpc = 0;  // blocks per CU (0 = as many as occupancy allows)
 
 static constexpr int kGemvWaves = 4;  // waves per block of the streaming GEMV
-static constexpr int kGemvDepth = 3;  // row groups in flight per wave (measured: 3 > 4, 5 > 2)
+static constexpr int kGemvDepth = 2;  // row groups in flight per wave (measured on the dot2 path: 2 > 3 > 4)
 static constexpr int kGemvBpc = 1;  // blocks per CU for the streaming GEMV (0 = occupancy)
 static constexpr int kTileQcap = 768;  // queue entries per epilogue wave (sample mode)
 static constexpr int kGemvR = 4;  // rows per wave step of the streaming GEMV
