@@ -36,10 +36,10 @@ for _p in (ROOT, os.path.join(ROOT, "nano-vllm-jax_amd")):
 HBM_PEAK = 8.0e12  # bytes/s, MI355X
 MALL_BYTES = 256 * 1024 * 1024
 V_FULL, H_FULL = 248320, 1024
-ALL_CONFIGS = "c1,c2,c3,c4,c5,x1,x2,x3,x4,x5,x6"
+ALL_CONFIGS = "c1,c2,c3,c4,c5,x1,x2,x3,x4,x5,x6,x7"
 # per-config generator seeds: each config's inputs depend only on its own seed
 SEEDS = {"c1": 101, "c2": 102, "c3": 103, "c4": 104, "c5": 105, "x1": 201, "x2": 202, "x3": 203, "x4": 204,
-         "x5": 205, "x6": 206}
+         "x5": 205, "x6": 206, "x7": 207}
 
 
 def _parse():
@@ -157,8 +157,8 @@ def make_inputs(torch, name, dev):
         else:
             d["k"] = 50
         return d
-    if name == "c4":
-        B = 64
+    if name in ("c4", "x7"):
+        B = 64 if name == "c4" else 256
         return {"batch": B, "hidden": torch.randn(B, H_FULL, device=dev, generator=gen).to(torch.bfloat16),
                 "temperature": torch.ones(B, device=dev), "keys": _engine_keys(torch, B, dev)}
     if name == "c5":
@@ -259,9 +259,11 @@ def build_configs(torch, which, with_cpu):
         cfgs.append(sampler_cfg("c3_topk_topp_b64", make_inputs(torch, "c3", dev), "sample_scan_kernel",
                                 "top-k=50 / top-p=0.9 / T=0.8, f32 logits [64,248320] Zipf(1.1)"))
 
-    if "c4" in which:
+    for name in ("c4", "x7"):
+        if name not in which:
+            continue
         Ws = weights()
-        d = make_inputs(torch, "c4", dev)
+        d = make_inputs(torch, name, dev)
         B, h, t, keys = d["batch"], d["hidden"], d["temperature"], d["keys"]
         out = torch.empty(B, dtype=torch.int32, device=dev)
         w = ws(lib.nvjsel_lm_head_workspace_size(B))
@@ -271,9 +273,14 @@ def build_configs(torch, which, with_cpu):
                                          t.data_ptr(), keys.data_ptr(), out.data_ptr(), w.data_ptr(),
                                          w.numel(), stream()))
 
-        cfgs.append(Cfg("c4_fused_lm_head_gumbel_b64", B, V_FULL * H_FULL * 2 + B * H_FULL * 2, launch, 2,
-                        "lm_head_tile_kernel", "fused LM-head + Gumbel-max, B=64, T=1",
-                        (lambda secs, h=h, d=d: cpu_lm_head(h, d, secs)) if with_cpu else None))
+        if name == "c4":
+            cfgs.append(Cfg("c4_fused_lm_head_gumbel_b64", B, V_FULL * H_FULL * 2 + B * H_FULL * 2, launch, 2,
+                            "lm_head_tile_kernel", "fused LM-head + Gumbel-max, B=64, T=1",
+                            (lambda secs, h=h, d=d: cpu_lm_head(h, d, secs)) if with_cpu else None))
+        else:
+            cfgs.append(Cfg("x7_gemm_fused_gumbel_b256", B, V_FULL * H_FULL * 2 + B * H_FULL * 2, launch, 2,
+                            "lm_head_gemm_kernel",
+                            "fused LM-head + Gumbel-max, B=256, T=1 (one W pass, blocked GEMM)"))
 
     if "c5" in which:
         cfgs.append(sampler_cfg("c5_mixed_b256_bf16", make_inputs(torch, "c5", dev), "sample_scan_kernel",

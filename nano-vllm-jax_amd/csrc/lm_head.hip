@@ -1204,6 +1204,7 @@ static int dispatch_tile(const LmArgs& a, hipStream_t s) {
 // more).  MODE_LOGITS stores the rounded logits instead.
 static constexpr int kGemmBBRows = 256;  // batch rows per blocked-GEMM pass
 static constexpr int kGemmBB = kGemmBBRows, kGemmKC = 32;
+static constexpr int kGemmQcap = 768;  // queue entries per wave (sample mode; LDS: 12 B each)
 
 // Epilogue of one block tile of the blocked GEMM for the wave's 128 x 64
 // sub-tile: D[vocab 8 (e >> 2) + 4 h + (e & 3)][batch c32] of 32 x 32 tile
@@ -1259,13 +1260,10 @@ __device__ __forceinline__ void gemm_epilogue(const LmArgs& a, const f32x16_t (&
 // running maxima (one atomicMax per block and row); the last block to finish
 // writes the ids and re-zeroes the keys (finish_rows).
 template <int VH, int NT>
-__device__ __forceinline__ void gemm_finish_rows(const LmArgs& a, const uint32_t (&bo)[2], const uint32_t (&bi)[2],
-                                                 int vi, int bj, int h, int c32,
-                                                 unsigned long long (*kred)[kGemmBBRows]) {
-  unsigned long long best[2];
+__device__ __forceinline__ void gemm_finish_rows(const LmArgs& a, unsigned long long (&best)[2], int vi, int bj,
+                                                 int h, int c32, unsigned long long (*kred)[kGemmBBRows]) {
 #pragma unroll
   for (int tb = 0; tb < 2; ++tb) {
-    best[tb] = ((unsigned long long)bo[tb] << 32) | (unsigned long long)(~bi[tb]);
     best[tb] = max_u64(best[tb], shfl_xor_u64(best[tb], 32));
     if (h == 0) kred[vi][bj * 64 + tb * 32 + c32] = best[tb];
   }
@@ -1290,6 +1288,16 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   __shared__ u32x4_t As[2][Q * BV];
   __shared__ u32x4_t Bs[2][Q * kGemmBB];
   __shared__ unsigned long long kred[VH][kGemmBB];
+  // sample mode: per-wave queue of entries that may be their row's maximum
+  // (scaled logit, approximate score, vocab << 7 | tb << 6 | lane) and the
+  // exact best key of each (lane, tb) row slot
+  constexpr bool SMP = MODE == MODE_SAMPLE;
+  constexpr int NW = NT / 64;
+  constexpr int QC = SMP ? kGemmQcap : 1;
+  __shared__ float gqx[SMP ? NW : 1][QC];
+  __shared__ float gqa[SMP ? NW : 1][QC];
+  __shared__ uint32_t gqv[SMP ? NW : 1][QC];
+  __shared__ unsigned long long gqbest[SMP ? NW : 1][SMP ? 128 : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int vi = wave % VH, bj = wave / VH;
   const int B = a.B, V = a.V, H = a.H;
@@ -1381,8 +1389,135 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
     }
   };
   uint32_t bo[2] = {0u, 0u}, bi[2] = {0u, 0u};  // running best: ordered value, row
+  // sample mode: the lane's two batch rows bj * 64 + tb * 32 + c32
+  float tp[2] = {1.0f, 1.0f}, amax[2] = {-INFINITY, -INFINITY};
+  bool greedy_row[2] = {true, true}, unit_tp[2] = {true, true};
+  TfKey key[2] = {tf_key(0u, 0u), tf_key(0u, 0u)};
+  unsigned long long sbest[2] = {0ull, 0ull};
+  uint32_t qcount = 0;  // wave-uniform
+  if constexpr (SMP) {
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      const int b = bj * 64 + tb * 32 + c32;
+      const float t = b < B ? a.temperature[b] : 0.0f;
+      greedy_row[tb] = (t <= 0.0f);
+      tp[tb] = temp_floor(t);
+      unit_tp[tb] = (tp[tb] == 1.0f);  // x / 1 == x exactly
+      if (b < B) key[tb] = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+      gqbest[wave][tb * 64 + lane] = 0ull;
+    }
+  }
+  // drops queued entries that can no longer be their row's maximum (the test
+  // each passed when queued, against the row slot's maximum, which has only
+  // grown since); compaction in place, a 64-entry group read before any
+  // survivor is written at or below it
+  auto gcompact = [&]() NVJSEL_INLINE {
+    uint32_t nk = 0;
+    for (uint32_t e0 = 0; e0 < qcount; e0 += 64) {  // wave-uniform trip count
+      const uint32_t e = e0 + lane;
+      const bool live = e < qcount;
+      const float x = live ? gqx[wave][e] : 0.0f;
+      const float ap = live ? gqa[wave][e] : -INFINITY;
+      const uint32_t pv = live ? gqv[wave][e] : 0u;
+      const int sl = (int)(pv & 63u);
+      const float a0 = __shfl(amax[0], sl, 64), a1 = __shfl(amax[1], sl, 64);
+      const float am = (pv & 64u) ? a1 : a0;
+      const float slack = 2e-4f + 4.8e-7f * (fminf(fabsf(ap), 1e30f) + fminf(fabsf(am), 1e30f));
+      const bool keep = live && !(ap + slack < am);
+      const unsigned long long m = __ballot(keep);
+      if (keep) {
+        const uint32_t slot = nk + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        gqx[wave][slot] = x;
+        gqa[wave][slot] = ap;
+        gqv[wave][slot] = pv;
+      }
+      nk += (uint32_t)__popcll(m);
+    }
+    qcount = nk;
+  };
+  // exact scores (fp64 logs) of the queued entries, a full wave at a time,
+  // folded into the row slots' exact best keys
+  auto gflush = [&]() NVJSEL_INLINE {
+    for (uint32_t e0 = 0; e0 < qcount; e0 += 64) {  // wave-uniform trip count
+      const uint32_t e = e0 + lane;
+      const bool live = e < qcount;
+      const uint32_t pv = live ? gqv[wave][e] : 0u;
+      const int sl = (int)(pv & 63u);
+      const bool t1 = (pv & 64u) != 0u;
+      // the shuffles run with the whole wave active
+      uint32_t kw[2][3];
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        kw[tb][0] = (uint32_t)__shfl((int)key[tb].k0, sl, 64);
+        kw[tb][1] = (uint32_t)__shfl((int)key[tb].k1, sl, 64);
+        kw[tb][2] = (uint32_t)__shfl((int)key[tb].k2, sl, 64);
+      }
+      const TfKey k2{t1 ? kw[1][0] : kw[0][0], t1 ? kw[1][1] : kw[0][1], t1 ? kw[1][2] : kw[0][2]};
+      const uint32_t v = pv >> 7;
+      if (live) atomicMax(&gqbest[wave][pv & 127u], argmax_key(gqx[wave][e] + gumbel_at(k2, v), v));
+    }
+    qcount = 0;
+  };
+  // one tile of the sample epilogue: runs of 2 consecutive vocabulary rows
+  // (D elements 2 qq, 2 qq + 1: rows v0 + tv * 32 + 8 (qq >> 1) + 4 h +
+  // 2 (qq & 1) + j) scored with the hardware log; entries that can still be
+  // the row's maximum queue.  Two Threefry chains per run and a runtime loop
+  // over the four vocabulary sub-tiles (acc[0] is scored, then the tiles
+  // shift down) keep the 128 accumulators, the loads in flight and the
+  // draws within the register file, and the loop body within the
+  // instruction cache.
+  auto sample_epilogue = [&](int v0) NVJSEL_INLINE {
+    // the two lane halves hold the same batch rows: share their maxima
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) amax[tb] = fmaxf(amax[tb], __shfl_xor(amax[tb], 32, 64));
+#pragma unroll 1
+    for (int tv = 0; tv < 4; ++tv) {
+#pragma unroll
+      for (int qq = 0; qq < 8; ++qq)
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+          if (qcount > (uint32_t)(QC - 128)) {  // room for one run of the wave
+            gcompact();
+            if (qcount > (uint32_t)(QC - 128)) gflush();
+          }
+          const int b = bj * 64 + tb * 32 + c32;
+          const int vs = v0 + tv * 32 + 8 * (qq >> 1) + 4 * h + 2 * (qq & 1);
+          bool q[2] = {false, false};
+          float xq[2], aq[2];
+          if (b < B) {
+            const float raw[2] = {acc[0][tb][2 * qq], acc[0][tb][2 * qq + 1]};
+            score_run<MODE_SAMPLE, 2>(raw, vs, V, a.reduce_cast, greedy_row[tb], unit_tp[tb], tp[tb], key[tb],
+                                      amax[tb], sbest[tb], q, xq, aq);
+          }
+          // queue the marked entries with the whole wave active: slots from a ballot
+          if (__any(q[0] | q[1])) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const unsigned long long m = __ballot(q[j]);
+              if (q[j]) {
+                const uint32_t slot = qcount + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                gqx[wave][slot] = xq[j];
+                gqa[wave][slot] = aq[j];
+                gqv[wave][slot] = ((uint32_t)(vs + j) << 7) | ((uint32_t)tb << 6) | (uint32_t)lane;
+              }
+              qcount += (uint32_t)__popcll(m);
+            }
+          }
+        }
+#pragma unroll
+      for (int t = 0; t < 3; ++t)
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) acc[t][tb] = acc[t + 1][tb];
+    }
+  };
   auto epilogue = [&](int t) NVJSEL_INLINE {
-    gemm_epilogue<MODE>(a, acc, (blockIdx.x + t * gridDim.x) * BV + vi * 128, bj, h, c32, bo, bi);
+    const int v0 = (blockIdx.x + t * gridDim.x) * BV + vi * 128;
+    if constexpr (SMP)
+      sample_epilogue(v0);
+    else
+      gemm_epilogue<MODE>(a, acc, v0, bj, h, c32, bo, bi);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -1422,7 +1557,17 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
     }
   }
   if constexpr (MODE == MODE_LOGITS) return;
-  gemm_finish_rows<VH, NT>(a, bo, bi, vi, bj, h, c32, kred);
+  unsigned long long best[2];
+  if constexpr (SMP) {
+    gcompact();
+    gflush();
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) best[tb] = greedy_row[tb] ? sbest[tb] : max_u64(sbest[tb], gqbest[wave][tb * 64 + lane]);
+  } else {
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) best[tb] = ((unsigned long long)bo[tb] << 32) | (unsigned long long)(~bi[tb]);
+  }
+  gemm_finish_rows<VH, NT>(a, best, vi, bj, h, c32, kred);
 }
 
 
@@ -1732,9 +1877,11 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     chunk = tiles * 16;
   }
   const bool tile = !gemv && bf16_mfma && H == 1024 && (prenorm || (((uintptr_t)hidden) & 15) == 0);
-  // blocked GEMM: 64 < B, bf16 activations, one pass over W per 256 rows (greedy/logits)
-  const bool gemm = mode != MODE_SAMPLE && batch > kGemmMinBatch && bf16_mfma && (H % (2 * kGemmKC)) == 0 &&
-                    eff_dtype == NVJSEL_BF16 && (prenorm || (((uintptr_t)hidden) & 15) == 0);
+  // blocked GEMM: 64 < B, bf16 activations, one pass over W per 256 rows (greedy, logits and Gumbel sampling)
+  // (sample mode packs vocabulary ids into 25 bits of its queue entries)
+  const bool gemm = batch > kGemmMinBatch && bf16_mfma && (H % (2 * kGemmKC)) == 0 &&
+                    eff_dtype == NVJSEL_BF16 && (prenorm || (((uintptr_t)hidden) & 15) == 0) &&
+                    (mode != MODE_SAMPLE || V < (1 << 25));
   const bool fused_prenorm = prenorm && !gemm && (gemv || tile);
   if (prenorm && !fused_prenorm) {
     LmArgs p{};
@@ -1788,7 +1935,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     a.out_stride = lo.stride;
     int rc;
     if (gemm) {
-      rc = mode == MODE_GREEDY ? launch_gemm<MODE_GREEDY>(a, s) : launch_gemm<MODE_LOGITS>(a, s);
+      rc = by_mode([&](auto M) { return launch_gemm<decltype(M)::value>(a, s); });
     } else if (gemv) {
       rc = by_mode([&](auto M) { return dispatch_gemv<decltype(M)::value>(a, s); });
     } else if (hv) {

@@ -274,3 +274,69 @@ def test_gemm_full_vocab_b256_with_prenorm():
     torch.cuda.synchronize()
     xin = sel.lm_head_input(x, nw, 1e-6, hidden_dtype="bf16", act_dtype="bf16")
     check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(xin, W), 1, "gemm B=256 prenorm")
+
+
+@pytest.mark.parametrize("B,H", [(65, 512), (130, 1024), (256, 1024)])
+def test_gemm_sample_mixed_temperatures(B, H):
+    """Fused Gumbel sampling through the blocked GEMM (64 < B <= 256): greedy
+    rows (T = 0) beside temperature rows, a vocabulary that is not a multiple
+    of the 256-row tile, against the oracle's scores s_v = rnd(z_v)/T + g_v."""
+    rng = np.random.default_rng(9100 + B + H)
+    V = 20011
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    h = _hidden(rng, B, H, torch.bfloat16)
+    T = [float(x) for x in rng.choice([0.0, 0.5, 1.0, 1.7], B)]
+    keys = engine_keys(B, 31 + B)
+    ids = nvjsel.lm_head_sample_token_ids(h, W, temperatures=torch.tensor(T).cuda(),
+                                          rng_keys=keys_tensor(keys), weight_layout="vh")
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(h.float().cpu().numpy(), W.float().cpu().numpy())
+    namb = check_fused_sampled(ids.cpu().numpy(), z, T, keys, 1, f"gemm sample B={B} H={H}")
+    assert namb <= max(1, B // 16)
+    # a second call on the same inputs draws the same ids
+    ids2 = nvjsel.lm_head_sample_token_ids(h, W, temperatures=torch.tensor(T).cuda(),
+                                           rng_keys=keys_tensor(keys), weight_layout="vh")
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ids2)
+
+
+def test_gemm_sample_nan_rows_fill_queue():
+    """NaN hidden rows score +inf everywhere, so every one of their entries
+    stays a candidate: the per-wave candidate queue of the GEMM's sample
+    epilogue fills, is compacted and rescored exactly mid-tile many times.
+    Those rows take index 0 (first NaN wins); the finite rows stay exact."""
+    rng = np.random.default_rng(9300)
+    B, H, V = 200, 1024, 30011
+    hn = rng.standard_normal((B, H))
+    nan_rows = [0, 33, 64, 127, 199]
+    for b in nan_rows:
+        hn[b, 5] = np.nan
+    h = bf16_tensor(hn)
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    T = [1.0] * B
+    keys = engine_keys(B, 47)
+    ids = nvjsel.lm_head_sample_token_ids(h, W, temperatures=torch.tensor(T).cuda(),
+                                          rng_keys=keys_tensor(keys), weight_layout="vh")
+    torch.cuda.synchronize()
+    got = ids.cpu().numpy()
+    assert [int(got[b]) for b in nan_rows] == [0] * len(nan_rows)
+    z = sel.lm_head_logits(as_f32(h), as_f32(W))
+    namb = check_fused_sampled(got, z, T, keys, 1, "gemm sample NaN rows")
+    assert namb <= max(1, B // 16)
+
+
+def test_gemm_sample_bench_workload_b256():
+    """The timed x7 workload (fused LM-head + Gumbel, B = 256, V = 248320,
+    T = 1, engine keys), built as the bench builds it, against the oracle."""
+    import bench
+
+    dev = torch.device("cuda:0")
+    W = bench.lm_weight(torch, dev)
+    d = bench.make_inputs(torch, "x7", dev)
+    B, h, t, kt = d["batch"], d["hidden"], d["temperature"], d["keys"]
+    ids = nvjsel.lm_head_sample_token_ids(h, W, temperatures=t, rng_keys=kt, weight_layout="vh")
+    torch.cuda.synchronize()
+    keys = [tuple(int(x) & 0xFFFFFFFF for x in row) for row in kt.cpu().numpy().reshape(B, 2)]
+    z = sel.lm_head_logits(as_f32(h), as_f32(W))
+    namb = check_fused_sampled(ids.cpu().numpy(), z, t.cpu().numpy().tolist(), keys, 1, "x7 B=256")
+    assert namb <= 8
