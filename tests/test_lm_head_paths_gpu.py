@@ -340,3 +340,21 @@ def test_gemm_sample_bench_workload_b256():
     z = sel.lm_head_logits(as_f32(h), as_f32(W))
     namb = check_fused_sampled(ids.cpu().numpy(), z, t.cpu().numpy().tolist(), keys, 1, "x7 B=256")
     assert namb <= 8
+
+
+@pytest.mark.parametrize("rc", [0, 2])
+def test_gemm_sample_other_roundings(rc):
+    """Sample mode of the blocked GEMM with fp32 (0) and f16 (2) rounding of
+    the logits before the draws, greedy rows beside temperature rows."""
+    rng = np.random.default_rng(9500 + rc)
+    B, H, V = 100, 1024, 12007
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    h = _hidden(rng, B, H, torch.bfloat16)
+    T = [float(x) for x in rng.choice([0.0, 0.8, 1.0], B)]
+    keys = engine_keys(B, 71 + rc)
+    ids = nvjsel.lm_head_sample_token_ids(h, W, temperatures=torch.tensor(T).cuda(),
+                                          rng_keys=keys_tensor(keys), weight_layout="vh", reduce_cast=rc)
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(h.float().cpu().numpy(), W.float().cpu().numpy())
+    namb = check_fused_sampled(ids.cpu().numpy(), z, T, keys, rc, f"gemm sample rc={rc}")
+    assert namb <= max(1, B // 16)
