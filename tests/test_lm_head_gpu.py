@@ -223,10 +223,11 @@ def test_mtp_draft_top1_casts_and_flattens(seq_len):
     check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(xb, as_f32(W)), 1, f"mtp T={seq_len}")
 
 
-@pytest.mark.parametrize("name", ["c1", "c4"])
+@pytest.mark.parametrize("name", ["c1", "c4", "x7"])
 def test_last_block_reduce_is_consistent_over_1000_calls(name):
     """The cross-block reduce (per-row atomicMax, then the last block by ticket
-    writes the ids and re-zeroes the workspace) at the C1 / C4 shapes: 1,000
+    writes the ids and re-zeroes the workspace) at the C1 / C4 shapes and the
+    B = 256 fused Gumbel shape of the blocked GEMM (x7): 1,000
     back-to-back launches on one workspace must all return the first call's
     ids.  Each launch writes its own output row; the first mismatch is named."""
     import bench
