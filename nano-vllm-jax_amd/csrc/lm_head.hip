@@ -1201,7 +1201,9 @@ static int dispatch_tile(const LmArgs& a, hipStream_t s) {
 // Blocks keep, per batch row, a running best key, fold it into the row's
 // maximum with one atomicMax per row, and the last block to finish writes the
 // ids (finish_rows; a reduce kernel over stored per-block keys cost ~7 us
-// more).  MODE_LOGITS stores the rounded logits instead.
+// more).  MODE_LOGITS stores the rounded logits instead; MODE_SAMPLE scores
+// every tile with the fast Gumbel draws after its K loop and rescores the
+// near-maximal entries exactly (the sample epilogue in the kernel).
 static constexpr int kGemmBBRows = 256;  // batch rows per blocked-GEMM pass
 static constexpr int kGemmBB = kGemmBBRows, kGemmKC = 32;
 static constexpr int kGemmQcap = 768;  // queue entries per wave (sample mode; LDS: 12 B each)
