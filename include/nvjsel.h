@@ -260,6 +260,21 @@ int nvjsel_derive_keys_table(const int32_t* slots, int batch, int32_t* counter_t
  */
 int nvjsel_debug_gumbel_draws(uint32_t first, int n, float* fast, float* exact, void* stream);
 
+/*
+ * Diagnostic (no counterpart in the reference): nvjsel_sample (no noise
+ * override) that also reports, per row, the top-p / top-k threshold the
+ * kernels settled on and the softmax mass of the kept set.  out_tau[b] is the
+ * threshold in x = logit / max(T, 1e-6) space (kept = {x >= tau}); out_mass[b]
+ * is mass(kept) / mass(top-k survivors) as the kernels' own fixed-point and
+ * grid-bin weights give it -- the intermediate that decides the threshold
+ * (nanovllm_jax/spec_decode.py:69-83).  Rows without a threshold (greedy,
+ * unfiltered, non-finite) get NaN in both.  out_ids as nvjsel_sample.
+ */
+int nvjsel_debug_sample_topp(const void* logits, int dtype, int batch, int vocab, int64_t row_stride,
+                             const float* temperature, const int32_t* top_k, const float* top_p,
+                             const uint32_t* keys, int32_t* out_ids, float* out_tau, double* out_mass,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -105,6 +105,12 @@ struct SampleArgs {
   int32_t* out_ids;
   float* lane_tops;                // [B, nchunks, 4 waves, kTopsPub] largest raw-logit lane maxima
   int topk;  // > 0: top-k selection (nvjsel_topk): every row FILTER with this k on raw logits
+  // nvjsel_debug_sample_topp only (null otherwise): each FILTER row's final
+  // threshold (x space) and the softmax mass of its kept set over the top-k
+  // survivors, as the kernels computed them; dbg_scale [B] is workspace
+  float* dbg_tau;
+  double* dbg_mass;
+  double* dbg_scale;
 };
 
 
@@ -760,6 +766,22 @@ __device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp,
     if (i0 + 1 < nk && ex + m0 < target && target <= ex + m0 + m1) s.tau = (uint32_t)(s.srt[i0 + 1] >> 32);
     __syncthreads();
     tau = s.tau;
+  }
+  if (a.dbg_tau) {  // nvjsel_debug_sample_topp: the kept prefix's share of the survivors' mass
+    unsigned long long kept = 0, all = 0;
+    for (int i = threadIdx.x; i < nk; i += kThreads) {
+      const uint32_t kk = (uint32_t)(s.srt[i] >> 32);
+      const unsigned long long w = fixed_mass(radix_value(kk), m);
+      all += w;
+      kept += kk >= tau ? w : 0ull;
+    }
+    unsigned long long K, Z;
+    (void)block_exclusive_scan<unsigned long long>(kept, s.wsum64, K);
+    (void)block_exclusive_scan<unsigned long long>(all, s.wsum64, Z);
+    if (threadIdx.x == 0) {
+      a.dbg_tau[b] = radix_value(tau);
+      a.dbg_mass[b] = (double)K / (double)Z;
+    }
   }
   // exact Gumbel-max over the survivors >= tau
   const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
@@ -1561,6 +1583,30 @@ __device__ uint32_t radix_descend(const SampleArgs& a, const char* row, float tp
   return prefix;
 }
 
+// nvjsel_debug_sample_topp: kept mass of a row whose threshold came from a
+// whole-row radix descent, by one more pass in the descent's own weights
+// (fixed-point exp(x - m) over x >= low): sum(x >= tau) / sum(x >= low).
+__device__ void dbg_row_mass(const SampleArgs& a, int b, const RowParams& rp, float m, uint32_t low, uint32_t tau,
+                             unsigned long long* wsum) {
+  const char* row = row_ptr(a, b);
+  unsigned long long kept = 0, all = 0;
+  for (int i = threadIdx.x; i < a.V; i += blockDim.x) {
+    const float x = load_logit(a, row, i) / rp.tp;
+    const uint32_t k = radix_key(x);
+    if (k < low) continue;
+    const unsigned long long w = fixed_mass(x, m);
+    all += w;
+    kept += k >= tau ? w : 0ull;
+  }
+  unsigned long long K, Z;
+  (void)block_exclusive_scan<unsigned long long>(kept, wsum, K);
+  (void)block_exclusive_scan<unsigned long long>(all, wsum, Z);
+  if (threadIdx.x == 0) {
+    a.dbg_tau[b] = radix_value(tau);
+    a.dbg_mass[b] = (double)K / (double)Z;
+  }
+}
+
 // ------------------------------------------------------------------ 2b. top-p rows (no top-k)
 // The row's histogram over grid bins (merged by select from the scan's chunk
 // histograms) gives the crossing bin; the gumbel pass then scores the
@@ -1571,6 +1617,7 @@ struct ToppXShared {
   double wsum[kThreads / 64];
   int bin;  // grid bin ib of the crossing, INT_MIN when the window holds no crossing
   unsigned long long target;
+  double above, scale;
 };
 
 // Crossing bin of a row histogram held as h[q] = bin D = PER * t + q of thread
@@ -1613,6 +1660,8 @@ __device__ __forceinline__ void topp_crossing(const unsigned long long (&h)[PER]
     if (cum <= pz && pz < cum + mq[q]) {
       sh.bin = tb - (threadIdx.x * PER + q);
       sh.target = (unsigned long long)floor((pz - cum) / sc[q]) + 1ull;
+      sh.above = cum / Z;  // nvjsel_debug_sample_topp: mass above the bin, and a bin weight's share
+      sh.scale = sc[q] / Z;
     }
     cum += mq[q];
   }
@@ -1746,7 +1795,13 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     const char* row = row_ptr(a, b);
     tau = 0;
     if (rp.k > 0) tau = radix_descend<false>(a, row, rp.tp, m, 0u, (unsigned long long)rp.k, 1.0f, s.hv);
+    const uint32_t tau_k = tau;
     if (rp.p < 1.0f) tau = radix_descend<true>(a, row, rp.tp, m, tau, 1ull, rp.p, s.hv);
+    if (a.dbg_tau) dbg_row_mass(a, b, rp, m, tau_k, tau, s.hv.wsum);
+  }
+  if (a.dbg_tau && ib != INT_MIN && threadIdx.x == 0) {
+    a.dbg_mass[b] = s.tx.above;  // the finish kernel adds the crossing bin's kept share
+    a.dbg_scale[b] = s.tx.scale;
   }
   // seed the row's best with the exact scores of the chunk maxima >= tau
   const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
@@ -1936,6 +1991,18 @@ __global__ void __launch_bounds__(kThreads) sample_finish_kernel(SampleArgs a) {
     for (int e = threadIdx.x; e < (int)n; e += kThreads) sh.v[e] = a.topp_cand[(size_t)b * kToppCap + e];
     __syncthreads();
     const uint32_t tau = lds_desc<true>(sh.d, sh.v, (int)n, a.row_target[b], ib);
+    if (a.dbg_tau) {  // nvjsel_debug_sample_topp: the bin's kept weight joins the mass above it
+      unsigned long long kept = 0, K;
+      for (int e = threadIdx.x; e < (int)n; e += kThreads) {
+        const uint32_t kk = (uint32_t)(sh.v[e] >> 32);
+        if (kk >= tau) kept += edge_mass(radix_value(kk), ib);
+      }
+      (void)block_exclusive_scan<unsigned long long>(kept, sh.d.wsum, K);
+      if (threadIdx.x == 0) {
+        a.dbg_tau[b] = radix_value(tau);
+        a.dbg_mass[b] += (double)K * a.dbg_scale[b];
+      }
+    }
     // fast scores first; exact ones only within the fast path's error of the
     // block maximum, and only if that maximum can beat the score above the bin
     float fm = -INFINITY;
@@ -1966,6 +2033,7 @@ __global__ void __launch_bounds__(kThreads) sample_finish_kernel(SampleArgs a) {
     const float m = chunk_max_x(rp, mk);
     const char* row = row_ptr(a, b);
     const uint32_t tau = radix_descend<true>(a, row, rp.tp, m, 0u, 1ull, rp.p, sh.hv);
+    if (a.dbg_tau) dbg_row_mass(a, b, rp, m, 0u, tau, sh.hv.wsum);
     for (int i = threadIdx.x; i < a.V; i += kThreads) {
       const float xv = load_logit(a, row, i) / rp.tp;
       if (!(xv >= lo && xv < hi) || radix_key(xv) < tau || xv + NVJSEL_GUMBEL_MAX < s_cur) continue;
@@ -1977,7 +2045,7 @@ __global__ void __launch_bounds__(kThreads) sample_finish_kernel(SampleArgs a) {
 }
 
 struct WsLayout {
-  size_t lane_tops, topp_chunk_hist, topp_chunk_tb, row_ib, row_target, row_key, row_tau, row_state, chunk_max, cand_count, cand_count_a, cand_floor_a, cand_floor, cand, topp_cand, topp_n;
+  size_t lane_tops, topp_chunk_hist, topp_chunk_tb, row_ib, row_target, row_key, row_tau, row_state, chunk_max, cand_count, cand_count_a, cand_floor_a, cand_floor, cand, topp_cand, topp_n, dbg_scale;
   size_t list_n, list_gumbel, total;
 };
 
@@ -2001,6 +2069,7 @@ static WsLayout ws_layout(int B, int V) {
   w.cand = o;       o += align_up((size_t)B * nc * kCandCap * 8, 256);
   w.topp_cand = o;  o += align_up((size_t)B * kToppCap * 8, 256);
   w.topp_n = o;     o += align_up((size_t)B * 4, 256);
+  w.dbg_scale = o;  o += align_up((size_t)B * 8, 256);
   w.list_n = o;     o += 256;
   w.list_gumbel = o; o += align_up((size_t)B * nc * 4, 256);
   w.total = o;
@@ -2043,6 +2112,7 @@ static SampleArgs make_args(const void* logits, int dtype, int batch, int vocab,
   a.cand = (unsigned long long*)(ws + w.cand);
   a.topp_cand = (unsigned long long*)(ws + w.topp_cand);
   a.topp_n = (uint32_t*)(ws + w.topp_n);
+  a.dbg_scale = (double*)(ws + w.dbg_scale);
   a.list_n = (uint32_t*)(ws + w.list_n);
   a.list_gumbel = (uint32_t*)(ws + w.list_gumbel);
   return a;
@@ -2053,11 +2123,10 @@ extern "C" size_t nvjsel_sample_workspace_size(int batch, int vocab) {
   return ws_layout(batch, vocab).total;
 }
 
-extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab, int64_t row_stride,
-                             const float* temperature, const int32_t* top_k, const float* top_p,
-                             const uint32_t* keys, const float* noise, int32_t* out_ids,
-                             void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
+static int sample_impl(const void* logits, int dtype, int batch, int vocab, int64_t row_stride,
+                       const float* temperature, const int32_t* top_k, const float* top_p,
+                       const uint32_t* keys, const float* noise, int32_t* out_ids,
+                       void* workspace, size_t workspace_bytes, void* stream, float* dbg_tau, double* dbg_mass) {
   if (!logits || !temperature || !keys || !out_ids)
     return fail(NVJSEL_EINVAL, "sample: null logits/temperature/keys/out_ids");
   if (batch <= 0 || vocab <= 0) {
@@ -2082,6 +2151,8 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   a.keys = keys;
   a.noise = noise;
   a.out_ids = out_ids;
+  a.dbg_tau = dbg_tau;
+  a.dbg_mass = dbg_mass;
   hipStream_t s = (hipStream_t)stream;
   const size_t esz = dtype_size(dtype);
   const int vec = (int)(16 / esz);
@@ -2121,6 +2192,31 @@ extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab
   NVJSEL_CHECK_LAUNCH("sample_finish_kernel");
 #undef NVJSEL_LAUNCH_CHUNK
   return NVJSEL_OK;
+}
+
+extern "C" int nvjsel_sample(const void* logits, int dtype, int batch, int vocab, int64_t row_stride,
+                             const float* temperature, const int32_t* top_k, const float* top_p,
+                             const uint32_t* keys, const float* noise, int32_t* out_ids,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return sample_impl(logits, dtype, batch, vocab, row_stride, temperature, top_k, top_p, keys, noise, out_ids,
+                     workspace, workspace_bytes, stream, nullptr, nullptr);
+}
+
+extern "C" int nvjsel_debug_sample_topp(const void* logits, int dtype, int batch, int vocab, int64_t row_stride,
+                                        const float* temperature, const int32_t* top_k, const float* top_p,
+                                        const uint32_t* keys, int32_t* out_ids, float* out_tau, double* out_mass,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (!out_tau || !out_mass) return fail(NVJSEL_EINVAL, "debug_sample_topp: null out_tau/out_mass");
+  if (batch <= 0) return fail(NVJSEL_EINVAL, "debug_sample_topp: batch <= 0");
+  hipStream_t s = (hipStream_t)stream;
+  // rows that settle no threshold keep NaN (all-ones bit patterns)
+  if (hipMemsetAsync(out_tau, 0xFF, (size_t)batch * sizeof(float), s) != hipSuccess ||
+      hipMemsetAsync(out_mass, 0xFF, (size_t)batch * sizeof(double), s) != hipSuccess)
+    return fail(NVJSEL_EHIP, "debug_sample_topp: hipMemsetAsync failed");
+  return sample_impl(logits, dtype, batch, vocab, row_stride, temperature, top_k, top_p, keys, nullptr, out_ids,
+                     workspace, workspace_bytes, stream, out_tau, out_mass);
 }
 
 extern "C" size_t nvjsel_topk_workspace_size(int batch, int vocab) {

@@ -43,6 +43,7 @@ SIGNATURES = {
     "nvjsel_topk_workspace_size": (_sz, [_i, _i]),
     "nvjsel_topk": (_i, [_vp, _i, _i, _i, _i64, _i, _vp, _vp, _vp, _sz, _vp]),
     "nvjsel_debug_gumbel_draws": (_i, [ctypes.c_uint32, _i, _vp, _vp, _vp]),
+    "nvjsel_debug_sample_topp": (_i, [_vp, _i, _i, _i, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
 }
 
 

@@ -184,6 +184,13 @@ def lm_head_greedy_top1_hip(hidden_norm: torch.Tensor, output_weight: torch.Tens
     return (ids, best) if return_best else ids
 
 
+def _row_stride(logits: torch.Tensor) -> int:
+    """Elements between rows of a [B, V] tensor with unit column stride.  A
+    size-1 batch dimension may carry any stride (torch keeps numpy's 0 there);
+    the library only needs it for B > 1."""
+    return int(logits.stride(0)) if int(logits.shape[0]) > 1 else int(logits.shape[1])
+
+
 def sample_token_ids(logits: torch.Tensor, temperatures: torch.Tensor, rng_keys: torch.Tensor, *,
                      top_k: torch.Tensor | None = None, top_p: torch.Tensor | None = None,
                      noise: torch.Tensor | None = None) -> torch.Tensor:
@@ -225,7 +232,7 @@ def sample_token_ids(logits: torch.Tensor, temperatures: torch.Tensor, rng_keys:
     stream = _stream_handle(dev)
     lib = _lib.load()
     ws = _WS.get(dev, stream, "sample", lib.nvjsel_sample_workspace_size(batch, vocab))
-    _lib.call("nvjsel_sample", logits.data_ptr(), dt, batch, vocab, int(logits.stride(0)),
+    _lib.call("nvjsel_sample", logits.data_ptr(), dt, batch, vocab, _row_stride(logits),
               temps.data_ptr(), tk.data_ptr() if tk is not None else None,
               tp.data_ptr() if tp is not None else None, keys.data_ptr(),
               nz.data_ptr() if nz is not None else None, out.data_ptr(), ws.data_ptr(), ws.numel(),
@@ -383,7 +390,7 @@ def topk_hip(logits: torch.Tensor, k: int):
     stream = _stream_handle(dev)
     lib = _lib.load()
     ws = _WS.get(dev, stream, "sample", lib.nvjsel_topk_workspace_size(batch, vocab))
-    _lib.call("nvjsel_topk", logits.data_ptr(), dt, batch, vocab, int(logits.stride(0)), k, values.data_ptr(),
+    _lib.call("nvjsel_topk", logits.data_ptr(), dt, batch, vocab, _row_stride(logits), k, values.data_ptr(),
               indices.data_ptr(), ws.data_ptr(), ws.numel(), stream)
     if squeeze:
         return values[:, None, :], indices[:, None, :]

@@ -31,3 +31,15 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """Every row a GPU parity checker exempted (tests/gpu_helpers.report)."""
+    try:
+        from tests.gpu_helpers import REPORTS
+    except Exception:  # pragma: no cover
+        return
+    if REPORTS:
+        terminalreporter.section("parity exemptions (rows reported, not hidden)")
+        for line in REPORTS:
+            terminalreporter.write_line(line)
