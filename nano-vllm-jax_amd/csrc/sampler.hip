@@ -53,6 +53,9 @@ enum { ROW_GREEDY = 0, ROW_FULL = 1, ROW_FILTER = 2 };
 // The per-row best key, hit by same-address atomics from many blocks, gets a
 // 256-byte line of its own.
 static constexpr int kRowPad8 = 32;  // uint64 words
+static constexpr int kRowPad32 = 64;  // uint32 words
+static constexpr int kOnepassRows = 256;    // rows a one-pass call may hold (its tickets' region)
+static constexpr int kOnepassSlots = 4096;  // (sub-chunk, row) blocks a one-pass call may launch
 
 enum { STATE_DONE = 1, STATE_HEAVY = 2, STATE_NEEDS_GUMBEL = 3, STATE_TOPP = 4 };
 
@@ -86,6 +89,8 @@ struct SampleArgs {
   const uint32_t* keys;
   const float* noise;  // optional [B, V] Gumbel override
   unsigned long long* row_key;     // [B * kRowPad8] best key per row
+  uint32_t* row_ticket;            // [kOnepassRows * kRowPad32] one-pass arrivals per row (zero at rest)
+  unsigned long long* onepass_slot;  // [kOnepassSlots] one-pass block keys, row-major (zero at rest)
   uint32_t* row_tau;               // [B]
   int32_t* row_state;              // [B]
   unsigned long long* chunk_max;   // [B, nchunks]
@@ -1896,60 +1901,175 @@ __global__ void __launch_bounds__(kThreads, 7) sample_gumbel_kernel(SampleArgs a
   }
 }
 
-// ------------------------------------------------------------------ one pass (no top-k, no top-p)
-// Calls without top-k and top-p arrays hold only greedy and temperature rows
-// (model.py:929-936): every element of a temperature row may need its draw,
-// so the scan / select / seed stages buy little.  One block per
-// (2048-element sub-chunk, row) scores its elements directly -- greedy rows
-// by argmax key of the raw logit, temperature rows by the block Gumbel-max
-// (fast draws, exact rescoring near the wave maximum) -- and leaves one key
-// per wave; a per-row kernel takes the maximum.
+// ------------------------------------------------------------------ one pass
+// Calls without top-k/top-p arrays whose (2048-element sub-chunk, row) grid
+// fits one round on the device run as ONE launch.  Each block scores its
+// elements directly: greedy rows by the argmax key of the raw logit;
+// temperature rows by fast scores -- x' = l * (1 / T') (within 1.2e-7 |x| of
+// the correctly rounded l / T') plus the hardware-log draw (within 1.91e-6 of
+// the exact one), four Threefry chains per lane, no LDS packing -- after which
+// only the elements within the fast path's error of the block's fast maximum
+// are rescored exactly (x = l / T', fp64 logs), usually one per block.  Blocks
+// holding a NaN, +inf or near-overflow scaled logit (or a noise override) take
+// the exact per-wave path instead.  Each block stores its exact best key in a
+// slot of its own (device-scope atomic store, not waited for) and takes a
+// ticket on its row's counter (a 256-byte line per row); the row's last block
+// takes every slot of the row with an atomic exchange to zero (a slot whose
+// store is still in flight reads zero and is read again), writes the id and
+// re-zeroes the counter: two memory round trips per block, not three.
 template <int DT, int VEC>
 __global__ void __launch_bounds__(kThreads) sample_onepass_kernel(SampleArgs a) {
   __shared__ GumbelShared sh;
+  __shared__ float s_fmax[kThreads / 64];
+  __shared__ int s_slow[kThreads / 64];
+  __shared__ unsigned long long s_key[kThreads / 64];
+  __shared__ int s_last;
+  constexpr int EPT = kGumbelEPT;
   const int b = blockIdx.y;
-  const int base = blockIdx.x * (kThreads * kGumbelEPT);
-  const int wave = threadIdx.x >> 6;
+  const int base = blockIdx.x * (kThreads * EPT);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const RowParams rp = row_params(a, b);
-  float x[kGumbelEPT];
+  float l[EPT];
   uint32_t valid;
-  load_chunk_elems<DT, VEC, kGumbelEPT>(row_ptr(a, b), base, a.V, true, 1.0f, x, valid);
+  load_chunk_elems<DT, VEC, EPT>(row_ptr(a, b), base, a.V, true, 1.0f, l, valid);
   unsigned long long best = 0;
-  // every wave settles its own 512 elements (no block barrier)
   if (rp.mode == ROW_GREEDY) {  // block-uniform
 #pragma unroll
-    for (int j = 0; j < kGumbelEPT; ++j)
-      if ((valid >> j) & 1u) best = max_u64(best, argmax_key(x[j], (uint32_t)elem_index<VEC>(base, j)));
-    best = wave_max_u64(best);
+    for (int j = 0; j < EPT; ++j)
+      if ((valid >> j) & 1u) best = max_u64(best, argmax_key(l[j], (uint32_t)elem_index<VEC>(base, j)));
   } else {
-    // a NaN or +inf scaled logit scores NaN / +inf whatever its draw: the
-    // first NaN, else the first +inf, is the row's argmax (jnp.argmax); their
-    // keys exceed every finite score's
-    unsigned long long nf = 0;
+    const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+    // the draws' random bits depend on the key and the index only: computed
+    // while the logits are still in flight
+    uint32_t bits[EPT];
 #pragma unroll
-    for (int j = 0; j < kGumbelEPT; ++j) {
-      x[j] = x[j] / rp.tp;
-      if (((valid >> j) & 1u) && (x[j] != x[j] || x[j] == INFINITY))
-        nf = max_u64(nf, argmax_key(x[j], (uint32_t)elem_index<VEC>(base, j)));
+    for (int g = 0; g < EPT / 4; ++g) {
+      uint32_t idx[4], bq[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) idx[j] = (uint32_t)elem_index<VEC>(base, 4 * g + j);
+      random_bits32_n<4>(key, idx, bq);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bits[4 * g + j] = bq[j];
     }
-    nf = wave_max_u64(nf);
-    if (nf) {
-      best = nf;
+    const float inv = 1.0f / rp.tp;
+    float xf[EPT];
+    bool slow = a.noise != nullptr;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      xf[j] = l[j] * inv;
+      // NaN, +inf, or a magnitude where l * (1 / T') may round across the
+      // overflow threshold that l / T' does not (or the reverse)
+      if (((valid >> j) & 1u) && !(fabsf(xf[j]) <= 1e37f || l[j] == -INFINITY)) slow = true;
+    }
+    // block-wide OR of `slow` (the barrier also orders the flags)
+    const bool wslow = __any(slow);  // every lane votes (outside the lane-0 branch)
+    if (lane == 0) s_slow[wave] = wslow ? 1 : 0;
+    __syncthreads();
+    slow = false;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) slow |= s_slow[w] != 0;
+    if (slow) {
+      // a NaN or +inf scaled logit scores NaN / +inf whatever its draw: the
+      // first NaN, else the first +inf, is the row's argmax (jnp.argmax);
+      // their keys exceed every finite score's
+      float x[EPT];
+      unsigned long long nf = 0;
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        x[j] = l[j] / rp.tp;
+        if (((valid >> j) & 1u) && (x[j] != x[j] || x[j] == INFINITY))
+          nf = max_u64(nf, argmax_key(x[j], (uint32_t)elem_index<VEC>(base, j)));
+      }
+      nf = wave_max_u64(nf);
+      if (nf) {
+        best = nf;
+      } else {
+        constexpr int WS = 64 * EPT;
+        best = wave_gumbel<EPT, VEC>(a, b, key, x, base, valid, -INFINITY, sh.dx + wave * WS, sh.di + wave * WS);
+      }
     } else {
-      const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
-      constexpr int WS = 64 * kGumbelEPT;
-      best = wave_gumbel<kGumbelEPT, VEC>(a, b, key, x, base, valid, -INFINITY, sh.dx + wave * WS, sh.di + wave * WS);
+      float st[EPT];
+      float fm = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < EPT; ++q) {
+        const float v = xf[q] + gumbel_fast_from_bits(bits[q]);  // branch-free, then masked
+        st[q] = ((valid >> q) & 1u) ? v : -INFINITY;
+        fm = fmaxf(fm, st[q]);
+      }
+      fm = wave_max_f32(fm);
+      if (lane == 0) s_fmax[wave] = fm;
+      __syncthreads();
+      float S = s_fmax[0];
+#pragma unroll
+      for (int w = 1; w < kThreads / 64; ++w) S = fmaxf(S, s_fmax[w]);
+      if (S == -INFINITY) {
+        // every valid element is -inf (x = -inf exactly): the first one
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+          if ((valid >> j) & 1u) best = max_u64(best, argmax_key(-INFINITY, (uint32_t)elem_index<VEC>(base, j)));
+      } else {
+        // |fast - exact| <= 1.2e-7 |x| + 1.91e-6 + one ulp of the sum for each
+        // score; any element that can hold the exact maximum is within twice
+        // that (ample) bound of S
+        const float thr = S - (2e-3f + 2e-6f * (fabsf(S) + 20.0f));
+        uint32_t cm = 0;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) cm |= (st[j] >= thr ? 1u : 0u) << j;
+        while (__any(cm != 0u)) {  // one exact rescoring per lane and pass
+          const int q = cm ? __builtin_ctz(cm) : 0;
+          float lv = l[0];
+          uint32_t bv = bits[0];
+#pragma unroll
+          for (int j = 1; j < EPT; ++j) {
+            lv = q == j ? l[j] : lv;
+            bv = q == j ? bits[j] : bv;
+          }
+          if (cm) {
+            const uint32_t i = (uint32_t)elem_index<VEC>(base, q);
+            best = max_u64(best, argmax_key(lv / rp.tp + gumbel_from_bits(bv), i));
+            cm &= cm - 1u;
+          }
+        }
+      }
     }
   }
-  if ((threadIdx.x & 63) == 0) a.cand[((size_t)b * gridDim.x + blockIdx.x) * (kThreads / 64) + wave] = best;
-}
-
-__global__ void __launch_bounds__(64) sample_onepass_finish_kernel(SampleArgs a, int nsub) {
-  const int b = blockIdx.x;
+  best = wave_max_u64(best);
+  if (lane == 0) s_key[wave] = best;
+  __syncthreads();
+  unsigned long long* slots = a.onepass_slot + (size_t)b * gridDim.x;
+  if (threadIdx.x == 0) {
+    unsigned long long m = s_key[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) m = max_u64(m, s_key[w]);
+    // every key is nonzero (its low word is ~index, index < 2^31)
+    __hip_atomic_store(slots + blockIdx.x, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t t = atomicAdd(&a.row_ticket[(size_t)b * kRowPad32], 1u);
+    s_last = t == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // The row's last block.  Every block issued its slot store before its
+  // ticket, so each store is performed or in flight: a slot still zero is
+  // read again until it lands (bounded: a slot that never lands -- impossible
+  // unless a block skipped its store -- leaves the row's id at -1).  Each
+  // read also zeroes the slot for the next call.
   unsigned long long m = 0;
-  for (int i = threadIdx.x; i < nsub; i += 64) m = max_u64(m, a.cand[(size_t)b * nsub + i]);
-  m = wave_max_u64(m);
-  if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)m);
+  bool lost = false;
+  for (int i = threadIdx.x; i < (int)gridDim.x; i += kThreads) {
+    unsigned long long v = atomicExch(slots + i, 0ull);
+    for (int spin = 0; v == 0ull && spin < (1 << 16); ++spin) {
+      __builtin_amdgcn_s_sleep(2);
+      v = atomicExch(slots + i, 0ull);
+    }
+    lost |= v == 0ull;
+    m = max_u64(m, v);
+  }
+  m = block_max_u64(m, sh.red);
+  lost = __syncthreads_or(lost);
+  if (threadIdx.x == 0) {
+    a.out_ids[b] = lost ? -1 : (int32_t)(~(uint32_t)m);
+    __hip_atomic_store(&a.row_ticket[(size_t)b * kRowPad32], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // ------------------------------------------------------------------ 5. finish
@@ -2045,7 +2165,7 @@ __global__ void __launch_bounds__(kThreads) sample_finish_kernel(SampleArgs a) {
 }
 
 struct WsLayout {
-  size_t lane_tops, topp_chunk_hist, topp_chunk_tb, row_ib, row_target, row_key, row_tau, row_state, chunk_max, cand_count, cand_count_a, cand_floor_a, cand_floor, cand, topp_cand, topp_n, dbg_scale;
+  size_t lane_tops, topp_chunk_hist, topp_chunk_tb, row_ib, row_target, row_key, row_tau, row_state, chunk_max, cand_count, cand_count_a, cand_floor_a, cand_floor, cand, topp_cand, topp_n, dbg_scale, row_ticket, onepass_slot;
   size_t list_n, list_gumbel, total;
 };
 
@@ -2053,6 +2173,10 @@ static WsLayout ws_layout(int B, int V) {
   const size_t nc = (size_t)((V + kChunkMin - 1) / kChunkMin);
   WsLayout w;
   size_t o = 0;
+  // zero at rest, at the same offset for every shape (a workspace is shared
+  // across shapes and with nvjsel_topk, whose other regions are scratch)
+  w.row_ticket = o; o += (size_t)kOnepassRows * kRowPad32 * 4;
+  w.onepass_slot = o; o += (size_t)kOnepassSlots * 8;
   w.lane_tops = o;  o += align_up((size_t)B * nc * (kThreads / 64) * kTopsPub * 4, 256);
   w.topp_chunk_hist = o; o += align_up((size_t)B * nc * kToppBins * 4, 256);
   w.topp_chunk_tb = o;   o += align_up((size_t)B * nc * 4, 256);
@@ -2113,6 +2237,8 @@ static SampleArgs make_args(const void* logits, int dtype, int batch, int vocab,
   a.topp_cand = (unsigned long long*)(ws + w.topp_cand);
   a.topp_n = (uint32_t*)(ws + w.topp_n);
   a.dbg_scale = (double*)(ws + w.dbg_scale);
+  a.row_ticket = (uint32_t*)(ws + w.row_ticket);
+  a.onepass_slot = (unsigned long long*)(ws + w.onepass_slot);
   a.list_n = (uint32_t*)(ws + w.list_n);
   a.list_gumbel = (uint32_t*)(ws + w.list_gumbel);
   return a;
@@ -2175,10 +2301,9 @@ static int sample_impl(const void* logits, int dtype, int batch, int vocab, int6
   // round on the device (8 per CU): a latency-bound call saves the scan and
   // select launches; larger ones keep the seeded, pruned Gumbel pass
   const int nsub = (vocab + kThreads * kGumbelEPT - 1) / (kThreads * kGumbelEPT);
-  if (!top_k && !top_p && (long long)batch * nsub <= 8LL * device_cu_count()) {
+  if (!top_k && !top_p && batch <= kOnepassRows && (long long)batch * nsub <= 8LL * device_cu_count() &&
+      (long long)batch * nsub <= kOnepassSlots) {
     NVJSEL_LAUNCH_CHUNK(sample_onepass_kernel, dim3(nsub, batch));
-    hipLaunchKernelGGL(sample_onepass_finish_kernel, dim3(batch), dim3(64), 0, s, a, nsub * (kThreads / 64));
-    NVJSEL_CHECK_LAUNCH("sample_onepass_finish_kernel");
     return NVJSEL_OK;
   }
   NVJSEL_LAUNCH_CHUNK(sample_scan_kernel, dim3(a.nchunks, batch));

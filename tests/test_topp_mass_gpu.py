@@ -41,7 +41,7 @@ def _debug_sample(logits: torch.Tensor, temps, top_k, top_p, keys_i32: torch.Ten
     mass = torch.empty(B, dtype=torch.float64, device=dev)
     lib = _lib.load()
     nbytes = lib.nvjsel_sample_workspace_size(B, V)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)  # zero at rest (include/nvjsel.h)
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     _lib.call("nvjsel_debug_sample_topp", logits.data_ptr(), dt, B, V, nvjsel.selection._row_stride(logits), t.data_ptr(),
               k.data_ptr(), p.data_ptr(), keys_i32.data_ptr(), ids.data_ptr(), tau.data_ptr(), mass.data_ptr(),
