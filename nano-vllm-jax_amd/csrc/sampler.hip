@@ -1902,7 +1902,7 @@ __global__ void __launch_bounds__(kThreads, 7) sample_gumbel_kernel(SampleArgs a
 }
 
 // ------------------------------------------------------------------ one pass
-// Calls without top-k/top-p arrays whose (2048-element sub-chunk, row) grid
+// Calls without top-k/top-p arrays whose (4096-element sub-chunk, row) grid
 // fits one round on the device run as ONE launch.  Each block scores its
 // elements directly: greedy rows by the argmax key of the raw logit;
 // temperature rows by fast scores -- x' = l * (1 / T') (within 1.2e-7 |x| of
@@ -1914,17 +1914,25 @@ __global__ void __launch_bounds__(kThreads, 7) sample_gumbel_kernel(SampleArgs a
 // the exact per-wave path instead.  Each block stores its exact best key in a
 // slot of its own (device-scope atomic store, not waited for) and takes a
 // ticket on its row's counter (a 256-byte line per row); the row's last block
-// takes every slot of the row with an atomic exchange to zero (a slot whose
-// store is still in flight reads zero and is read again), writes the id and
-// re-zeroes the counter: two memory round trips per block, not three.
+// reads the row's slots (one still zero holds a store in flight and is read
+// again), writes the id and re-zeroes the slots and the counter.  (Reading the
+// slots speculatively in every block while its ticket is in flight measured
+// 1.5 us slower on C2: the extra coherent loads contend.)
+static constexpr int kOnepassEPT = 16;  // elements per thread (measured: 16 beats 8 by ~0.4 us on C2)
+struct OnepassShared {
+  unsigned long long red[kThreads / 64];
+  float dx[kThreads * kOnepassEPT];  // the exact path's per-wave dense lists
+  uint32_t di[kThreads * kOnepassEPT];
+};
+
 template <int DT, int VEC>
 __global__ void __launch_bounds__(kThreads) sample_onepass_kernel(SampleArgs a) {
-  __shared__ GumbelShared sh;
+  __shared__ OnepassShared sh;
   __shared__ float s_fmax[kThreads / 64];
   __shared__ int s_slow[kThreads / 64];
   __shared__ unsigned long long s_key[kThreads / 64];
   __shared__ int s_last;
-  constexpr int EPT = kGumbelEPT;
+  constexpr int EPT = kOnepassEPT;
   const int b = blockIdx.y;
   const int base = blockIdx.x * (kThreads * EPT);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1951,6 +1959,9 @@ __global__ void __launch_bounds__(kThreads) sample_onepass_kernel(SampleArgs a) 
 #pragma unroll
       for (int j = 0; j < 4; ++j) bits[4 * g + j] = bq[j];
     }
+    // the logits are first used here, after the draws (no instruction is
+    // scheduled across this point, so their wait stays below the draws)
+    __builtin_amdgcn_sched_barrier(0);
     const float inv = 1.0f / rp.tp;
     float xf[EPT];
     bool slow = a.noise != nullptr;
@@ -2051,18 +2062,19 @@ __global__ void __launch_bounds__(kThreads) sample_onepass_kernel(SampleArgs a) 
   // The row's last block.  Every block issued its slot store before its
   // ticket, so each store is performed or in flight: a slot still zero is
   // read again until it lands (bounded: a slot that never lands -- impossible
-  // unless a block skipped its store -- leaves the row's id at -1).  Each
-  // read also zeroes the slot for the next call.
+  // unless a block skipped its store -- leaves the row's id at -1).  The slots
+  // and the counter are re-zeroed for the next call.
   unsigned long long m = 0;
   bool lost = false;
   for (int i = threadIdx.x; i < (int)gridDim.x; i += kThreads) {
-    unsigned long long v = atomicExch(slots + i, 0ull);
-    for (int spin = 0; v == 0ull && spin < (1 << 16); ++spin) {
+    unsigned long long x = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int spin = 0; x == 0ull && spin < (1 << 16); ++spin) {
       __builtin_amdgcn_s_sleep(2);
-      v = atomicExch(slots + i, 0ull);
+      x = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    lost |= v == 0ull;
-    m = max_u64(m, v);
+    lost |= x == 0ull;
+    m = max_u64(m, x);
+    __hip_atomic_store(slots + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   m = block_max_u64(m, sh.red);
   lost = __syncthreads_or(lost);
@@ -2298,10 +2310,10 @@ static int sample_impl(const void* logits, int dtype, int batch, int vocab, int6
     NVJSEL_CHECK_LAUNCH(#KERN);                                                                 \
   } while (0)
   // one pass when the call has no top-k/top-p arrays and its blocks fit one
-  // round on the device (8 per CU): a latency-bound call saves the scan and
+  // round on the device (4 per CU): a latency-bound call saves the scan and
   // select launches; larger ones keep the seeded, pruned Gumbel pass
-  const int nsub = (vocab + kThreads * kGumbelEPT - 1) / (kThreads * kGumbelEPT);
-  if (!top_k && !top_p && batch <= kOnepassRows && (long long)batch * nsub <= 8LL * device_cu_count() &&
+  const int nsub = (vocab + kThreads * kOnepassEPT - 1) / (kThreads * kOnepassEPT);
+  if (!top_k && !top_p && batch <= kOnepassRows && (long long)batch * nsub <= 4LL * device_cu_count() &&
       (long long)batch * nsub <= kOnepassSlots) {
     NVJSEL_LAUNCH_CHUNK(sample_onepass_kernel, dim3(nsub, batch));
     return NVJSEL_OK;
