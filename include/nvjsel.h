@@ -93,9 +93,11 @@ int nvjsel_lm_head_top1(const void* hidden, int hidden_dtype,
  * own (one per GPU, held until the process ends) and calls no allocating
  * routine.  batch <= 4096 (NVJSEL_EUNSUPPORTED above).  Every call on a GPU
  * shares that GPU's array, so calls that overlap in time on one GPU (other
- * streams, other threads) race; calls ordered on a stream do not.  The first
- * call on a device looks up the array's address and zero-fills it on
- * `stream`.
+ * streams, other threads) race; calls ordered on a stream do not.  The array
+ * starts zeroed (static device storage without an initializer, zero-filled
+ * when the code object is loaded) and every call leaves it zeroed; the first
+ * call on a device only looks up its address, so it may itself be captured
+ * into a graph.
  */
 int nvjsel_lm_head_top1_noalloc(const void* hidden, int hidden_dtype,
                                 const void* weight, int weight_dtype, int weight_layout,
@@ -124,10 +126,10 @@ int nvjsel_lm_head_sample(const void* hidden, int hidden_dtype,
  * route of lm_head_token_ids_and_topk(top_k > 0) (nanovllm_jax/model.py:
  * 866-898: jnp.dot(hidden_norm, W) then lax.top_k / radix_topk) and sampling
  * with top-k / top-p from the hidden state.  out_logits[b, v] (rows
- * out_row_stride elements apart, out_dtype f32 or bf16) = sum_k hidden[b,k] *
- * W(v,k) accumulated in fp32 and rounded per reduce_cast (the reference's dot
- * output: bf16 for bf16 x bf16), then stored as out_dtype (bf16: round to
- * nearest even).  Same kernels as nvjsel_lm_head_top1, with a store epilogue;
+ * out_row_stride elements apart, out_dtype f32, bf16 or f16) = sum_k
+ * hidden[b,k] * W(v,k) accumulated in fp32 and rounded per reduce_cast (the
+ * reference's dot output: bf16 for bf16 x bf16, f16 for f16 x f16), then
+ * stored as out_dtype (bf16 / f16: round to nearest even).  Same kernels as nvjsel_lm_head_top1, with a store epilogue;
  * no workspace.
  */
 int nvjsel_lm_head_logits(const void* hidden, int hidden_dtype,

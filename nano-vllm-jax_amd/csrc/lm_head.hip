@@ -87,15 +87,16 @@ struct LmArgs {
   int32_t* out_ids;
   float* out_best;
   void* out_logits;      // MODE_LOGITS: [B, out_stride] of out_dtype, offset to this launch's first row
-  int out_dtype;         // DT_F32 or DT_BF16
+  int out_dtype;         // DT_F32, DT_BF16 or DT_F16
   long long out_stride;  // elements between output rows
 };
 
-// MODE_LOGITS store of logit (b, v): f32 as is, bf16 rounded to nearest even.
+// MODE_LOGITS store of logit (b, v): f32 as is, bf16 / f16 rounded to nearest even.
 __device__ __forceinline__ void store_logit(const LmArgs& a, int b, int v, float val) {
   const size_t i = (size_t)b * (size_t)a.out_stride + (size_t)v;
   if (a.out_dtype == DT_F32) ((float*)a.out_logits)[i] = val;
-  else ((__bf16*)a.out_logits)[i] = (__bf16)val;
+  else if (a.out_dtype == DT_BF16) ((__bf16*)a.out_logits)[i] = (__bf16)val;
+  else ((_Float16*)a.out_logits)[i] = (_Float16)val;
 }
 
 template <int WT>
@@ -1833,7 +1834,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   if (reduce_cast < 0 || reduce_cast > 2) { set_error("%s: reduce_cast must be 0, 1 or 2", who); return NVJSEL_EINVAL; }
   if (mode == MODE_SAMPLE && (!temperature || !keys)) { set_error("%s: null temperature/keys", who); return NVJSEL_EINVAL; }
   if (mode == MODE_LOGITS) {
-    if (lo.dtype != DT_F32 && lo.dtype != DT_BF16) { set_error("%s: out dtype must be f32 or bf16", who); return NVJSEL_EINVAL; }
+    if (!valid_dtype(lo.dtype)) { set_error("%s: out dtype must be f32, bf16 or f16", who); return NVJSEL_EINVAL; }
     if (lo.stride < V) { set_error("%s: out row stride < vocab", who); return NVJSEL_EINVAL; }
   }
   if (prenorm) {
@@ -1996,11 +1997,11 @@ static int noalloc_scratch(hipStream_t stream, void** out) {
     void* p = nullptr;
     NVJSEL_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
     if (!p) return fail(NVJSEL_EHIP, "lm_head_top1_noalloc: no device address for the scratch array");
-    // a fill kernel rather than hipMemsetAsync: safe under graph capture
-    const size_t words = kNoAllocScratchBytes / 4;
-    hipLaunchKernelGGL(lm_zero_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream, (uint32_t*)p,
-                       words);
-    NVJSEL_CHECK_LAUNCH("lm_zero_kernel");
+    // No fill: the array has static storage duration without an initializer,
+    // so the code object's loader zero-fills it on every device, and every
+    // call leaves it zero again.  (A fill launched here would, on a first call
+    // made under graph capture, only be recorded into the graph.)
+    (void)stream;
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];

@@ -297,12 +297,12 @@ def lm_head_sample_token_ids(hidden_norm: torch.Tensor, output_weight: torch.Ten
 def _dense_logits(x: torch.Tensor, w: torch.Tensor, layout: int, vocab: int, rc: int) -> torch.Tensor:
     """Logits ``[B, V]`` of ``x [B, H]`` against the weight operand, from the
     library's LM-head kernels (nvjsel_lm_head_logits): fp32 accumulation
-    rounded as the reference's dot (``rc``); stored bf16 when they are
-    bf16-rounded, f32 otherwise."""
+    rounded as the reference's dot (``rc``); stored bf16 / f16 when they are
+    bf16- / f16-rounded (the dtype jnp.dot returns), f32 otherwise."""
     batch, hidden_dim = int(x.shape[0]), int(x.shape[1])
     dev = _require_cuda(x, w)
     x = x.contiguous()
-    out_dtype = torch.bfloat16 if rc == 1 else torch.float32
+    out_dtype = {1: torch.bfloat16, 2: torch.float16}.get(rc, torch.float32)
     out = torch.empty((batch, vocab), dtype=out_dtype, device=dev)
     _lib.call("nvjsel_lm_head_logits", x.data_ptr(), _dtype_code(x, "hidden"), w.data_ptr(),
               _dtype_code(w, "weight"), layout, batch, hidden_dim, vocab, rc, out.data_ptr(),
@@ -313,7 +313,7 @@ def _dense_logits(x: torch.Tensor, w: torch.Tensor, layout: int, vocab: int, rc:
 def lm_head_logits_hip(hidden_norm: torch.Tensor, output_weight: torch.Tensor, *,
                        weight_layout: str | None = None, reduce_cast: int | None = None) -> torch.Tensor:
     """Dense LM-head logits ``[B, V]`` (``jnp.dot(hidden_norm, W)``,
-    model.py:765-780): fp32 accumulation; bf16 x bf16 gives bf16 logits (the
+    model.py:765-780): fp32 accumulation; bf16 x bf16 gives bf16 logits and f16 x f16 f16 logits (the
     reference's dot output), other operand types f32 logits."""
     x = _flatten_hidden(hidden_norm, require_3d=False)
     batch, hidden_dim = int(x.shape[0]), int(x.shape[1])
@@ -443,6 +443,9 @@ def mtp_greedy_top1_token_ids(x_normed: torch.Tensor, output_weight: torch.Tenso
     return ids.reshape(batch, seq_len)
 
 
+DERIVE_KEYS_TABLE_MAX_BATCH = 8192  # nvjsel_derive_keys_table's limit (include/nvjsel.h)
+
+
 def derive_rng_keys_from_table(slots: torch.Tensor, counter_table: torch.Tensor) -> torch.Tensor:
     """Keys for the rows' slots from the device-resident counter table, which
     is advanced in place (model_executor.py:3593-3619).  ``counter_table`` is
@@ -454,6 +457,9 @@ def derive_rng_keys_from_table(slots: torch.Tensor, counter_table: torch.Tensor)
     s = slots.to(dtype=torch.int32).reshape(-1).contiguous()
     if s.numel() == 0 or counter_table.numel() == 0:
         raise ValueError("slots and counter_table must be non-empty")
+    if s.numel() > DERIVE_KEYS_TABLE_MAX_BATCH:
+        # one launch gathers every counter before any is written (LDS staging)
+        raise ValueError(f"derive_rng_keys_from_table serves at most {DERIVE_KEYS_TABLE_MAX_BATCH} rows per call")
     keys = torch.empty((s.numel(), 2), dtype=torch.int32, device=dev)
     _lib.call("nvjsel_derive_keys_table", s.data_ptr(), s.numel(), counter_table.data_ptr(),
               counter_table.numel(), keys.data_ptr(), _stream_handle(dev))

@@ -178,7 +178,8 @@ def test_dense_logits_match_float64(B, H, layout, act, wdt):
     logits = nvjsel.lm_head_logits_hip(h, W, weight_layout=layout)
     torch.cuda.synchronize()
     rc = nvjsel.reference_reduce_cast(act, wdt)
-    assert logits.dtype == (torch.bfloat16 if rc == 1 else torch.float32)
+    # the dtype jnp.dot returns: bf16 x bf16 -> bf16, f16 x f16 -> f16, else f32
+    assert logits.dtype == {1: torch.bfloat16, 2: torch.float16}.get(rc, torch.float32)
     _check_logits(logits, h.float().cpu().numpy(), Wvh.float().cpu().numpy(), rc, f"{B},{H},{layout},{act},{wdt}")
 
 
@@ -276,11 +277,13 @@ def test_gemm_full_vocab_b256_with_prenorm():
     check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(xin, W), 1, "gemm B=256 prenorm")
 
 
-@pytest.mark.parametrize("B,H", [(65, 512), (130, 1024), (256, 1024)])
+@pytest.mark.parametrize("B,H", [(65, 512), (130, 1024), (256, 1024), (300, 1024), (513, 512)])
 def test_gemm_sample_mixed_temperatures(B, H):
-    """Fused Gumbel sampling through the blocked GEMM (64 < B <= 256): greedy
-    rows (T = 0) beside temperature rows, a vocabulary that is not a multiple
-    of the 256-row tile, against the oracle's scores s_v = rnd(z_v)/T + g_v."""
+    """Fused Gumbel sampling through the blocked GEMM (64 < B <= 256 per
+    pass; B = 300 and 513 take two and three 256-row passes that reuse the
+    row keys and the ticket): greedy rows (T = 0) beside temperature rows, a
+    vocabulary that is not a multiple of the 256-row tile, against the
+    oracle's scores s_v = rnd(z_v)/T + g_v."""
     rng = np.random.default_rng(9100 + B + H)
     V = 20011
     W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)

@@ -4,7 +4,8 @@ nvjsel_lm_head_top1_noalloc keeps its workspace in a fixed device array
 instead of a caller workspace; its ids (and winning logits) must equal
 nvjsel_lm_head_top1's on the same inputs -- on two calls in a row, the second
 with a smaller batch (the array keeps the first call's state between calls),
-across the streaming (B <= 2), tile (3..64) and chunked (> 64) paths."""
+across the streaming (B <= 2), tile (3..64), blocked-GEMM (65..256) and
+multi-pass (> 256: 256-row passes reusing the keys and ticket) paths."""
 import numpy as np
 import pytest
 import torch
@@ -33,7 +34,7 @@ def _run_both(lib, h, W, B, H, V):
     return ids_a.cpu().numpy(), best_a.cpu().numpy(), ids_b.cpu().numpy(), best_b.cpu().numpy()
 
 
-@pytest.mark.parametrize("batches", [(64, 8), (1, 1), (200, 2), (33, 3)])
+@pytest.mark.parametrize("batches", [(64, 8), (1, 1), (200, 2), (33, 3), (300, 70)])
 def test_noalloc_matches_workspace_entry(batches):
     lib = _lib.load()
     rng = np.random.default_rng(sum(batches))
