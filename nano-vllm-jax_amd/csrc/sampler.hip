@@ -810,12 +810,16 @@ __device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp,
 // under its load time): a max3 tree per vector and an unordered compare per
 // pair for NaN detection; the first index of the maximum is found per wave
 // with one ballot per vector slot.
+static constexpr int kScanStage = 4;  // candidates a lane stages in LDS between counting and writing
 struct ScanShared {
   unsigned long long wkey[kThreads / 64];
   uint32_t wfloor[kThreads / 64];
   float wtop[kThreads / 64];  // each wave's kTops-th largest lane maximum
   uint32_t cnt, cnt_b, waves;
-  uint32_t topp_h[kToppBins];  // top-p-only rows: the chunk's grid-bin histogram (2^-17 units)
+  union {
+    uint32_t topp_h[kToppBins];  // top-p-only rows: the chunk's grid-bin histogram (2^-17 units)
+    unsigned long long stage[kScanStage][kThreads];  // top-k rows: each lane's first candidates
+  };
 };
 
 typedef short nvjsel_s16x2 __attribute__((ext_vector_type(2)));
@@ -1095,14 +1099,28 @@ __device__ __forceinline__ void scan_item(const SampleArgs& a, int b, int c, Chu
 #pragma unroll
     for (int q = 0; q < Q; ++q) pend |= (r.vok[q] && r.vmax[q] >= lo ? 1u : 0u) << q;
   }
+  // one walk counts the lane's candidates and stages the first kScanStage of
+  // them (final entries, in walk order) in LDS; a lane holding more walks
+  // again to write them (rare)
   uint32_t mine = 0;  // tier A count | tier B count << 16
+  uint32_t nst = 0, st_a = 0;  // staged entries, and which of them are tier A
   for (uint32_t p = pend; p; p &= p - 1) {
+    const int q = __builtin_ctz(p);
     uint32_t wv[ChunkRegs<DT, VEC>::W];
-    r.pick(__builtin_ctz(p), wv);
+    r.pick(q, wv);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const float l = ChunkRegs<DT, VEC>::decode(wv, e);
-      mine += l >= th_a ? 1u : (l >= lo ? 0x10000u : 0u);
+      if (l >= lo) {
+        const bool ta = l >= th_a;
+        mine += ta ? 1u : 0x10000u;
+        if (nst < (uint32_t)kScanStage) {
+          sh.stage[nst][threadIdx.x] =
+              ((unsigned long long)radix_key(l / rp.tp) << 32) | (uint32_t)elem_index<VEC>(base, q * VEC + e);
+          st_a |= (ta ? 1u : 0u) << nst;
+        }
+        ++nst;
+      }
     }
   }
   // wave-level reservations: one LDS atomic per wave and tier
@@ -1120,7 +1138,18 @@ __device__ __forceinline__ void scan_item(const SampleArgs& a, int b, int c, Chu
     slot_b = n_a + (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase) + ((incl - mine) >> 16);
   }
   unsigned long long* out = a.cand + ((size_t)b * a.nchunks + c) * kCandCap;
-  for (uint32_t p = mine ? pend : 0u; p; p &= p - 1) {
+  const bool restage = nst > (uint32_t)kScanStage;
+#pragma unroll
+  for (int n = 0; n < kScanStage; ++n) {
+    if (!restage && (uint32_t)n < nst) {  // the staged entries (the lane's own LDS column)
+      const bool ta = (st_a >> n) & 1u;
+      const uint32_t slot = ta ? slot_a : slot_b;
+      if (slot < (uint32_t)kCandCap) out[slot] = sh.stage[n][threadIdx.x];
+      slot_a += ta ? 1u : 0u;
+      slot_b += ta ? 0u : 1u;
+    }
+  }
+  for (uint32_t p = restage ? pend : 0u; p; p &= p - 1) {
     const int q = __builtin_ctz(p);
     uint32_t wv[ChunkRegs<DT, VEC>::W];
     r.pick(q, wv);
