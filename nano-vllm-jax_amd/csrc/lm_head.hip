@@ -184,7 +184,7 @@ __device__ __forceinline__ void finish_rows(unsigned long long* row_keys, unsign
   __shared__ int s_last;
   __syncthreads();
   if (threadIdx.x == 0) {
-    unsigned int t = atomicAdd(counter, 1u);
+    unsigned int t = ticket_add(counter);
     s_last = (t == gridDim.x - 1);
   }
   __syncthreads();

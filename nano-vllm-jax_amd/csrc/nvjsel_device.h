@@ -279,6 +279,27 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return v;
 }
 
+// Cross-block ordering of the last-block reductions.  By default an atomic
+// whose value is used (after()) orders the atomics that follow it: this rests
+// on a property of the hardware -- a device-scope atomic returns its value
+// once it is performed at the device-wide coherence point -- rather than on
+// the HIP memory model, and it avoids the release fence, which on gfx950
+// writes back the XCD's L2.  Building with -DNVJSEL_STRICT_ORDERING=1 (or
+// NVJSEL_STRICT_ORDERING=1 in the environment of build.py) takes the memory
+// model's own route instead: the ticket is an acquire-release atomic (a
+// release of everything the block wrote before it, an acquire for the block
+// that draws the last ticket).
+#ifndef NVJSEL_STRICT_ORDERING
+#define NVJSEL_STRICT_ORDERING 0
+#endif
+__device__ __forceinline__ unsigned int ticket_add(unsigned int* counter) {
+#if NVJSEL_STRICT_ORDERING
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+#else
+  return atomicAdd(counter, 1u);
+#endif
+}
+
 // An opaque 0 that the compiler must compute from `v`: placed in the address of
 // a later atomic it makes that atomic wait for the value `v` returned by an
 // earlier one.  Device-scope atomics are performed at the device-wide

@@ -2083,7 +2083,7 @@ __global__ void __launch_bounds__(kThreads) sample_onepass_kernel(SampleArgs a) 
     for (int w = 1; w < kThreads / 64; ++w) m = max_u64(m, s_key[w]);
     // every key is nonzero (its low word is ~index, index < 2^31)
     __hip_atomic_store(slots + blockIdx.x, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t t = atomicAdd(&a.row_ticket[(size_t)b * kRowPad32], 1u);
+    const uint32_t t = ticket_add(&a.row_ticket[(size_t)b * kRowPad32]);
     s_last = t == gridDim.x - 1;
   }
   __syncthreads();

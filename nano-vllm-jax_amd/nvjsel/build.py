@@ -45,7 +45,11 @@ def sources() -> list[Path]:
 
 def _compile(src: Path) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    # NVJSEL_STRICT_ORDERING=1: order the last-block reductions with the HIP
+    # memory model's acquire-release ticket instead of data dependencies
+    # (csrc/nvjsel_device.h, ticket_add)
+    extra = ["-DNVJSEL_STRICT_ORDERING=1"] if os.environ.get("NVJSEL_STRICT_ORDERING") == "1" else []
+    cmd = [HIPCC, *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stderr[-6000:]}")
