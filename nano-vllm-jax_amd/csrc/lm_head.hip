@@ -572,7 +572,9 @@ __global__ void __launch_bounds__(kGemvWaves * 64) lm_head_gemv_kernel(LmArgs a)
         }
         p[b][r] = acc;
       }
-    // transpose-reduce: after the halving rounds lane holds row `sel` only
+    // transpose-reduce: after the halving rounds lane holds row `sel` only.
+    // Rounds across lane halves and 16-lane rows are register permutes
+    // (v_permlane32/16_swap), the sums within a row DPP rotations: no LDS.
     int sel = 0;
     int mask = 32;
 #pragma unroll
@@ -583,16 +585,28 @@ __global__ void __launch_bounds__(kGemvWaves * 64) lm_head_gemv_kernel(LmArgs a)
       for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int i = 0; i < half; ++i) {
-          const float keep = upper ? p[b][i + half] : p[b][i];
-          const float send = upper ? p[b][i] : p[b][i + half];
-          p[b][i] = keep + __shfl_xor(send, mask, 64);
+          if (mask == 32) {
+            p[b][i] = xpose_add32(p[b][i], p[b][i + half]);
+          } else if (mask == 16) {
+            p[b][i] = xpose_add16(p[b][i], p[b][i + half]);
+          } else {
+            const float keep = upper ? p[b][i + half] : p[b][i];
+            const float send = upper ? p[b][i] : p[b][i + half];
+            p[b][i] = keep + __shfl_xor(send, mask, 64);
+          }
         }
       if (upper) sel += half;
     }
 #pragma unroll
     for (; mask >= 1; mask >>= 1)
 #pragma unroll
-      for (int b = 0; b < NB; ++b) p[b][0] += __shfl_xor(p[b][0], mask, 64);
+      for (int b = 0; b < NB; ++b) {
+        if (mask == 8) p[b][0] = row_ror_add<8>(p[b][0]);
+        else if (mask == 4) p[b][0] = row_ror_add<4>(p[b][0]);
+        else if (mask == 2) p[b][0] = row_ror_add<2>(p[b][0]);
+        else if (mask == 1) p[b][0] = row_ror_add<1>(p[b][0]);
+        else p[b][0] += __shfl_xor(p[b][0], mask, 64);
+      }
     const int v = v0 + sel;
     if (v < V) {
       // every lane of a row group (64 / R lanes) holds the same totals; in
@@ -1473,7 +1487,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   auto sample_epilogue = [&](int v0) NVJSEL_INLINE {
     // the two lane halves hold the same batch rows: share their maxima
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) amax[tb] = fmaxf(amax[tb], __shfl_xor(amax[tb], 32, 64));
+    for (int tb = 0; tb < 2; ++tb) amax[tb] = xor32_max(amax[tb]);
 #pragma unroll 1
     for (int tv = 0; tv < 4; ++tv) {
 #pragma unroll

@@ -311,6 +311,34 @@ __device__ __forceinline__ uint32_t after(uint64_t v) {
   return z;
 }
 
+// ---------------------------------------------------------------- cross-lane sums without LDS
+// One round of a transpose-reduction across lane halves (gfx950
+// v_permlane32_swap): lanes 0-31 get a[l] + a[l + 32], lanes 32-63 get
+// b[l - 32] + b[l] -- the values of a[l] + shfl_xor(a, 32) below and of
+// b[l] + shfl_xor(b, 32) above, bitwise (addition commutes).
+__device__ __forceinline__ float xpose_add32(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// max(v[l], v[l ^ 32]) in every lane (v_permlane32_swap of v with itself).
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// The same across 16-lane rows (v_permlane16_swap): even rows get
+// a[l] + a[l + 16], odd rows b[l - 16] + b[l].
+__device__ __forceinline__ float xpose_add16(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// v + v[(l + N) mod 16 within the row] (DPP row_ror).  Applied for N = 8, 4,
+// 2, 1 it leaves every lane of a 16-lane row with the row's sum, with the
+// same values as the xor butterfly (after the N round v has period N).
+template <int N>
+__device__ __forceinline__ float row_ror_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false));
+}
+
 // ---------------------------------------------------------------- number formats
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
