@@ -966,18 +966,39 @@ __device__ __forceinline__ unsigned long long wave_first_max(const ChunkRegs<DT,
   return key;
 }
 
-// Largest 16-bit prefix p such that at least kk lanes of the wave have
-// radix_key(v) >> 16 >= p (lanes holding no element of the row pass 0): a
-// bit-by-bit search, one compare and one popcount per step.
-__device__ __forceinline__ uint32_t wave_kth_prefix(float v, bool ok, uint32_t kk) {
-  const uint32_t k16 = ok ? (radix_key(v) >> 16) : 0u;
-  uint32_t p = 0;
-#pragma unroll
-  for (int bit = 15; bit >= 0; --bit) {
-    const uint32_t c = p | (1u << bit);
-    if ((uint32_t)__popcll(__ballot(k16 >= c)) >= kk) p = c;
+// The wave's 64 values sorted descending across lanes (lane t ends with the
+// t-th largest): a bitonic network of 21 compare-exchange rounds, partners
+// lane ^ j by ds_swizzle (j < 32) or a half-wave permute (j = 32).
+template <int J>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+  if constexpr (J == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (threadIdx.x & 32) ? r[0] : r[1];
+  } else {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (J << 10) | 0x1F);
   }
-  return p;
+}
+template <int K, int J>
+__device__ __forceinline__ uint32_t sort_round(uint32_t v, int lane) {
+  const uint32_t o = lane_xor<J>(v);
+  // blocks of K lanes alternate direction so that block pairs merge into
+  // descending runs; the lower lane of a pair keeps the larger in a
+  // descending block
+  const bool desc = (lane & K) == 0, lower = (lane & J) == 0;
+  return (desc == lower) ? max(v, o) : min(v, o);
+}
+__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v) {
+  const int lane = threadIdx.x & 63;
+  v = sort_round<2, 1>(v, lane);
+  v = sort_round<4, 2>(v, lane);   v = sort_round<4, 1>(v, lane);
+  v = sort_round<8, 4>(v, lane);   v = sort_round<8, 2>(v, lane);   v = sort_round<8, 1>(v, lane);
+  v = sort_round<16, 8>(v, lane);  v = sort_round<16, 4>(v, lane);  v = sort_round<16, 2>(v, lane);
+  v = sort_round<16, 1>(v, lane);
+  v = sort_round<32, 16>(v, lane); v = sort_round<32, 8>(v, lane);  v = sort_round<32, 4>(v, lane);
+  v = sort_round<32, 2>(v, lane);  v = sort_round<32, 1>(v, lane);
+  v = sort_round<64, 32>(v, lane); v = sort_round<64, 16>(v, lane); v = sort_round<64, 8>(v, lane);
+  v = sort_round<64, 4>(v, lane);  v = sort_round<64, 2>(v, lane);  v = sort_round<64, 1>(v, lane);
+  return v;
 }
 
 // One (row b, chunk c) item of the scan; r holds its raw words.  Block-uniform.
@@ -1017,18 +1038,17 @@ __device__ __forceinline__ void scan_item(const SampleArgs& a, int b, int c, Chu
 #pragma unroll
     for (int q = 1; q < Q; ++q)
       if (r.vok[q]) tv = fmaxf(tv, r.vmax[q]);
-    wfloor = kk ? wave_kth_prefix(tv, r.vok[0], kk) << 16 : 0xFFFFFFFFu;
-    // the wave's kTops largest lane maxima (-inf fills), for the row floor
-    float v = r.vok[0] ? tv : -INFINITY;
+    // the lane maxima as radix keys (lanes holding no element of the row: 0,
+    // below every value), sorted: lane t holds the t-th largest.  The
+    // kk-th largest gives the wave floor (its top 16 bits: the largest
+    // prefix that kk lane maxima reach), lanes 0..kTopsPub-1 publish the
+    // largest lane maxima, lane kTops-1 the kTops-th (-inf fills)
+    const uint32_t sk = wave_sort_desc(r.vok[0] ? radix_key(tv) : 0u);
+    wfloor = kk ? ((uint32_t)__builtin_amdgcn_readlane((int)sk, (int)kk - 1) >> 16) << 16 : 0xFFFFFFFFu;
+    const float sv = sk > 0x007FFFFFu ? radix_value(sk) : -INFINITY;
     float* tops = a.lane_tops + (((size_t)b * a.nchunks + c) * (kThreads / 64) + wave) * kTopsPub;
-#pragma unroll
-    for (int t = 0; t < kTops; ++t) {
-      const float mx = wave_max_f32(v);
-      if (lane == 0 && t < kTopsPub) tops[t] = mx;
-      if (lane == 0 && t == kTops - 1) sh.wtop[wave] = mx;
-      const unsigned long long hm = __ballot(v == mx);
-      if (lane == __ffsll((long long)hm) - 1) v = -INFINITY;
-    }
+    if (lane < kTopsPub) tops[lane] = sv;
+    if (lane == kTops - 1) sh.wtop[wave] = sv;
   } else if (topk && lane < kTopsPub) {
     if (lane == 0) sh.wtop[wave] = -INFINITY;
     a.lane_tops[(((size_t)b * a.nchunks + c) * (kThreads / 64) + wave) * kTopsPub + lane] = -INFINITY;
