@@ -53,3 +53,54 @@ def test_noalloc_rejects_batch_beyond_scratch():
     rc = _noalloc(lib)(0x1000, _lib.BF16, 0x1000, _lib.BF16, _lib.W_VH, 4097, 1024, 1000, 1, 0x1000, None, None)
     assert rc == -2
     assert b"4096" in lib.nvjsel_last_error()
+
+
+_CAPTURE_SCRIPT = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + "/nano-vllm-jax_amd")
+from nvjsel import _lib
+lib = _lib.load()
+rng = np.random.default_rng(5)
+B, H, V = 8, 1024, 30_000
+W = torch.from_numpy(rng.standard_normal((V, H)).astype(np.float32) * 0.02).cuda().to(torch.bfloat16)
+hs = [torch.from_numpy(rng.standard_normal((B, H)).astype(np.float32)).cuda().to(torch.bfloat16) for _ in range(3)]
+h = hs[0].clone()
+ids = torch.full((B,), -1, dtype=torch.int32, device="cuda")
+s = torch.cuda.Stream()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=s):
+    # the process's first no-alloc call: the scratch address is looked up
+    # here, under capture; nothing but the LM-head kernels is recorded
+    rc = lib.nvjsel_lm_head_top1_noalloc(h.data_ptr(), _lib.BF16, W.data_ptr(), _lib.BF16, _lib.W_VH, B, H, V, 1,
+                                         ids.data_ptr(), None, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.nvjsel_last_error()
+ws = torch.zeros(lib.nvjsel_lm_head_workspace_size(B), dtype=torch.uint8, device="cuda")
+for rep in range(6):
+    h.copy_(hs[rep % 3])
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    ref = torch.full((B,), -1, dtype=torch.int32, device="cuda")
+    _lib.call("nvjsel_lm_head_top1", h.data_ptr(), _lib.BF16, W.data_ptr(), _lib.BF16, _lib.W_VH, B, H, V, 1,
+              ref.data_ptr(), None, ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ref), (rep, ids.tolist(), ref.tolist())
+print("capture ok")
+"""
+
+
+def test_noalloc_first_call_under_graph_capture(tmp_path):
+    """A fresh process whose FIRST no-alloc call is made under HIP graph
+    capture: the scratch array must already be zero (no fill is recorded),
+    and every replay -- with the process's own eager calls between them --
+    must equal the workspace entry point's ids."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = tmp_path / "capture_first_call.py"
+    script.write_text(_CAPTURE_SCRIPT)
+    r = subprocess.run([sys.executable, str(script), root], capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert "capture ok" in r.stdout
