@@ -1078,18 +1078,23 @@ __device__ __forceinline__ void scan_item(const SampleArgs& a, int b, int c, Chu
     if (fabsf(cx) < 0x1p25f) {  // finite and on the grid
       tb = topp_ibin(cx);
       const float lowb = topp_edge(tb - (kToppBins - 1));
+      auto hist = [&](auto unit) NVJSEL_INLINE {
 #pragma unroll
-      for (int q = 0; q < Q; ++q) {
-        if (!r.vok[q]) continue;
+        for (int q = 0; q < Q; ++q) {
+          if (!r.vok[q]) continue;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float x = r.elem(q, e) / rp.tp;
-          if (x >= lowb) {
-            const int ib = topp_ibin(x);
-            atomicAdd(&sh.topp_h[tb - ib], edge_mass17(x, ib));
+          for (int e = 0; e < VEC; ++e) {
+            const float x = decltype(unit)::value ? r.elem(q, e) : r.elem(q, e) / rp.tp;
+            if (x >= lowb) {
+              const int ib = topp_ibin(x);
+              atomicAdd(&sh.topp_h[tb - ib], edge_mass17(x, ib));
+            }
           }
         }
-      }
+      };
+      // (block-uniform) x / 1 == x bitwise: T' = 1 skips the division
+      if (rp.tp == 1.0f) hist(std::true_type{});
+      else hist(std::false_type{});
     }
     lds_barrier();
     uint32_t* ch = a.topp_chunk_hist + ((size_t)b * a.nchunks + c) * kToppBins;
@@ -1901,11 +1906,12 @@ __device__ __forceinline__ void gumbel_item(const SampleArgs& a, uint32_t item, 
   const unsigned long long seen = load_row_best(rk);
   const float s_cur = prune_level(seen);
   uint32_t act = 0;
+  if (rp.tp != 1.0f) {  // (block-uniform) x / 1 == x bitwise: T' = 1 skips the division
 #pragma unroll
-  for (int j = 0; j < kGumbelEPT; ++j) {
-    x[j] = x[j] / rp.tp;
-    act |= (((valid >> j) & 1u) && radix_key(x[j]) >= tau ? 1u : 0u) << j;
+    for (int j = 0; j < kGumbelEPT; ++j) x[j] = x[j] / rp.tp;
   }
+#pragma unroll
+  for (int j = 0; j < kGumbelEPT; ++j) act |= (((valid >> j) & 1u) && radix_key(x[j]) >= tau ? 1u : 0u) << j;
   if (ib != INT_MIN) {  // (block-uniform) top-p row: collect the crossing bin
     const float lo = topp_edge(ib), hi = topp_edge(ib + 1);
     uint32_t in_bin = 0;
