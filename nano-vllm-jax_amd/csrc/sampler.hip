@@ -2150,6 +2150,7 @@ __global__ void __launch_bounds__(kThreads) sample_onepass_kernel(SampleArgs a) 
 struct ToppFinishShared {
   DescShared d;
   unsigned long long red[kThreads / 64];
+  float fs[kToppCap];  // the bin elements' fast scores (-inf: cannot win)
   union {
     unsigned long long v[kToppCap];
     HeavyShared hv;
@@ -2159,23 +2160,38 @@ struct ToppFinishShared {
 __global__ void __launch_bounds__(kThreads) sample_finish_kernel(SampleArgs a) {
   __shared__ ToppFinishShared sh;
   const int b = blockIdx.x;
+  // the row's words, loaded together (one memory round trip, not a chain of
+  // them); those a row's state does not use are ignored
   const int state = a.row_state[b];
   unsigned long long* rk = &a.row_key[(size_t)b * kRowPad8];
+  const unsigned long long above = load_row_best(rk);
+  const int ib = a.row_ib[b];
+  const uint32_t n = a.topp_n[b];
   if (state == STATE_NEEDS_GUMBEL) {  // the gumbel pass left the row's best key
-    if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)load_row_best(rk));
+    if (threadIdx.x == 0) a.out_ids[b] = (int32_t)(~(uint32_t)above);
     return;
   }
   if (state != STATE_TOPP) return;
   const RowParams rp = row_params(a, b);
-  const int ib = a.row_ib[b];
-  const uint32_t n = a.topp_n[b];
-  const unsigned long long above = load_row_best(rk);
   const float s_cur = prune_level(above);
   const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
   const float lo = topp_edge(ib), hi = topp_edge(ib + 1);
   unsigned long long best = 0;
   if (n <= (uint32_t)kToppCap) {
-    for (int e = threadIdx.x; e < (int)n; e += kThreads) sh.v[e] = a.topp_cand[(size_t)b * kToppCap + e];
+    const unsigned long long* cand = a.topp_cand + (size_t)b * kToppCap;
+    for (int e0 = 0; e0 < (int)n; e0 += 8 * kThreads) {  // eight loads in flight per lane
+      unsigned long long c[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = e0 + j * kThreads + (int)threadIdx.x;
+        c[j] = e < (int)n ? cand[e] : 0ull;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = e0 + j * kThreads + (int)threadIdx.x;
+        if (e < (int)n) sh.v[e] = c[j];
+      }
+    }
     __syncthreads();
     const uint32_t tau = lds_desc<true>(sh.d, sh.v, (int)n, a.row_target[b], ib);
     if (a.dbg_tau) {  // nvjsel_debug_sample_topp: the bin's kept weight joins the mass above it
@@ -2190,27 +2206,52 @@ __global__ void __launch_bounds__(kThreads) sample_finish_kernel(SampleArgs a) {
         a.dbg_mass[b] += (double)K * a.dbg_scale[b];
       }
     }
-    // fast scores first; exact ones only within the fast path's error of the
-    // block maximum, and only if that maximum can beat the score above the bin
+    // fast scores first, four Threefry chains per lane (a bin at bf16
+    // resolution is often one value repeated thousands of times, all kept),
+    // kept in LDS; exact ones only within the fast path's error of the block
+    // maximum, and only if that maximum can beat the score above the bin
     float fm = -INFINITY;
-    for (int e = threadIdx.x; e < (int)n; e += kThreads) {
-      const unsigned long long ce = sh.v[e];
-      const uint32_t kk = (uint32_t)(ce >> 32);
-      const float xv = radix_value(kk);
-      if (kk < tau || xv + NVJSEL_GUMBEL_MAX < s_cur) continue;
-      fm = fmaxf(fm, xv + fast_noise(a, b, key, (int)(uint32_t)ce));
+    for (int e0 = 0; e0 < (int)n; e0 += 4 * kThreads) {  // block-uniform trip count
+      int e[4];
+      float xv[4];
+      bool live[4], any = false;
+      uint32_t idx[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        e[j] = e0 + j * kThreads + (int)threadIdx.x;
+        const unsigned long long ce = e[j] < (int)n ? sh.v[e[j]] : 0ull;
+        const uint32_t kk = (uint32_t)(ce >> 32);
+        xv[j] = radix_value(kk);
+        idx[j] = (uint32_t)ce;
+        live[j] = e[j] < (int)n && kk >= tau && !(xv[j] + NVJSEL_GUMBEL_MAX < s_cur);
+        any |= live[j];
+      }
+      float g[4];
+      if (a.noise) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) g[j] = live[j] ? a.noise[(size_t)b * a.V + idx[j]] : 0.0f;
+      } else if (__any(any)) {  // the asm block runs with the whole wave
+        uint32_t bits[4];
+        random_bits32_n<4>(key, idx, bits);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) g[j] = gumbel_fast_from_bits(bits[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (e[j] < (int)n) {
+          const float f = live[j] ? xv[j] + g[j] : -INFINITY;
+          sh.fs[e[j]] = f;
+          fm = fmaxf(fm, f);
+        }
     }
-    fm = unord_f32((uint32_t)block_max_u64(ord_f32(fm), sh.red));
+    fm = unord_f32((uint32_t)block_max_u64(ord_f32(fm), sh.red));  // (its barrier orders the fs stores)
     const float margin = 1e-3f + fabsf(fm) * 4.8e-7f;
     if (fm + margin >= s_cur) {
       for (int e = threadIdx.x; e < (int)n; e += kThreads) {
+        if (!(sh.fs[e] >= fm - margin)) continue;  // -inf entries: below tau or pruned
         const unsigned long long ce = sh.v[e];
-        const uint32_t kk = (uint32_t)(ce >> 32);
-        const float xv = radix_value(kk);
-        if (kk < tau || xv + NVJSEL_GUMBEL_MAX < s_cur) continue;
         const uint32_t i = (uint32_t)ce;
-        if (xv + fast_noise(a, b, key, (int)i) < fm - margin) continue;
-        best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
+        best = max_u64(best, argmax_key(radix_value((uint32_t)(ce >> 32)) + exact_noise(a, b, key, (int)i), i));
       }
     }
   } else {
