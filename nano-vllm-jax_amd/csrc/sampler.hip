@@ -746,7 +746,7 @@ __device__ int topk_sorted_survivors(const SampleArgs& a, int b, const RowParams
 // the scan's candidates.  Returns false (nothing written) when
 // topk_sorted_survivors cannot settle the row.
 __device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp, float m, const TopkPrefetch& pf,
-                                FinishShared& s) {
+                                const TfKey& key, FinishShared& s) {
   const int n = topk_sorted_survivors(a, b, rp, pf, s);
   if (n < 0) return false;
   // kept: every survivor >= the k-th largest (ties kept) -- a prefix
@@ -789,7 +789,6 @@ __device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp,
     }
   }
   // exact Gumbel-max over the survivors >= tau
-  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
   unsigned long long best = 0;
   for (int i = threadIdx.x; i < nk; i += kThreads) {
     const unsigned long long ce = s.srt[i];
@@ -1744,14 +1743,24 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
   const int b = blockIdx.x;
   const RowParams rp = row_params(a, b);
   const int NC = a.nchunks;
+  // what every row class may need, loaded at once with the row's parameters
+  // (not after its class is known: one memory round trip less on the row's
+  // chain of dependent steps); unused words are ignored
+  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
+  TopkPrefetch pf;
+  topk_prefetch(a, b, pf);
+  unsigned long long mk = 0;
+  for (int c = threadIdx.x; c < NC; c += blockDim.x) {
+    const unsigned long long ck = a.chunk_max[(size_t)b * NC + c];
+    s.ck[c] = ck;
+    mk = max_u64(mk, ck);
+  }
   if (rp.mode == ROW_FULL) {
     // seed the row's best with the exact scores of the chunk maxima: a prune
     // level for the gumbel kernel before any of its blocks has run
-    const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
     unsigned long long best = 0;
     for (int c = threadIdx.x; c < NC; c += blockDim.x) {
-      const unsigned long long ck = a.chunk_max[(size_t)b * NC + c];
-      s.ck[c] = ck;
+      const unsigned long long ck = s.ck[c];
       const uint32_t i = ~(uint32_t)ck;
       const float xv = chunk_max_x(rp, ck);
       best = max_u64(best, argmax_key(xv + exact_noise(a, b, key, (int)i), i));
@@ -1767,8 +1776,6 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
   }
   const bool fast_topk = rp.mode == ROW_FILTER && rp.k > 0 && rp.k <= kFastK;
   const bool topp_only = rp.mode == ROW_FILTER && rp.k == 0 && rp.p < 1.0f;
-  TopkPrefetch pf;
-  if (fast_topk) topk_prefetch(a, b, pf);
   int tbm = INT_MIN;  // top-p-only rows: the chunks' top grid bins, loaded with the maxima
   if (topp_only)
     for (int c = threadIdx.x; c < NC; c += kThreads) {
@@ -1776,12 +1783,6 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
       s.tb[c] = t;
       tbm = max(tbm, t);
     }
-  unsigned long long mk = 0;
-  for (int c = threadIdx.x; c < NC; c += blockDim.x) {
-    const unsigned long long ck = a.chunk_max[(size_t)b * NC + c];
-    s.ck[c] = ck;
-    mk = max_u64(mk, ck);
-  }
   mk = block_max_u64(mk, s.red);
   if (rp.mode == ROW_GREEDY) {  // the row's first maximum
     if (threadIdx.x == 0) { a.out_ids[b] = (int32_t)(~(uint32_t)mk); a.row_state[b] = STATE_DONE; }
@@ -1803,7 +1804,7 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     if (threadIdx.x == 0) { a.out_ids[b] = (int32_t)(~(uint32_t)ans); a.row_state[b] = STATE_DONE; }
     return;
   }
-  if (fast_topk && finish_topk_row(a, b, rp, m, pf, s.fin)) {
+  if (fast_topk && finish_topk_row(a, b, rp, m, pf, key, s.fin)) {
     if (threadIdx.x == 0) a.row_state[b] = STATE_DONE;
     return;
   }
@@ -1863,7 +1864,6 @@ __global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a) {
     a.dbg_scale[b] = s.tx.scale;
   }
   // seed the row's best with the exact scores of the chunk maxima >= tau
-  const TfKey key = tf_key(a.keys[2 * b], a.keys[2 * b + 1]);
   unsigned long long best = 0;
   for (int c = threadIdx.x; c < NC; c += kThreads) {
     const unsigned long long ck = s.ck[c];
