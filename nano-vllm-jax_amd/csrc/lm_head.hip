@@ -1315,7 +1315,10 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   __shared__ float gqa[SMP ? NW : 1][QC];
   __shared__ uint32_t gqv[SMP ? NW : 1][QC];
   __shared__ unsigned long long gqbest[SMP ? NW : 1][SMP ? 128 : 1];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index in a scalar register and the lane from mbcnt: nothing
+  // derived from threadIdx.x has to stay live (or spill) across the loops
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = (int)__lane_id();
+  const int tid = wave * 64 + lane;
   const int vi = wave % VH, bj = wave / VH;
   const int B = a.B, V = a.V, H = a.H;
   const uint16_t* W = (const uint16_t*)a.W;
