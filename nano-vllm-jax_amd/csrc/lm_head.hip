@@ -982,6 +982,8 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
   };
 
   __shared__ float pre_ss[KSPLIT][ROWS];
+  // prologue with a 16-byte-aligned bf16 pre-norm hidden (block-uniform)
+  const bool raw16 = PN && a.hidden_dtype == DT_BF16 && (((uintptr_t)a.hidden) & 15) == 0;
   if (gemm) {
     const int brow = nb * 16 + r;
     if constexpr (!PN && NS == 1) {
@@ -1005,14 +1007,31 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
       // RMSNorm prologue, pass 1: this lane's sum of squares; the four lanes
       // of a row combine by butterfly, the k-split waves through LDS
       float ss = 0.0f;
-#pragma unroll 4
-      for (int kk = 0; kk < KPW; ++kk)
+      const size_t rb = (size_t)(brow < B ? brow : 0) * 1024;  // rows past B: any row, unused
+      if (raw16) {
+        // bf16 hidden: the raw fragments go straight into hb (all loads in
+        // flight at once); pass 2 normalises them in place
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x = brow < B ? load_as_f32(a.hidden, a.hidden_dtype,
-                                                 (size_t)brow * 1024 + (ks * KPW + kk) * 32 + g * 8 + e) : 0.0f;
-          ss = fmaf(x, x, ss);
+        for (int kk = 0; kk < KPW; ++kk)
+          hb[0][kk] = *(const u32x4_t*)((const uint16_t*)a.hidden + rb + (ks * KPW + kk) * 32 + g * 8);
+#pragma unroll
+        for (int kk = 0; kk < KPW; ++kk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float lo = __uint_as_float(hb[0][kk][e] << 16), hi = __uint_as_float(hb[0][kk][e] & 0xFFFF0000u);
+            ss = fmaf(lo, lo, ss);
+            ss = fmaf(hi, hi, ss);
+          }
+      } else {
+#pragma unroll 4
+        for (int kk = 0; kk < KPW; ++kk) {
+          float x[8];
+          load8_as_f32(a.hidden, a.hidden_dtype, rb + (ks * KPW + kk) * 32 + g * 8, x);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
         }
+      }
+      if (brow >= B) ss = 0.0f;
       ss += __shfl_xor(ss, 16, 64);
       ss += __shfl_xor(ss, 32, 64);
       if (g == 0) pre_ss[ks][brow] = ss;
@@ -1043,17 +1062,26 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
 #pragma unroll
     for (int s2 = 0; s2 < KSPLIT; ++s2) tot += pre_ss[s2][brow];
     const float inv = prenorm_inv(a, tot);
+    // compile-time k-steps (a plain loop was left partly rolled, which put
+    // the fragment array in scratch memory for the whole tile loop)
+    static_for<KPW>([&](auto KK) NVJSEL_INLINE {
+      constexpr int kk = decltype(KK)::value;
+      const int k0 = (ks * KPW + kk) * 32 + g * 8;
+      float v[8], w[8];
+      if (raw16) {
 #pragma unroll
-    for (int kk = 0; kk < KPW; ++kk) {
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int k = (ks * KPW + kk) * 32 + g * 8 + e;
-        const float x = brow < B ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)brow * 1024 + k) : 0.0f;
-        v[e] = brow < B ? prenorm_apply(a, x, inv, k) : 0.0f;
+        for (int e = 0; e < 4; ++e) {
+          v[2 * e] = __uint_as_float(hb[0][kk][e] << 16);
+          v[2 * e + 1] = __uint_as_float(hb[0][kk][e] & 0xFFFF0000u);
+        }
+      } else {
+        load8_as_f32(a.hidden, a.hidden_dtype, (size_t)(brow < B ? brow : 0) * 1024 + k0, v);
       }
+      load8_as_f32(a.norm_w, a.norm_dtype, (size_t)k0, w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = brow < B ? prenorm_apply_w(a, v[e], inv, w[e]) : 0.0f;
       split_terms<NS>(v, hb, kk);
-    }
+    });
   };
 
   if (gemm) {

@@ -366,6 +366,33 @@ __device__ __forceinline__ float load_as_f32(const void* p, int dtype, size_t i)
   return f16_to_f32(((const uint16_t*)p)[i]);
 }
 
+// Elements i .. i + 7 (i a multiple of 8) as f32: one 16-byte load for
+// 16-bit types, two for f32, where the base pointer is 16-byte aligned
+// (block-uniform); element loads otherwise.
+__device__ __forceinline__ void load8_as_f32(const void* p, int dtype, size_t i, float (&v)[8]) {
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  if ((((uintptr_t)p) & 15) == 0) {
+    if (dtype == DT_F32) {
+      const u32x4v w0 = *((const u32x4v*)((const float*)p + i)), w1 = *((const u32x4v*)((const float*)p + i) + 1);
+      const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(w[e]);
+      return;
+    }
+    const u32x4v w4 = *(const u32x4v*)((const uint16_t*)p + i);
+    const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t lo = (uint16_t)(w[e] & 0xFFFFu), hi = (uint16_t)(w[e] >> 16);
+      v[2 * e] = dtype == DT_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+      v[2 * e + 1] = dtype == DT_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+    }
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = load_as_f32(p, dtype, i + e);
+}
+
 // JAX's jnp.maximum(T, 1e-6) propagates NaN (fmaxf would not).
 __device__ __forceinline__ float temp_floor(float t) {
   return (t != t) ? t : fmaxf(t, 1e-6f);

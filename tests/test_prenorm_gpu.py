@@ -53,6 +53,34 @@ def test_prenorm_greedy(batch, H, hidden_dtype, act_dtype):
                  f"prenorm B={batch} H={H} {hidden_dtype}->{act_dtype}")
 
 
+@pytest.mark.parametrize("batch,hidden_dtype,act_dtype", [
+    (12, "bf16", "bf16"),  # tile kernel, hidden one element past a 16-byte boundary: element loads
+    (40, "f16", "bf16"),   # tile kernel, f16 hidden: 16-byte loads converted per element
+    (7, "bf16", "f32"),    # tile kernel, three-term activations from an unaligned bf16 hidden
+])
+def test_prenorm_tile_unaligned_and_f16_hidden(batch, hidden_dtype, act_dtype):
+    """The tile kernel's prologue loads a 16-byte-aligned bf16 hidden straight
+    into its fragment registers and any other hidden eight elements at a time
+    (16-byte loads when aligned, element loads when not)."""
+    rng = np.random.default_rng(500 + batch)
+    H, V = 1024, 5003
+    x, nw, W = _inputs(rng, batch, H, V, hidden_dtype)
+    xt = torch.from_numpy(x).to(TORCH[hidden_dtype]).cuda()
+    if hidden_dtype == "bf16":  # the same rows one element into a buffer: an unaligned base pointer
+        buf = torch.zeros(batch * H + 1, dtype=xt.dtype, device="cuda")
+        buf[1:] = xt.reshape(-1)
+        xt = buf[1:].view(batch, H)
+        assert xt.data_ptr() % 16 != 0
+    ids = nvjsel.lm_head_greedy_top1_hip(
+        xt, torch.from_numpy(W).to(torch.bfloat16).cuda(), weight_layout="vh",
+        norm_weight=torch.from_numpy(nw).cuda(), rms_norm_eps=1e-6, act_dtype=TORCH[act_dtype])
+    torch.cuda.synchronize()
+    xin = sel.lm_head_input(x, nw, 1e-6, hidden_dtype=hidden_dtype, act_dtype=act_dtype)
+    z = sel.lm_head_logits(xin, W)
+    check_greedy(ids.cpu().numpy(), z, RC.get((act_dtype, "bf16"), 0),
+                 f"prenorm tile B={batch} {hidden_dtype}->{act_dtype}")
+
+
 @pytest.mark.parametrize("batch,act_dtype", [(1, "bf16"), (2, "f32"), (16, "bf16"), (24, "bf16"), (64, "bf16"), (9, "f32")])
 def test_prenorm_fused_sample(batch, act_dtype):
     rng = np.random.default_rng(300 + batch)
