@@ -994,15 +994,14 @@ __global__ void __launch_bounds__((GW + NB * EPM) * 64) lm_head_tile_kernel(LmAr
         hb[0][kk] = brow < B ? *(const u32x4_t*)(hp + kb * 32 + g * 8) : u32x4_t{0u, 0u, 0u, 0u};
       }
     } else if constexpr (!PN) {
-#pragma unroll
-      for (int kk = 0; kk < KPW; ++kk) {
+      static_for<KPW>([&](auto KK) NVJSEL_INLINE {
+        constexpr int kk = decltype(KK)::value;
         float v[8];
+        load8_as_f32(a.hidden, a.hidden_dtype, (size_t)(brow < B ? brow : 0) * 1024 + (ks * KPW + kk) * 32 + g * 8, v);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          v[e] = brow < B ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)brow * 1024 + (ks * KPW + kk) * 32 + g * 8 + e)
-                          : 0.0f;
+        for (int e = 0; e < 8; ++e) v[e] = brow < B ? v[e] : 0.0f;
         split_terms<NS>(v, hb, kk);
-      }
+      });
     } else {
       // RMSNorm prologue, pass 1: this lane's sum of squares; the four lanes
       // of a row combine by butterfly, the k-split waves through LDS
