@@ -467,9 +467,9 @@ __global__ void __launch_bounds__(kGemvWaves * 64) lm_head_gemv_kernel(LmArgs a)
                                 : u32x4_t{0u, 0u, 0u, 0u};
         hp[b][j][0] = v.x; hp[b][j][1] = v.y; hp[b][j][2] = v.z; hp[b][j][3] = v.w;
       } else {
+        load8_as_f32(a.hidden, a.hidden_dtype, (size_t)(b < B ? b : 0) * H + j * 512 + lane * 8, hv[b][j]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          hv[b][j][e] = (b < B) ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)b * H + j * 512 + lane * 8 + e) : 0.0f;
+        for (int e = 0; e < 8; ++e) hv[b][j][e] = b < B ? hv[b][j][e] : 0.0f;
       }
     }
   // RMSNorm prologue: its operands are requested with the hidden, and it runs
@@ -477,9 +477,7 @@ __global__ void __launch_bounds__(kGemvWaves * 64) lm_head_gemv_kernel(LmArgs a)
   float nwv[KJ][8] = {};
   if (a.prenorm) {
 #pragma unroll
-    for (int j = 0; j < KJ; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) nwv[j][e] = load_as_f32(a.norm_w, a.norm_dtype, j * 512 + lane * 8 + e);
+    for (int j = 0; j < KJ; ++j) load8_as_f32(a.norm_w, a.norm_dtype, (size_t)(j * 512 + lane * 8), nwv[j]);
   }
   auto finish_prenorm = [&]() NVJSEL_INLINE {
     {
