@@ -291,9 +291,9 @@ lm_head_mfma_kernel(LmArgs a) {
     const int n = f % BP;
     const int kq = f / BP;
     float v[8];
+    load8_as_f32(a.hidden, a.hidden_dtype, (size_t)(n < B ? n : 0) * H + kq * 8, v);
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      v[j] = (n < B) ? load_as_f32(a.hidden, a.hidden_dtype, (size_t)n * H + kq * 8 + j) : 0.0f;
+    for (int j = 0; j < 8; ++j) v[j] = n < B ? v[j] : 0.0f;
 #pragma unroll
     for (int s = 0; s < NSPLIT; ++s) {
       uint32_t bits[8];
