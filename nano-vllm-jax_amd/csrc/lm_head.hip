@@ -1320,15 +1320,20 @@ __device__ __forceinline__ void gemm_finish_rows(const LmArgs& a, unsigned long 
 }
 
 
-template <int MODE, int BV>
+// NS = 1: bf16 hidden.  NS = 3: f32 hidden, each value split exactly into
+// three bf16 terms as it is staged into LDS (split_terms), and three MFMAs
+// per fragment pair (fp32 products and sums, as the tile kernel's NS = 3).
+template <int MODE, int BV, int NS>
 __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a) {
-  constexpr int Q = kGemmKC / 8;  // 16-byte columns per row and stage
+  constexpr int Q = kGemmKC / 8;  // 8-element columns per row and stage
   constexpr int VH = BV / 128;  // 128-row vocabulary parts; 4 batch quarters each
   constexpr int NT = VH * 4 * 64;  // threads
-  constexpr int PA = Q * BV / NT, PB = Q * kGemmBB / NT;  // 16 B load pieces per thread (W, hidden)
+  constexpr int PA = Q * BV / NT, PB = Q * kGemmBB / NT;  // 8-element load pieces per thread (W, hidden)
+  constexpr int HB = NS == 1 ? 1 : 2;  // 16-byte loads per hidden piece
   static_assert(PA == 2, "two W pieces per thread and stage");
+  static_assert(NS == 1 || (NS == 3 && MODE != MODE_SAMPLE), "f32 hidden: greedy and logits modes");
   __shared__ u32x4_t As[2][Q * BV];
-  __shared__ u32x4_t Bs[2][Q * kGemmBB];
+  __shared__ u32x4_t Bs[2][NS][Q * kGemmBB];
   __shared__ unsigned long long kred[VH][kGemmBB];
   // sample mode: per-wave queue of entries that may be their row's maximum
   // (scaled logit, approximate score, vocab << 7 | tb << 6 | lane) and the
@@ -1347,7 +1352,6 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   const int vi = wave % VH, bj = wave / VH;
   const int B = a.B, V = a.V, H = a.H;
   const uint16_t* W = (const uint16_t*)a.W;
-  const uint16_t* X = (const uint16_t*)a.hidden;
   const int ntiles = (V + BV - 1) / BV;
   const int nkc = H / kGemmKC;
   const int my_tiles = blockIdx.x < ntiles ? (ntiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
@@ -1369,13 +1373,14 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
     // rows >= B repeat row B - 1: a fixed count of loads in flight and no
     // select on the loaded data (which would make the compiler wait for it
     // early); their batch columns are never read
-    xp[i] = (const u32x4_t*)(X + (size_t)min(row, B - 1) * H) + q;
+    xp[i] = NS == 1 ? (const u32x4_t*)((const uint16_t*)a.hidden + (size_t)min(row, B - 1) * H) + q
+                    : (const u32x4_t*)((const float*)a.hidden + (size_t)min(row, B - 1) * H) + 2 * q;
   }
   // Two register sets: stages s+2 and s+3 (W and hidden) are in flight while
   // stage s is multiplied.  Loads past the last stage re-read it, so every
   // path has the same loads in flight and each LDS store waits for exactly
   // its own stage.
-  u32x4_t RA[2][PA], RB[2][PB];
+  u32x4_t RA[2][PA], RB[2][PB][HB];
   auto stage_of = [&](int st, int& v0, int& kc) NVJSEL_INLINE {
     st = st < S ? st : S - 1;
     const int t = st / nkc;
@@ -1397,14 +1402,31 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
     int v0, kc;
     stage_of(st, v0, kc);
 #pragma unroll
-    for (int i = 0; i < PB; ++i) RB[e][i] = xp[i][kc * Q];
+    for (int i = 0; i < PB; ++i)
+#pragma unroll
+      for (int j = 0; j < HB; ++j) RB[e][i][j] = xp[i][kc * Q * HB + j];
   };
   auto lstore = [&](auto set, auto buf) NVJSEL_INLINE {
     constexpr int e = decltype(set)::value, f = decltype(buf)::value;
 #pragma unroll
     for (int i = 0; i < PA; ++i) As[f][aslot[i]] = RA[e][i];
 #pragma unroll
-    for (int i = 0; i < PB; ++i) Bs[f][bslot[i]] = RB[e][i];
+    for (int i = 0; i < PB; ++i) {
+      if constexpr (NS == 1) {
+        Bs[f][0][bslot[i]] = RB[e][i][0];
+      } else {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = __uint_as_float(RB[e][i][0][j]);
+          v[4 + j] = __uint_as_float(RB[e][i][1][j]);
+        }
+        u32x4_t t3[NS][1];
+        split_terms<NS>(v, t3, 0);
+#pragma unroll
+        for (int t = 0; t < NS; ++t) Bs[f][t][bslot[i]] = t3[t][0];
+      }
+    }
   };
   // 32 x 32 tiles: 4 (vocab) x 2 (batch) per wave
   const int h = lane >> 5, c32 = lane & 31;
@@ -1422,14 +1444,18 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
 #pragma unroll
     for (int ks = 0; ks < kGemmKC / 16; ++ks) {
       const int q = ks * 2 + h, sw = q << 1;
-      u32x4_t bf[2];
+      u32x4_t bf[NS][2];
 #pragma unroll
-      for (int tb = 0; tb < 2; ++tb) bf[tb] = Bs[f][q * kGemmBB + ((bj * 64 + tb * 32 + c32) ^ sw)];
+      for (int t = 0; t < NS; ++t)
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) bf[t][tb] = Bs[f][t][q * kGemmBB + ((bj * 64 + tb * 32 + c32) ^ sw)];
 #pragma unroll
       for (int tv = 0; tv < 4; ++tv) {
         const u32x4_t af = As[f][q * BV + ((vi * 128 + tv * 32 + c32) ^ sw)];
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) acc[tv][tb] = mfma32x32x16_bf16(af, bf[tb], acc[tv][tb]);
+        for (int t = 0; t < NS; ++t)
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb) acc[tv][tb] = mfma32x32x16_bf16(af, bf[t][tb], acc[tv][tb]);
       }
     }
   };
@@ -1620,12 +1646,12 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
 // 185 us at B = 256, V = 248320) or 128 (4 waves, two blocks per CU: 195 us)
 static constexpr int kGemmBV = 256;
 static constexpr int kGemmBpc = 256 / kGemmBV;  // blocks per CU of the blocked GEMM
-template <int MODE>
+template <int MODE, int NS>
 static int launch_gemm(const LmArgs& a, hipStream_t stream) {
   const int ntiles = (a.V + kGemmBV - 1) / kGemmBV;
   int grid = kGemmBpc * device_cu_count();
   if (grid > ntiles) grid = ntiles;
-  hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
+  hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
   NVJSEL_CHECK_LAUNCH("lm_head_gemm_kernel");
   return NVJSEL_OK;
 }
@@ -1798,6 +1824,7 @@ static size_t lm_ws_small_bytes(int batch) {
   return batch <= 0 ? 0 : lm_ws_keys_bytes(batch) + 256;
 }
 static constexpr int kGemmMinBatch = 64;
+static constexpr int kGemm3MinBatch = 80;  // f32 activations (three-term GEMM)
 
 
 // Final-RMSNorm prologue request (norm_w == nullptr: hidden is already normed).
@@ -1927,7 +1954,12 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   const bool gemm = batch > kGemmMinBatch && bf16_mfma && (H % (2 * kGemmKC)) == 0 &&
                     eff_dtype == NVJSEL_BF16 && (prenorm || (((uintptr_t)hidden) & 15) == 0) &&
                     (mode != MODE_SAMPLE || V < (1 << 25));
-  const bool fused_prenorm = prenorm && !gemm && (gemv || tile);
+  // f32 activations, greedy / logits: the same one-pass GEMM on three bf16
+  // terms per value, ~460 us per 256-row pass at V = 248k; from 81 rows on
+  // it beats the 16-row tile passes (~85 us each: B = 80 435 vs 502 us)
+  const bool gemm3 = !gemm && batch > kGemm3MinBatch && bf16_mfma && (H % (2 * kGemmKC)) == 0 &&
+                     eff_dtype == NVJSEL_F32 && mode != MODE_SAMPLE && (prenorm || (((uintptr_t)hidden) & 15) == 0);
+  const bool fused_prenorm = prenorm && !gemm && !gemm3 && (gemv || tile);
   if (prenorm && !fused_prenorm) {
     LmArgs p{};
     p.hidden = hidden;
@@ -1946,7 +1978,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   if (tile) chunk = eff_dtype == NVJSEL_BF16 ? 64 : 16;
   if (gemv) chunk = 0;
   if (hv) chunk = 8;
-  if (gemm) chunk = kGemmBB;
+  if (gemm || gemm3) chunk = kGemmBB;
   auto by_mode = [&](auto fn) -> int {
     if (mode == MODE_GREEDY) return fn(std::integral_constant<int, MODE_GREEDY>{});
     if (mode == MODE_SAMPLE) return fn(std::integral_constant<int, MODE_SAMPLE>{});
@@ -1980,7 +2012,12 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     a.out_stride = lo.stride;
     int rc;
     if (gemm) {
-      rc = by_mode([&](auto M) { return launch_gemm<decltype(M)::value>(a, s); });
+      rc = by_mode([&](auto M) { return launch_gemm<decltype(M)::value, 1>(a, s); });
+    } else if (gemm3) {
+      rc = by_mode([&](auto M) -> int {
+        if constexpr (decltype(M)::value == MODE_SAMPLE) return NVJSEL_EINVAL;  // not routed here
+        else return launch_gemm<decltype(M)::value, 3>(a, s);
+      });
     } else if (gemv) {
       rc = by_mode([&](auto M) { return dispatch_gemv<decltype(M)::value>(a, s); });
     } else if (hv) {

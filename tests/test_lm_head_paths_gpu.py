@@ -244,6 +244,42 @@ def test_gemm_greedy_and_logits(B, H):
     assert torch.equal(ids, ids2)
 
 
+@pytest.mark.parametrize("B,H", [(81, 512), (200, 1024), (300, 1024), (80, 1024)])
+def test_gemm_f32_activations(B, H):
+    """fp32 activations (lm_head_decode_act_dtype fp32) above 80 rows: the
+    blocked GEMM on three bf16 terms per value -- one pass over W per 256
+    rows, greedy and logits -- against the float64 dot (fp32 logits); 80 rows
+    take five 16-row tile passes."""
+    rng = np.random.default_rng(7700 + B + H)
+    V = 9001
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    h = _hidden(rng, B, H, torch.float32)
+    ids = nvjsel.lm_head_greedy_top1_hip(h, W.T)
+    logits = nvjsel.lm_head_logits_hip(h, W.T)
+    torch.cuda.synchronize()
+    assert logits.dtype == torch.float32
+    hf, wf = h.cpu().numpy(), W.float().cpu().numpy()
+    check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(hf, wf), 0, f"gemm f32 B={B} H={H}")
+    _check_logits(logits, hf, wf, 0, f"gemm f32 logits B={B} H={H}")
+
+
+def test_gemm_f32_activations_with_prenorm():
+    """The reference's default decode configuration at a serving batch: the
+    final RMSNorm into fp32 activations (prologue kernel), then the GEMM on
+    three bf16 terms, B = 256, V = 151936."""
+    rng = np.random.default_rng(4343)
+    B, H, V = 256, 1024, 151936
+    x = sel.round_bf16(rng.normal(0.0, 3.0, (B, H)).astype(np.float32))
+    nw = rng.normal(0.0, 0.2, H).astype(np.float32)
+    W = sel.round_bf16(rng.normal(0.0, 0.02, (V, H)).astype(np.float32))
+    ids = nvjsel.lm_head_greedy_top1_hip(
+        torch.from_numpy(x).to(torch.bfloat16).cuda(), torch.from_numpy(W).to(torch.bfloat16).cuda(),
+        weight_layout="vh", norm_weight=torch.from_numpy(nw).cuda(), rms_norm_eps=1e-6, act_dtype=torch.float32)
+    torch.cuda.synchronize()
+    xin = sel.lm_head_input(x, nw, 1e-6, hidden_dtype="bf16", act_dtype="f32")
+    check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(xin, W), 0, "gemm f32 B=256 prenorm")
+
+
 @pytest.mark.parametrize("rc", [0, 2])
 def test_gemm_other_roundings(rc):
     """The blocked GEMM with the caller's reduce_cast: 0 (fp32 logits, f32
