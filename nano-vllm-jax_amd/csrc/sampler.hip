@@ -1533,12 +1533,13 @@ struct QueueShared {
 };
 
 // Whole block, after the row's seed `best` (an exact score some kept element
-// reaches) is known, with the row's chunk maxima ck[] (in LDS): appends a gumbel item (b << 16 | c) for every chunk c that
+// reaches) is known, with the row's chunk maxima ck[] (in LDS): appends a
+// gumbel item (b << 16 | c) to the call's work list for every chunk c that
 // can hold the row's maximum -- it has a kept element (chunk max >= tau) whose
 // best possible score, chunk max + the largest Gumbel draw, is not below the
-// seed -- and records the row's item count for the gumbel kernel's last-item
-// test.  A row left with no item (it cannot happen: the seed's own chunk
-// qualifies) is answered with the seed.
+// seed (prune = false: every chunk with a kept element).  A row left with no
+// item (it cannot happen: the seed's own chunk qualifies) is answered with
+// the seed.
 __device__ __forceinline__ void queue_chunks(const SampleArgs& a, int b, const RowParams& rp, uint32_t tau,
                                              unsigned long long best, const unsigned long long* ck, QueueShared& q,
                                              bool prune = true) {
