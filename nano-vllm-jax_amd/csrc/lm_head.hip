@@ -1323,15 +1323,17 @@ __device__ __forceinline__ void gemm_finish_rows(const LmArgs& a, unsigned long 
 // NS = 1: bf16 hidden.  NS = 3: f32 hidden, each value split exactly into
 // three bf16 terms as it is staged into LDS (split_terms), and three MFMAs
 // per fragment pair (fp32 products and sums, as the tile kernel's NS = 3).
-template <int MODE, int BV, int NS>
+// KC: K per stage (32; 16 for f32 hidden in sample mode, whose three-term
+// stages and candidate queues would not fit the LDS at 32).
+template <int MODE, int BV, int NS, int KC>
 __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a) {
-  constexpr int Q = kGemmKC / 8;  // 8-element columns per row and stage
+  constexpr int Q = KC / 8;  // 8-element columns per row and stage
   constexpr int VH = BV / 128;  // 128-row vocabulary parts; 4 batch quarters each
   constexpr int NT = VH * 4 * 64;  // threads
   constexpr int PA = Q * BV / NT, PB = Q * kGemmBB / NT;  // 8-element load pieces per thread (W, hidden)
   constexpr int HB = NS == 1 ? 1 : 2;  // 16-byte loads per hidden piece
-  static_assert(PA == 2, "two W pieces per thread and stage");
-  static_assert(NS == 1 || (NS == 3 && MODE != MODE_SAMPLE), "f32 hidden: greedy and logits modes");
+  static_assert(PA >= 1 && PA * NT == Q * BV && PB * NT == Q * kGemmBB, "whole load pieces per thread");
+  static_assert(NS == 1 || NS == 3, "bf16 or three-term f32 hidden");
   __shared__ u32x4_t As[2][Q * BV];
   __shared__ u32x4_t Bs[2][NS][Q * kGemmBB];
   __shared__ unsigned long long kred[VH][kGemmBB];
@@ -1353,7 +1355,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   const int B = a.B, V = a.V, H = a.H;
   const uint16_t* W = (const uint16_t*)a.W;
   const int ntiles = (V + BV - 1) / BV;
-  const int nkc = H / kGemmKC;
+  const int nkc = H / KC;
   const int my_tiles = blockIdx.x < ntiles ? (ntiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
   const int S = my_tiles * nkc;  // stages of this block
   // load piece p: row p >> 2, 16-byte column p & 3, LDS slot q * ROWS + (row ^ 2q)
@@ -1361,14 +1363,15 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   const u32x4_t* xp[PB];
 #pragma unroll
   for (int i = 0; i < PA; ++i) {
-    const int p = tid + NT * i;
-    arow[i] = p >> 2;
-    aq[i] = p & 3;
+    const unsigned p = (unsigned)(tid + NT * i);  // (unsigned: / Q and % Q are a shift and a mask)
+    arow[i] = (int)(p / Q);
+    aq[i] = (int)(p % Q);
     aslot[i] = aq[i] * BV + (arow[i] ^ (aq[i] << 1));
   }
 #pragma unroll
   for (int i = 0; i < PB; ++i) {
-    const int p = tid + NT * i, row = p >> 2, q = p & 3;
+    const unsigned p = (unsigned)(tid + NT * i);
+    const int row = (int)(p / Q), q = (int)(p % Q);
     bslot[i] = q * kGemmBB + (row ^ (q << 1));
     // rows >= B repeat row B - 1: a fixed count of loads in flight and no
     // select on the loaded data (which would make the compiler wait for it
@@ -1394,7 +1397,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
 #pragma unroll
     for (int i = 0; i < PA; ++i) {
       const int v = min(v0 + arow[i], V - 1);
-      RA[e][i] = *((const u32x4_t*)(W + (size_t)v * H + kc * kGemmKC) + aq[i]);
+      RA[e][i] = *((const u32x4_t*)(W + (size_t)v * H + kc * KC) + aq[i]);
     }
   };
   auto gload_b = [&](auto set, int st) NVJSEL_INLINE {
@@ -1442,7 +1445,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   auto compute = [&](auto buf) NVJSEL_INLINE {
     constexpr int f = decltype(buf)::value;
 #pragma unroll
-    for (int ks = 0; ks < kGemmKC / 16; ++ks) {
+    for (int ks = 0; ks < KC / 16; ++ks) {
       const int q = ks * 2 + h, sw = q << 1;
       u32x4_t bf[NS][2];
 #pragma unroll
@@ -1592,7 +1595,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
-  if (S > 0) {  // S is even: nkc = H / 32 with H % 64 == 0
+  if (S > 0) {  // S is even: nkc = H / KC with H % (2 KC) == 0
     // prologue: stage 0 in LDS buffer 0, stages 1 and 2 in sets 1 and 0 --
     // issued in the order the loop's back edge leaves them in flight, so the
     // wait counts agree at the loop head and no store waits for more than
@@ -1651,7 +1654,8 @@ static int launch_gemm(const LmArgs& a, hipStream_t stream) {
   const int ntiles = (a.V + kGemmBV - 1) / kGemmBV;
   int grid = kGemmBpc * device_cu_count();
   if (grid > ntiles) grid = ntiles;
-  hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
+  constexpr int KC = (NS == 3 && MODE == MODE_SAMPLE) ? kGemmKC / 2 : kGemmKC;
+  hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
   NVJSEL_CHECK_LAUNCH("lm_head_gemm_kernel");
   return NVJSEL_OK;
 }
@@ -1824,7 +1828,7 @@ static size_t lm_ws_small_bytes(int batch) {
   return batch <= 0 ? 0 : lm_ws_keys_bytes(batch) + 256;
 }
 static constexpr int kGemmMinBatch = 64;
-static constexpr int kGemm3MinBatch = 80;  // f32 activations (three-term GEMM)
+static constexpr int kGemm3MinBatch = 80, kGemm3MinBatchSample = 96;  // f32 activations (three-term GEMM)
 
 
 // Final-RMSNorm prologue request (norm_w == nullptr: hidden is already normed).
@@ -1954,11 +1958,14 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   const bool gemm = batch > kGemmMinBatch && bf16_mfma && (H % (2 * kGemmKC)) == 0 &&
                     eff_dtype == NVJSEL_BF16 && (prenorm || (((uintptr_t)hidden) & 15) == 0) &&
                     (mode != MODE_SAMPLE || V < (1 << 25));
-  // f32 activations, greedy / logits: the same one-pass GEMM on three bf16
-  // terms per value, ~460 us per 256-row pass at V = 248k; from 81 rows on
-  // it beats the 16-row tile passes (~85 us each: B = 80 435 vs 502 us)
-  const bool gemm3 = !gemm && batch > kGemm3MinBatch && bf16_mfma && (H % (2 * kGemmKC)) == 0 &&
-                     eff_dtype == NVJSEL_F32 && mode != MODE_SAMPLE && (prenorm || (((uintptr_t)hidden) & 15) == 0);
+  // f32 activations: the same one-pass GEMM on three bf16 terms per value,
+  // per 256-row pass at V = 248k ~460 us (greedy) / ~550-620 us (sampling);
+  // it beats the 16-row tile passes (~85 / ~90 us each) from 81 rows
+  // (greedy; B = 80 435 vs 502 us) and from 97 rows (sampling; B = 96 535 vs
+  // 571 us, B = 128 696 vs 547 us)
+  const bool gemm3 = !gemm && batch > (mode == MODE_SAMPLE ? kGemm3MinBatchSample : kGemm3MinBatch) && bf16_mfma && (H % (2 * kGemmKC)) == 0 &&
+                     eff_dtype == NVJSEL_F32 && (prenorm || (((uintptr_t)hidden) & 15) == 0) &&
+                     (mode != MODE_SAMPLE || V < (1 << 25));
   const bool fused_prenorm = prenorm && !gemm && !gemm3 && (gemv || tile);
   if (prenorm && !fused_prenorm) {
     LmArgs p{};
@@ -2014,10 +2021,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     if (gemm) {
       rc = by_mode([&](auto M) { return launch_gemm<decltype(M)::value, 1>(a, s); });
     } else if (gemm3) {
-      rc = by_mode([&](auto M) -> int {
-        if constexpr (decltype(M)::value == MODE_SAMPLE) return NVJSEL_EINVAL;  // not routed here
-        else return launch_gemm<decltype(M)::value, 3>(a, s);
-      });
+      rc = by_mode([&](auto M) { return launch_gemm<decltype(M)::value, 3>(a, s); });
     } else if (gemv) {
       rc = by_mode([&](auto M) { return dispatch_gemv<decltype(M)::value>(a, s); });
     } else if (hv) {

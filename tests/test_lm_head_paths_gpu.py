@@ -263,6 +263,26 @@ def test_gemm_f32_activations(B, H):
     _check_logits(logits, hf, wf, 0, f"gemm f32 logits B={B} H={H}")
 
 
+@pytest.mark.parametrize("B", [100, 300])
+def test_gemm_sample_f32_activations(B):
+    """Fused Gumbel sampling with fp32 activations above 96 rows: the blocked
+    GEMM on three bf16 terms with 16-wide K stages (B = 300: two 256-row
+    passes), greedy rows beside temperature rows, against the oracle's scores
+    on the float64 logits (fp32 logits, no rounding)."""
+    rng = np.random.default_rng(9300 + B)
+    H, V = 1024, 12007
+    W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    h = _hidden(rng, B, H, torch.float32)
+    T = [float(x) for x in rng.choice([0.0, 0.6, 1.0], B)]
+    keys = engine_keys(B, 77 + B)
+    ids = nvjsel.lm_head_sample_token_ids(h, W, temperatures=torch.tensor(T).cuda(),
+                                          rng_keys=keys_tensor(keys), weight_layout="vh")
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(h.cpu().numpy(), W.float().cpu().numpy())
+    namb = check_fused_sampled(ids.cpu().numpy(), z, T, keys, 0, f"gemm f32 sample B={B}")
+    assert namb <= max(1, B // 16)
+
+
 def test_gemm_f32_activations_with_prenorm():
     """The reference's default decode configuration at a serving batch: the
     final RMSNorm into fp32 activations (prologue kernel), then the GEMM on
