@@ -1272,11 +1272,17 @@ __device__ __forceinline__ void gemm_epilogue(const LmArgs& a, const f32x16_t (&
           if (v < a.V && b < a.B) store_logit(a, b, v, apply_cast(d[e], a.reduce_cast));
         }
       } else {
-        float m = d[0];
+        f32x16_t dm = d;
+        if (v0 + tv * 32 + 32 > a.V) {  // the last tile: rows past V hold re-read data
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (v0 + tv * 32 + 8 * (e >> 2) + 4 * h + (e & 3) >= a.V) dm[e] = -INFINITY;
+        }
+        float m = dm[0];
 #pragma unroll
         for (int e = 1; e < 15; e += 2)
-          m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, d[e]), d[e + 1]);
-        m = __builtin_elementwise_maximum(m, d[15]);
+          m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, dm[e]), dm[e + 1]);
+        m = __builtin_elementwise_maximum(m, dm[15]);
         const float rm = apply_cast(m, a.reduce_cast);
         const uint32_t om = ord_f32(rm);
         const bool up = om > bo[tb];
@@ -1285,7 +1291,7 @@ __device__ __forceinline__ void gemm_epilogue(const LmArgs& a, const f32x16_t (&
           const bool nan = rm != rm;
 #pragma unroll
           for (int e = 14; e >= 0; --e) {
-            const float x = apply_cast(d[e], a.reduce_cast);
+            const float x = apply_cast(dm[e], a.reduce_cast);
             if (nan ? x != x : x == rm) first = e;
           }
           if (up) {
@@ -1325,7 +1331,15 @@ __device__ __forceinline__ void gemm_finish_rows(const LmArgs& a, unsigned long 
 // per fragment pair (fp32 products and sums, as the tile kernel's NS = 3).
 // KC: K per stage (32; 16 for f32 hidden in sample mode, whose three-term
 // stages and candidate queues would not fit the LDS at 32).
-template <int MODE, int BV, int NS, int KC>
+// HV: weight stored [H, V] (vocabulary contiguous).  A W stage is then KC
+// k-rows of BV columns (512-byte rows, read whole), kept row-major in LDS
+// (rows padded by 16 bytes), and the A fragments -- 8 consecutive k of one
+// vocabulary column per lane -- come from two transposing LDS reads
+// (ds_read_b64_tr_b16: in each 16-lane group, lane j receives element j & 3
+// of the 8-byte chunks addressed by lanes (j >> 2) + 4m, m = 0..3; group lane
+// r addresses k = kb + (r >> 2), columns c0 + 4 (r & 3) .. + 3, so lane j gets
+// k = kb .. kb + 3 of column c0 + j).
+template <int MODE, int BV, int NS, int KC, bool HV>
 __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a) {
   constexpr int Q = KC / 8;  // 8-element columns per row and stage
   constexpr int VH = BV / 128;  // 128-row vocabulary parts; 4 batch quarters each
@@ -1334,7 +1348,9 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   constexpr int HB = NS == 1 ? 1 : 2;  // 16-byte loads per hidden piece
   static_assert(PA >= 1 && PA * NT == Q * BV && PB * NT == Q * kGemmBB, "whole load pieces per thread");
   static_assert(NS == 1 || NS == 3, "bf16 or three-term f32 hidden");
-  __shared__ u32x4_t As[2][Q * BV];
+  constexpr int ROWV = BV + 8;  // HV: LDS row length in elements (16-byte pad)
+  constexpr int AW = HV ? KC * ROWV / 8 : Q * BV;  // 16-byte slots of a W stage
+  __shared__ u32x4_t As[2][AW];
   __shared__ u32x4_t Bs[2][NS][Q * kGemmBB];
   __shared__ unsigned long long kred[VH][kGemmBB];
   // sample mode: per-wave queue of entries that may be their row's maximum
@@ -1364,9 +1380,15 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
 #pragma unroll
   for (int i = 0; i < PA; ++i) {
     const unsigned p = (unsigned)(tid + NT * i);  // (unsigned: / Q and % Q are a shift and a mask)
-    arow[i] = (int)(p / Q);
-    aq[i] = (int)(p % Q);
-    aslot[i] = aq[i] * BV + (arow[i] ^ (aq[i] << 1));
+    if constexpr (HV) {  // k-row p / (BV / 8), 8-column group p % (BV / 8)
+      arow[i] = (int)(p / (BV / 8));
+      aq[i] = (int)(p % (BV / 8));
+      aslot[i] = (arow[i] * ROWV + aq[i] * 8) / 8;
+    } else {
+      arow[i] = (int)(p / Q);
+      aq[i] = (int)(p % Q);
+      aslot[i] = aq[i] * BV + (arow[i] ^ (aq[i] << 1));
+    }
   }
 #pragma unroll
   for (int i = 0; i < PB; ++i) {
@@ -1396,8 +1418,15 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
     stage_of(st, v0, kc);
 #pragma unroll
     for (int i = 0; i < PA; ++i) {
-      const int v = min(v0 + arow[i], V - 1);
-      RA[e][i] = *((const u32x4_t*)(W + (size_t)v * H + kc * KC) + aq[i]);
+      if constexpr (HV) {
+        // groups past the row end re-read the last group (V % 8 == 0); their
+        // columns are masked where they could win
+        const int v = min(v0 + aq[i] * 8, V - 8);
+        RA[e][i] = *(const u32x4_t*)(W + (size_t)(kc * KC + arow[i]) * V + v);
+      } else {
+        const int v = min(v0 + arow[i], V - 1);
+        RA[e][i] = *((const u32x4_t*)(W + (size_t)v * H + kc * KC) + aq[i]);
+      }
     }
   };
   auto gload_b = [&](auto set, int st) NVJSEL_INLINE {
@@ -1433,6 +1462,8 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   };
   // 32 x 32 tiles: 4 (vocab) x 2 (batch) per wave
   const int h = lane >> 5, c32 = lane & 31;
+  // HV: this lane's transposing-read position in a stage (k-row, column)
+  const int trk = 8 * (lane >> 5) + ((lane & 15) >> 2), trc = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   f32x16_t acc[4][2];
   auto zero_acc = [&]() NVJSEL_INLINE {
 #pragma unroll
@@ -1454,7 +1485,21 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
         for (int tb = 0; tb < 2; ++tb) bf[t][tb] = Bs[f][t][q * kGemmBB + ((bj * 64 + tb * 32 + c32) ^ sw)];
 #pragma unroll
       for (int tv = 0; tv < 4; ++tv) {
-        const u32x4_t af = As[f][q * BV + ((vi * 128 + tv * 32 + c32) ^ sw)];
+        u32x4_t af;
+        if constexpr (HV) {
+          typedef __bf16 bf16x4_lds __attribute__((ext_vector_type(4)));
+          typedef __attribute__((address_space(3))) bf16x4_lds lds_bf16x4;
+          const int off = (ks * 16 + trk) * ROWV + vi * 128 + tv * 32 + trc;
+          auto* base = (__attribute__((address_space(3))) uint16_t*)(uint16_t*)As[f];
+          const bf16x4_lds lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + off));
+          const bf16x4_lds hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + off + 4 * ROWV));
+          uint32_t w[4];
+          __builtin_memcpy(w, &lo, 8);
+          __builtin_memcpy(w + 2, &hi, 8);
+          af = u32x4_t{w[0], w[1], w[2], w[3]};
+        } else {
+          af = As[f][q * BV + ((vi * 128 + tv * 32 + c32) ^ sw)];
+        }
 #pragma unroll
         for (int t = 0; t < NS; ++t)
 #pragma unroll
@@ -1649,13 +1694,13 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
 // 185 us at B = 256, V = 248320) or 128 (4 waves, two blocks per CU: 195 us)
 static constexpr int kGemmBV = 256;
 static constexpr int kGemmBpc = 256 / kGemmBV;  // blocks per CU of the blocked GEMM
-template <int MODE, int NS>
+template <int MODE, int NS, bool HV>
 static int launch_gemm(const LmArgs& a, hipStream_t stream) {
   const int ntiles = (a.V + kGemmBV - 1) / kGemmBV;
   int grid = kGemmBpc * device_cu_count();
   if (grid > ntiles) grid = ntiles;
   constexpr int KC = (NS == 3 && MODE == MODE_SAMPLE) ? kGemmKC / 2 : kGemmKC;
-  hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
+  hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
   NVJSEL_CHECK_LAUNCH("lm_head_gemm_kernel");
   return NVJSEL_OK;
 }
@@ -1829,6 +1874,7 @@ static size_t lm_ws_small_bytes(int batch) {
 }
 static constexpr int kGemmMinBatch = 64;
 static constexpr int kGemm3MinBatch = 80, kGemm3MinBatchSample = 96;  // f32 activations (three-term GEMM)
+static constexpr int kGemmHvMinBatch = 8, kGemmHvMinBatchSample = 16, kGemm3HvMinBatch = 40, kGemm3HvMinBatchSample = 56;  // [H, V] weights
 
 
 // Final-RMSNorm prologue request (norm_w == nullptr: hidden is already normed).
@@ -1954,18 +2000,24 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   }
   const bool tile = !gemv && bf16_mfma && H == 1024 && (prenorm || (((uintptr_t)hidden) & 15) == 0);
   // blocked GEMM: 64 < B, bf16 activations, one pass over W per 256 rows (greedy, logits and Gumbel sampling)
-  // (sample mode packs vocabulary ids into 25 bits of its queue entries)
-  const bool gemm = batch > kGemmMinBatch && bf16_mfma && (H % (2 * kGemmKC)) == 0 &&
-                    eff_dtype == NVJSEL_BF16 && (prenorm || (((uintptr_t)hidden) & 15) == 0) &&
-                    (mode != MODE_SAMPLE || V < (1 << 25));
+  // (sample mode packs vocabulary ids into 25 bits of its queue entries).
+  // [H, V] weights (transposing LDS reads): from 9 rows greedy / logits, 17
+  // sampling -- the [H, V] streaming kernel takes 8 rows per pass over W
+  // (V = 248k: B = 16 two passes 188 / 224 us, the GEMM ~165 / ~255 us; B = 64
+  // 706 / 826 us against 164 / 255 us)
+  const bool hv_gemm_ok = layout == NVJSEL_W_HV && weight_dtype == NVJSEL_BF16 && aligned && (V % 8) == 0;
+  const bool gemm_ok = (bf16_mfma || hv_gemm_ok) && (H % (2 * kGemmKC)) == 0 &&
+                       (prenorm || (((uintptr_t)hidden) & 15) == 0) && (mode != MODE_SAMPLE || V < (1 << 25));
+  const bool gemm = gemm_ok && eff_dtype == NVJSEL_BF16 &&
+                    batch > (hv_gemm_ok ? (mode == MODE_SAMPLE ? kGemmHvMinBatchSample : kGemmHvMinBatch) : kGemmMinBatch);
   // f32 activations: the same one-pass GEMM on three bf16 terms per value,
   // per 256-row pass at V = 248k ~460 us (greedy) / ~550-620 us (sampling);
   // it beats the 16-row tile passes (~85 / ~90 us each) from 81 rows
   // (greedy; B = 80 435 vs 502 us) and from 97 rows (sampling; B = 96 535 vs
-  // 571 us, B = 128 696 vs 547 us)
-  const bool gemm3 = !gemm && batch > (mode == MODE_SAMPLE ? kGemm3MinBatchSample : kGemm3MinBatch) && bf16_mfma && (H % (2 * kGemmKC)) == 0 &&
-                     eff_dtype == NVJSEL_F32 && (prenorm || (((uintptr_t)hidden) & 15) == 0) &&
-                     (mode != MODE_SAMPLE || V < (1 << 25));
+  // 571 us, B = 128 696 vs 547 us), and the 8-row [H, V] passes from 41 / 57
+  const bool gemm3 = gemm_ok && eff_dtype == NVJSEL_F32 &&
+                     batch > (hv_gemm_ok ? (mode == MODE_SAMPLE ? kGemm3HvMinBatchSample : kGemm3HvMinBatch)
+                                         : (mode == MODE_SAMPLE ? kGemm3MinBatchSample : kGemm3MinBatch));
   const bool fused_prenorm = prenorm && !gemm && !gemm3 && (gemv || tile);
   if (prenorm && !fused_prenorm) {
     LmArgs p{};
@@ -2019,9 +2071,13 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     a.out_stride = lo.stride;
     int rc;
     if (gemm) {
-      rc = by_mode([&](auto M) { return launch_gemm<decltype(M)::value, 1>(a, s); });
+      rc = by_mode([&](auto M) {
+        return hv_gemm_ok ? launch_gemm<decltype(M)::value, 1, true>(a, s) : launch_gemm<decltype(M)::value, 1, false>(a, s);
+      });
     } else if (gemm3) {
-      rc = by_mode([&](auto M) { return launch_gemm<decltype(M)::value, 3>(a, s); });
+      rc = by_mode([&](auto M) {
+        return hv_gemm_ok ? launch_gemm<decltype(M)::value, 3, true>(a, s) : launch_gemm<decltype(M)::value, 3, false>(a, s);
+      });
     } else if (gemv) {
       rc = by_mode([&](auto M) { return dispatch_gemv<decltype(M)::value>(a, s); });
     } else if (hv) {

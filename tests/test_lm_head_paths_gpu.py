@@ -300,6 +300,90 @@ def test_gemm_f32_activations_with_prenorm():
     check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(xin, W), 0, "gemm f32 B=256 prenorm")
 
 
+@pytest.mark.parametrize("B,H,act", [(9, 1024, torch.bfloat16), (17, 1024, torch.bfloat16), (64, 512, torch.bfloat16),
+                                     (300, 1024, torch.bfloat16), (48, 1024, torch.float32)])
+def test_gemm_hv_weights(B, H, act):
+    """[H, V] weights (vocabulary contiguous: the reference's materialised
+    lm_head operand) above the 8-row streaming kernel: the blocked GEMM with
+    row-major W stages and transposing LDS reads, greedy and logits, a
+    vocabulary whose last 256-column tile is partial (V % 256 = 16)."""
+    rng = np.random.default_rng(7900 + B + H)
+    V = 10000
+    Whv = bf16_tensor(rng.standard_normal((H, V)) * 0.05)  # contiguous [H, V]
+    h = _hidden(rng, B, H, act)
+    ids = nvjsel.lm_head_greedy_top1_hip(h, Whv)
+    logits = nvjsel.lm_head_logits_hip(h, Whv)
+    torch.cuda.synchronize()
+    rc = 1 if act == torch.bfloat16 else 0
+    hf, wf = h.float().cpu().numpy(), Whv.float().cpu().numpy().T.copy()
+    check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(hf, wf), rc, f"gemm hv B={B} H={H}")
+    _check_logits(logits, hf, wf, rc, f"gemm hv logits B={B} H={H}")
+
+
+def test_gemm_hv_greedy_winner_in_last_columns():
+    """The greedy maximum in the last 8 columns of a partial last tile: the
+    re-read groups past V duplicate those columns and must not win."""
+    rng = np.random.default_rng(7999)
+    B, H, V = 40, 512, 4104  # V % 256 = 8
+    Whv = rng.standard_normal((H, V)) * 0.02
+    h = rng.standard_normal((B, H)).astype(np.float32)
+    for b in range(B):  # row b's winner at column V - 1 - (b % 8)
+        Whv[:, V - 1 - (b % 8)] += 0.5 * h[b] / np.linalg.norm(h[b])
+    Wt = bf16_tensor(Whv)
+    ht = torch.from_numpy(h).cuda().to(torch.bfloat16)
+    ids = nvjsel.lm_head_greedy_top1_hip(ht, Wt)
+    torch.cuda.synchronize()
+    z = sel.lm_head_logits(ht.float().cpu().numpy(), Wt.float().cpu().numpy().T.copy())
+    check_greedy(ids.cpu().numpy().reshape(-1), z, 1, "gemm hv last columns")
+    assert np.all(ids.cpu().numpy().reshape(-1) < V)
+
+
+@pytest.mark.parametrize("B,act", [(130, torch.bfloat16), (100, torch.float32)])
+def test_gemm_hv_matches_vh_bitwise(B, act):
+    """Where both layouts run the blocked GEMM (bf16 above 64 rows, fp32
+    activations above 80 / 96), the [H, V] kernel multiplies the same products
+    in the same k order as the [V, H] one: logits bitwise equal, sampled ids
+    equal."""
+    rng = np.random.default_rng(9600 + B)
+    H, V = 1024, 12008
+    Wvh = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    Whv = Wvh.T.contiguous()
+    h = _hidden(rng, B, H, act)
+    T = torch.tensor([float(x) for x in rng.choice([0.0, 0.7, 1.0], B)]).cuda()
+    keys = keys_tensor(engine_keys(B, 56 + B))
+    la = nvjsel.lm_head_logits_hip(h, Whv)
+    lb = nvjsel.lm_head_logits_hip(h, Wvh.T)
+    assert torch.equal(la, lb)
+    ga = nvjsel.lm_head_greedy_top1_hip(h, Whv)
+    gb = nvjsel.lm_head_greedy_top1_hip(h, Wvh.T)
+    assert torch.equal(ga, gb)
+    ia = nvjsel.lm_head_sample_token_ids(h, Whv, temperatures=T, rng_keys=keys)
+    ib = nvjsel.lm_head_sample_token_ids(h, Wvh, temperatures=T, rng_keys=keys, weight_layout="vh")
+    torch.cuda.synchronize()
+    assert torch.equal(ia, ib)
+
+
+@pytest.mark.parametrize("B,act", [(20, torch.bfloat16), (130, torch.bfloat16), (64, torch.float32)])
+def test_gemm_hv_sample(B, act):
+    """Fused Gumbel sampling through the [H, V] blocked GEMM (bf16 above 16
+    rows, fp32 activations above 56), greedy rows beside temperature rows.
+    Rows whose kernel id differs within the rounding-flip exemption are
+    listed in the terminal summary."""
+    rng = np.random.default_rng(9500 + B)
+    H, V = 1024, 12008
+    Whv = bf16_tensor(rng.standard_normal((H, V)) * 0.05)
+    h = _hidden(rng, B, H, act)
+    T = [float(x) for x in rng.choice([0.0, 0.7, 1.0], B)]
+    keys = engine_keys(B, 55 + B)
+    ids = nvjsel.lm_head_sample_token_ids(h, Whv, temperatures=torch.tensor(T).cuda(), rng_keys=keys_tensor(keys))
+    torch.cuda.synchronize()
+    rc = 1 if act == torch.bfloat16 else 0
+    z = sel.lm_head_logits(h.float().cpu().numpy(), Whv.float().cpu().numpy().T.copy())
+    namb = check_fused_sampled(ids.cpu().numpy(), z, T, keys, rc, f"gemm hv sample B={B}")
+    from tests.gpu_helpers import REPORTS
+    assert namb <= max(2, B // 16), REPORTS[-1:]
+
+
 @pytest.mark.parametrize("rc", [0, 2])
 def test_gemm_other_roundings(rc):
     """The blocked GEMM with the caller's reduce_cast: 0 (fp32 logits, f32
