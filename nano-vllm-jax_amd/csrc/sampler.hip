@@ -613,7 +613,7 @@ struct FinishShared {
   uint32_t cnt[kThreads], cnt_a[kThreads];
   float fl_a[kThreads];
   uint32_t hist[256];
-  uint32_t n, kf, tau, rem;
+  uint32_t n, kf, tau, rem, nk;
 };
 
 // The first loads of a fast top-k row, issued by select before it reduces the
@@ -751,11 +751,11 @@ __device__ bool finish_topk_row(const SampleArgs& a, int b, const RowParams& rp,
   if (n < 0) return false;
   // kept: every survivor >= the k-th largest (ties kept) -- a prefix
   const uint32_t thr = (uint32_t)(s.srt[rp.k - 1] >> 32);
-  uint32_t mine = 0;
-  for (int i = threadIdx.x; i < n; i += kThreads) mine += (uint32_t)(s.srt[i] >> 32) >= thr ? 1u : 0u;
-  uint32_t tot;
-  (void)block_exclusive_scan<uint32_t>(mine, s.wsum32, tot);
-  const int nk = (int)tot;
+  // the kept prefix ends where the sorted keys fall below thr
+  for (int i = threadIdx.x; i < n; i += kThreads)
+    if ((uint32_t)(s.srt[i] >> 32) >= thr && (i + 1 == n || (uint32_t)(s.srt[i + 1] >> 32) < thr)) s.nk = (uint32_t)(i + 1);
+  __syncthreads();
+  const int nk = (int)s.nk;
   uint32_t tau = thr;
   if (rp.p < 1.0f) {
     // top-p over the kept prefix in sorted order: thread t holds entries 2t, 2t + 1;
