@@ -624,6 +624,7 @@ struct TopkPrefetch {
   uint32_t cnt, cnt_a;
   float fl_a, fl;
   uint32_t key[4];  // published lane maxima t + 256 i, as 16-bit keys (0: none)
+  unsigned long long cv[4];  // entries (t & 7) + 8 q of chunk t >> 3's list (the gather's first reads)
 };
 
 __device__ __forceinline__ void topk_prefetch(const SampleArgs& a, int b, TopkPrefetch& pf) {
@@ -646,6 +647,13 @@ __device__ __forceinline__ void topk_prefetch(const SampleArgs& a, int b, TopkPr
     const int j = (int)threadIdx.x + kThreads * i;
     pf.key[i] = j < nvals ? radix_key(tops[j]) >> 16 : 0u;
   }
+  // the first list entries the gather reads, requested now rather than once
+  // the row floor is known (inside each chunk's list area; entries past the
+  // chunk's count are never used)
+  const int c = (int)(threadIdx.x >> 3);
+  const unsigned long long* src = a.cand + ((size_t)b * NC + (c < NC ? c : 0)) * kCandCap;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) pf.cv[q] = src[(threadIdx.x & 7) + 8 * q];
 }
 
 // Largest 16-bit prefix p with at least k of the row's published lane maxima
@@ -717,8 +725,13 @@ __device__ int topk_sorted_survivors(const SampleArgs& a, int b, const RowParams
     const unsigned long long* src = a.cand + ((size_t)b * NC + c) * kCandCap;
     for (int e0 = (int)(threadIdx.x & 7); e0 < need; e0 += 32) {
       unsigned long long v[4];
+      if (c0 == 0 && e0 < 8) {  // prefetched with the row's other words
 #pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] = e0 + 8 * q < need ? src[e0 + 8 * q] : 0ull;
+        for (int q = 0; q < 4; ++q) v[q] = pf.cv[q];
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = e0 + 8 * q < need ? src[e0 + 8 * q] : 0ull;
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         if (e0 + 8 * q < need && (uint32_t)(v[q] >> 32) >= kf) {
