@@ -1339,7 +1339,8 @@ __device__ __forceinline__ void gemm_finish_rows(const LmArgs& a, unsigned long 
 // of the 8-byte chunks addressed by lanes (j >> 2) + 4m, m = 0..3; group lane
 // r addresses k = kb + (r >> 2), columns c0 + 4 (r & 3) .. + 3, so lane j gets
 // k = kb .. kb + 3 of column c0 + j).
-template <int MODE, int BV, int NS, int KC, bool HV>
+// PART: B <= 192, some 64-row batch quarter holds only repeats of row B - 1.
+template <int MODE, int BV, int NS, int KC, bool HV, bool PART>
 __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a) {
   constexpr int Q = KC / 8;  // 8-element columns per row and stage
   constexpr int VH = BV / 128;  // 128-row vocabulary parts; 4 batch quarters each
@@ -1655,24 +1656,37 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
     __syncthreads();
     // stage s: store stage s+1 (set (s+1)&1) to buffer (s+1)&1, load stage
     // s+3 into that set, multiply buffer s&1
-    auto step = [&](int st, auto cur) NVJSEL_INLINE {
+    auto step = [&](int st, auto cur, auto live) NVJSEL_INLINE {
       constexpr int c = decltype(cur)::value;
       using N = std::integral_constant<int, 1 - c>;
       lstore(N{}, N{});
       gload_b(N{}, st + 3);
       gload_a(N{}, st + 3);
-      compute(cur);
+      if constexpr (decltype(live)::value) compute(cur);
       __syncthreads();
     };
     // the accumulators are zeroed and read outside the stage loop, so they
-    // stay in place across it
-    for (int t = 0; t < my_tiles; ++t) {
-      zero_acc();
-      for (int kc = 0; kc < nkc; kc += 2) {
-        step(t * nkc + kc, I0{});
-        step(t * nkc + kc + 1, I1{});
+    // stay in place across it.  PART: a wave whose 64 batch rows all lie past
+    // B (repeats of row B - 1) runs the stages without fragment reads or
+    // products (B = 64 leaves 2 of the 8 waves multiplying); the full-batch
+    // kernel has one loop and no test
+    auto tiles = [&](auto live) NVJSEL_INLINE {
+      for (int t = 0; t < my_tiles; ++t) {
+        zero_acc();
+        for (int kc = 0; kc < nkc; kc += 2) {
+          step(t * nkc + kc, I0{}, live);
+          step(t * nkc + kc + 1, I1{}, live);
+        }
+        epilogue(t);
       }
-      epilogue(t);
+    };
+    if constexpr (PART) {
+      if (bj * 64 < B)  // wave-uniform
+        tiles(std::true_type{});
+      else
+        tiles(std::false_type{});
+    } else {
+      tiles(std::true_type{});
     }
   }
   if constexpr (MODE == MODE_LOGITS) return;
@@ -1700,7 +1714,10 @@ static int launch_gemm(const LmArgs& a, hipStream_t stream) {
   int grid = kGemmBpc * device_cu_count();
   if (grid > ntiles) grid = ntiles;
   constexpr int KC = (NS == 3 && MODE == MODE_SAMPLE) ? kGemmKC / 2 : kGemmKC;
-  hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
+  if (a.B <= kGemmBB - 64)
+    hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV, true>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
+  else
+    hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV, false>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
   NVJSEL_CHECK_LAUNCH("lm_head_gemm_kernel");
   return NVJSEL_OK;
 }
