@@ -1889,7 +1889,11 @@ static size_t lm_ws_keys_bytes(int batch) { return align_up((size_t)batch * 8, 2
 static size_t lm_ws_small_bytes(int batch) {
   return batch <= 0 ? 0 : lm_ws_keys_bytes(batch) + 256;
 }
-static constexpr int kGemmMinBatch = 64;
+// [V, H] bf16: the GEMM above 64 rows; where the tile kernel serves the shape
+// (H = 1024) above 128 rows (greedy / logits) and 192 (sampling) -- below,
+// its 64-row passes are faster (one box: B = 96 157 vs 168 us greedy, 192 vs
+// 244 us sampled; B = 160 greedy 236 vs 183 us; B = 192 sampled 304 vs 339 us)
+static constexpr int kGemmMinBatch = 64, kGemmMinBatchTile = 128, kGemmMinBatchTileSample = 192;
 static constexpr int kGemm3MinBatch = 80, kGemm3MinBatchSample = 96;  // f32 activations (three-term GEMM)
 static constexpr int kGemmHvMinBatch = 8, kGemmHvMinBatchSample = 16, kGemm3HvMinBatch = 40, kGemm3HvMinBatchSample = 56;  // [H, V] weights
 
@@ -2026,7 +2030,9 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   const bool gemm_ok = (bf16_mfma || hv_gemm_ok) && (H % (2 * kGemmKC)) == 0 &&
                        (prenorm || (((uintptr_t)hidden) & 15) == 0) && (mode != MODE_SAMPLE || V < (1 << 25));
   const bool gemm = gemm_ok && eff_dtype == NVJSEL_BF16 &&
-                    batch > (hv_gemm_ok ? (mode == MODE_SAMPLE ? kGemmHvMinBatchSample : kGemmHvMinBatch) : kGemmMinBatch);
+                    batch > (hv_gemm_ok ? (mode == MODE_SAMPLE ? kGemmHvMinBatchSample : kGemmHvMinBatch)
+                             : !tile    ? kGemmMinBatch
+                                        : (mode == MODE_SAMPLE ? kGemmMinBatchTileSample : kGemmMinBatchTile));
   // f32 activations: the same one-pass GEMM on three bf16 terms per value,
   // per 256-row pass at V = 248k ~460 us (greedy) / ~550-620 us (sampling);
   // it beats the 16-row tile passes (~85 / ~90 us each) from 81 rows

@@ -223,9 +223,12 @@ def test_hidden_to_filtered_sampling_native():
     check_sampled(ids.cpu().numpy(), logits.float().cpu().numpy(), T, K, P, keys, ctx="hidden->filtered")
 
 
-# Blocked GEMM (64 < B, bf16 activations, [V, H] bf16): one pass over W per
-# 256 rows, greedy and logits; B = 300 takes a 256-row and a 44-row launch.
-@pytest.mark.parametrize("B,H", [(65, 1024), (128, 1024), (256, 1024), (300, 512), (100, 2048), (77, 64)])
+# Blocked GEMM (bf16 activations, [V, H] bf16): one pass over W per 256 rows,
+# greedy and logits, above 64 rows -- above 128 where the tile kernel serves
+# the shape (H = 1024; B = 65 and 128 take 64-row tile passes); B = 300 takes
+# a 256-row and a 44-row launch; B = 160 the kernel that skips padding waves.
+@pytest.mark.parametrize("B,H", [(65, 1024), (128, 1024), (160, 1024), (256, 1024), (300, 512), (100, 2048),
+                                 (77, 64)])
 def test_gemm_greedy_and_logits(B, H):
     rng = np.random.default_rng(7000 + B + H)
     V = 10000 + (B % 7)  # not a multiple of the 128-row tile
@@ -417,10 +420,11 @@ def test_gemm_full_vocab_b256_with_prenorm():
     check_greedy(ids.cpu().numpy().reshape(-1), sel.lm_head_logits(xin, W), 1, "gemm B=256 prenorm")
 
 
-@pytest.mark.parametrize("B,H", [(65, 512), (130, 1024), (256, 1024), (300, 1024), (513, 512)])
+@pytest.mark.parametrize("B,H", [(65, 512), (130, 1024), (200, 1024), (256, 1024), (300, 1024), (513, 512)])
 def test_gemm_sample_mixed_temperatures(B, H):
-    """Fused Gumbel sampling through the blocked GEMM (64 < B <= 256 per
-    pass; B = 300 and 513 take two and three 256-row passes that reuse the
+    """Fused Gumbel sampling through the blocked GEMM (above 64 rows, above
+    192 where the tile kernel serves H = 1024: B = 130 takes 64-row tile
+    passes; B = 300 and 513 take two and three 256-row passes that reuse the
     row keys and the ticket): greedy rows (T = 0) beside temperature rows, a
     vocabulary that is not a multiple of the 256-row tile, against the
     oracle's scores s_v = rnd(z_v)/T + g_v."""
