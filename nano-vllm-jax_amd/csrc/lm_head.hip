@@ -1894,7 +1894,7 @@ static size_t lm_ws_small_bytes(int batch) {
 // its 64-row passes are faster (one box: B = 96 157 vs 168 us greedy, 192 vs
 // 244 us sampled; B = 160 greedy 236 vs 183 us; B = 192 sampled 304 vs 339 us)
 static constexpr int kGemmMinBatch = 64, kGemmMinBatchTile = 128, kGemmMinBatchTileSample = 192;
-static constexpr int kGemm3MinBatch = 80, kGemm3MinBatchSample = 96;  // f32 activations (three-term GEMM)
+static constexpr int kGemm3MinBatch = 64, kGemm3MinBatchSample = 80;  // f32 activations (three-term GEMM)
 static constexpr int kGemmHvMinBatch = 8, kGemmHvMinBatchSample = 16, kGemm3HvMinBatch = 40, kGemm3HvMinBatchSample = 56;  // [H, V] weights
 
 
@@ -2034,10 +2034,11 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
                              : !tile    ? kGemmMinBatch
                                         : (mode == MODE_SAMPLE ? kGemmMinBatchTileSample : kGemmMinBatchTile));
   // f32 activations: the same one-pass GEMM on three bf16 terms per value,
-  // per 256-row pass at V = 248k ~460 us (greedy) / ~550-620 us (sampling);
-  // it beats the 16-row tile passes (~85 / ~90 us each) from 81 rows
-  // (greedy; B = 80 435 vs 502 us) and from 97 rows (sampling; B = 96 535 vs
-  // 571 us, B = 128 696 vs 547 us), and the 8-row [H, V] passes from 41 / 57
+  // per 256-row pass at V = 248k ~460 us (greedy) / ~550-620 us (sampling),
+  // ~345-370 / ~475 us below 97 rows (padding waves idle); it beats the
+  // 16-row tile passes (~85 / ~90 us each) from 65 rows greedy (B = 80 371 vs
+  // 419 us) and 81 sampling (B = 96 475 vs 528 us), and the 8-row [H, V]
+  // passes from 41 / 57
   const bool gemm3 = gemm_ok && eff_dtype == NVJSEL_F32 &&
                      batch > (hv_gemm_ok ? (mode == MODE_SAMPLE ? kGemm3HvMinBatchSample : kGemm3HvMinBatch)
                                          : (mode == MODE_SAMPLE ? kGemm3MinBatchSample : kGemm3MinBatch));
