@@ -1,0 +1,69 @@
+"""GPU: every LM-head route at the batch sizes on both sides of its
+thresholds, against the oracle.
+
+The library picks among the streaming GEMV / [H, V] streaming kernel, the
+MFMA tile kernel (64-row passes for bf16, 16-row for three-term fp32
+activations), the blocked GEMM (the kernel that idles padding waves below
+193 rows, the full-batch kernel above, 256-row passes beyond 256) and the
+three-term blocked GEMM, by layout, activation dtype, mode and batch.  Each
+case checks greedy ids (check_greedy: first index of the maximum of the
+rounded logits, rows within the fp32-summation flip accepted) or sampled ids
+(check_fused_sampled: the oracle's Gumbel-max scores) on a vocabulary that is
+not a multiple of any tile (V % 256 = 8)."""
+import numpy as np
+import pytest
+import torch
+
+import nvjsel
+from oracle import selection as sel
+from tests.gpu_helpers import bf16_tensor, check_fused_sampled, check_greedy, engine_keys, keys_tensor
+
+pytestmark = pytest.mark.gpu
+
+H, V = 1024, 4104
+BATCHES = [9, 17, 57, 65, 81, 97, 129, 193, 257]
+
+
+@pytest.fixture(scope="module")
+def weights():
+    rng = np.random.default_rng(2024)
+    Wvh = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
+    return Wvh, Wvh.T.contiguous(), Wvh.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("layout", ["vh", "hv"])
+@pytest.mark.parametrize("act", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B", BATCHES)
+def test_greedy_routes(weights, layout, act, B):
+    Wvh, Whv, wf = weights
+    rng = np.random.default_rng(31 * B + (act == torch.float32))
+    h = torch.from_numpy(rng.standard_normal((B, H)).astype(np.float32)).cuda().to(act)
+    if layout == "vh":
+        ids = nvjsel.lm_head_greedy_top1_hip(h, Wvh, weight_layout="vh")
+    else:
+        ids = nvjsel.lm_head_greedy_top1_hip(h, Whv)
+    torch.cuda.synchronize()
+    rc = 1 if act == torch.bfloat16 else 0
+    z = sel.lm_head_logits(h.float().cpu().numpy(), wf)
+    check_greedy(ids.cpu().numpy().reshape(-1), z, rc, f"route greedy {layout} {act} B={B}")
+
+
+@pytest.mark.parametrize("layout", ["vh", "hv"])
+@pytest.mark.parametrize("act", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B", BATCHES)
+def test_sample_routes(weights, layout, act, B):
+    Wvh, Whv, wf = weights
+    rng = np.random.default_rng(37 * B + (act == torch.float32))
+    h = torch.from_numpy(rng.standard_normal((B, H)).astype(np.float32)).cuda().to(act)
+    T = [float(x) for x in rng.choice([0.0, 0.8, 1.0], B)]
+    keys = engine_keys(B, 101 + B)
+    Tt = torch.tensor(T).cuda()
+    if layout == "vh":
+        ids = nvjsel.lm_head_sample_token_ids(h, Wvh, temperatures=Tt, rng_keys=keys_tensor(keys), weight_layout="vh")
+    else:
+        ids = nvjsel.lm_head_sample_token_ids(h, Whv, temperatures=Tt, rng_keys=keys_tensor(keys))
+    torch.cuda.synchronize()
+    rc = 1 if act == torch.bfloat16 else 0
+    z = sel.lm_head_logits(h.float().cpu().numpy(), wf)
+    namb = check_fused_sampled(ids.cpu().numpy(), z, T, keys, rc, f"route sample {layout} {act} B={B}")
+    assert namb <= max(2, B // 16)
