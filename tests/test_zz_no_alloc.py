@@ -48,6 +48,30 @@ def test_noalloc_matches_workspace_entry(batches):
         assert np.all((ia >= 0) & (ia < V))
 
 
+def test_noalloc_hv_weights():
+    """[H, V] weights through the no-alloc entry: the streaming kernel (8
+    rows) and the blocked GEMM with transposing reads (40 rows), on two calls
+    in a row, against the workspace entry."""
+    lib = _lib.load()
+    rng = np.random.default_rng(77)
+    H, V = 1024, 20008
+    Whv = torch.from_numpy(rng.standard_normal((H, V)).astype(np.float32) * 0.02).cuda().to(torch.bfloat16)
+    stream = torch.cuda.current_stream().cuda_stream
+    for B in (40, 8):  # second call smaller
+        h = torch.from_numpy(rng.standard_normal((B, H)).astype(np.float32)).cuda().to(torch.bfloat16)
+        ids_a = torch.full((B,), -1, dtype=torch.int32, device="cuda")
+        ws = torch.zeros(lib.nvjsel_lm_head_workspace_size(B), dtype=torch.uint8, device="cuda")
+        _lib.call("nvjsel_lm_head_top1", h.data_ptr(), _lib.BF16, Whv.data_ptr(), _lib.BF16, _lib.W_HV, B, H, V, 1,
+                  ids_a.data_ptr(), None, ws.data_ptr(), ws.numel(), stream)
+        ids_b = torch.full((B,), -1, dtype=torch.int32, device="cuda")
+        rc = _noalloc(lib)(h.data_ptr(), _lib.BF16, Whv.data_ptr(), _lib.BF16, _lib.W_HV, B, H, V, 1,
+                           ids_b.data_ptr(), None, stream)
+        assert rc == 0, lib.nvjsel_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(ids_a, ids_b), B
+        assert bool(((ids_a >= 0) & (ids_a < V)).all())
+
+
 def test_noalloc_rejects_batch_beyond_scratch():
     lib = _lib.load()
     rc = _noalloc(lib)(0x1000, _lib.BF16, 0x1000, _lib.BF16, _lib.W_VH, 4097, 1024, 1000, 1, 0x1000, None, None)
