@@ -1256,11 +1256,11 @@ static constexpr int kGemmQcap = 768;  // queue entries per wave (sample mode; L
 // looked up.  Rounding is monotone, so max(round(x)) = round(max(x)), and ties
 // keep the lowest vocabulary row (rows ascend with e and with the tiles).
 // Rows past V repeat row V - 1 (clamped loads) and lose its ties.
-template <int MODE>
-__device__ __forceinline__ void gemm_epilogue(const LmArgs& a, const f32x16_t (&acc)[4][2], int v0, int bj, int h,
+template <int MODE, int TV>
+__device__ __forceinline__ void gemm_epilogue(const LmArgs& a, const f32x16_t (&acc)[TV][2], int v0, int bj, int h,
                                               int c32, uint32_t (&bo)[2], uint32_t (&bi)[2]) {
 #pragma unroll
-  for (int tv = 0; tv < 4; ++tv)
+  for (int tv = 0; tv < TV; ++tv)
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
       const f32x16_t& d = acc[tv][tb];
@@ -1307,9 +1307,9 @@ __device__ __forceinline__ void gemm_epilogue(const LmArgs& a, const f32x16_t (&
 // over the two lane halves and the vocabulary parts, folded into the rows'
 // running maxima (one atomicMax per block and row); the last block to finish
 // writes the ids and re-zeroes the keys (finish_rows).
-template <int VH, int NT>
+template <int VH, int NT, int KBR>
 __device__ __forceinline__ void gemm_finish_rows(const LmArgs& a, unsigned long long (&best)[2], int vi, int bj,
-                                                 int h, int c32, unsigned long long (*kred)[kGemmBBRows]) {
+                                                 int h, int c32, unsigned long long (*kred)[KBR]) {
 #pragma unroll
   for (int tb = 0; tb < 2; ++tb) {
     best[tb] = max_u64(best[tb], shfl_xor_u64(best[tb], 32));
@@ -1340,11 +1340,18 @@ __device__ __forceinline__ void gemm_finish_rows(const LmArgs& a, unsigned long 
 // r addresses k = kb + (r >> 2), columns c0 + 4 (r & 3) .. + 3, so lane j gets
 // k = kb .. kb + 3 of column c0 + j).
 // PART: B <= 192, some 64-row batch quarter holds only repeats of row B - 1.
-template <int MODE, int BV, int NS, int KC, bool HV, bool PART>
+// NARROW: B <= 64; each wave owns 32 vocabulary rows x the 64 batch rows
+// (instead of 128 x 64 of one batch quarter), so all 8 waves multiply and,
+// in sample mode, draw.
+template <int MODE, int BV, int NS, int KC, bool HV, bool PART, bool NARROW>
 __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a) {
   constexpr int Q = KC / 8;  // 8-element columns per row and stage
-  constexpr int VH = BV / 128;  // 128-row vocabulary parts; 4 batch quarters each
-  constexpr int NT = VH * 4 * 64;  // threads
+  static_assert(!(PART && NARROW), "one batch layout");
+  constexpr int TV = NARROW ? 1 : 4;  // 32-row vocabulary tiles per wave
+  constexpr int VH = BV / (32 * TV);  // vocabulary parts
+  constexpr int NBQ = NARROW ? 1 : 4;  // 64-row batch quarters
+  constexpr int NT = VH * NBQ * 64;  // threads
+  constexpr int KBR = NARROW ? 64 : kGemmBB;  // batch rows of the block's row reduction
   constexpr int PA = Q * BV / NT, PB = Q * kGemmBB / NT;  // 8-element load pieces per thread (W, hidden)
   constexpr int HB = NS == 1 ? 1 : 2;  // 16-byte loads per hidden piece
   static_assert(PA >= 1 && PA * NT == Q * BV && PB * NT == Q * kGemmBB, "whole load pieces per thread");
@@ -1353,7 +1360,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   constexpr int AW = HV ? KC * ROWV / 8 : Q * BV;  // 16-byte slots of a W stage
   __shared__ u32x4_t As[2][AW];
   __shared__ u32x4_t Bs[2][NS][Q * kGemmBB];
-  __shared__ unsigned long long kred[VH][kGemmBB];
+  __shared__ unsigned long long kred[VH][KBR];
   // sample mode: per-wave queue of entries that may be their row's maximum
   // (scaled logit, approximate score, vocab << 7 | tb << 6 | lane) and the
   // exact best key of each (lane, tb) row slot
@@ -1465,10 +1472,10 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   const int h = lane >> 5, c32 = lane & 31;
   // HV: this lane's transposing-read position in a stage (k-row, column)
   const int trk = 8 * (lane >> 5) + ((lane & 15) >> 2), trc = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  f32x16_t acc[4][2];
+  f32x16_t acc[TV][2];
   auto zero_acc = [&]() NVJSEL_INLINE {
 #pragma unroll
-    for (int tv = 0; tv < 4; ++tv)
+    for (int tv = 0; tv < TV; ++tv)
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
@@ -1485,12 +1492,12 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) bf[t][tb] = Bs[f][t][q * kGemmBB + ((bj * 64 + tb * 32 + c32) ^ sw)];
 #pragma unroll
-      for (int tv = 0; tv < 4; ++tv) {
+      for (int tv = 0; tv < TV; ++tv) {
         u32x4_t af;
         if constexpr (HV) {
           typedef __bf16 bf16x4_lds __attribute__((ext_vector_type(4)));
           typedef __attribute__((address_space(3))) bf16x4_lds lds_bf16x4;
-          const int off = (ks * 16 + trk) * ROWV + vi * 128 + tv * 32 + trc;
+          const int off = (ks * 16 + trk) * ROWV + vi * 32 * TV + tv * 32 + trc;
           auto* base = (__attribute__((address_space(3))) uint16_t*)(uint16_t*)As[f];
           const bf16x4_lds lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + off));
           const bf16x4_lds hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + off + 4 * ROWV));
@@ -1499,7 +1506,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
           __builtin_memcpy(w + 2, &hi, 8);
           af = u32x4_t{w[0], w[1], w[2], w[3]};
         } else {
-          af = As[f][q * BV + ((vi * 128 + tv * 32 + c32) ^ sw)];
+          af = As[f][q * BV + ((vi * 32 * TV + tv * 32 + c32) ^ sw)];
         }
 #pragma unroll
         for (int t = 0; t < NS; ++t)
@@ -1592,7 +1599,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) amax[tb] = xor32_max(amax[tb]);
 #pragma unroll 1
-    for (int tv = 0; tv < 4; ++tv) {
+    for (int tv = 0; tv < TV; ++tv) {
 #pragma unroll
       for (int qq = 0; qq < 8; ++qq)
 #pragma unroll
@@ -1627,17 +1634,17 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
           }
         }
 #pragma unroll
-      for (int t = 0; t < 3; ++t)
+      for (int t = 0; t < TV - 1; ++t)
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) acc[t][tb] = acc[t + 1][tb];
     }
   };
   auto epilogue = [&](int t) NVJSEL_INLINE {
-    const int v0 = (blockIdx.x + t * gridDim.x) * BV + vi * 128;
+    const int v0 = (blockIdx.x + t * gridDim.x) * BV + vi * 32 * TV;
     if constexpr (SMP)
       sample_epilogue(v0);
     else
-      gemm_epilogue<MODE>(a, acc, v0, bj, h, c32, bo, bi);
+      gemm_epilogue<MODE, TV>(a, acc, v0, bj, h, c32, bo, bi);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -1700,7 +1707,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) best[tb] = ((unsigned long long)bo[tb] << 32) | (unsigned long long)(~bi[tb]);
   }
-  gemm_finish_rows<VH, NT>(a, best, vi, bj, h, c32, kred);
+  gemm_finish_rows<VH, NT, KBR>(a, best, vi, bj, h, c32, kred);
 }
 
 
@@ -1714,10 +1721,14 @@ static int launch_gemm(const LmArgs& a, hipStream_t stream) {
   int grid = kGemmBpc * device_cu_count();
   if (grid > ntiles) grid = ntiles;
   constexpr int KC = (NS == 3 && MODE == MODE_SAMPLE) ? kGemmKC / 2 : kGemmKC;
-  if (a.B <= kGemmBB - 64)
-    hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV, true>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
+  // (the narrow layout only for [H, V]: [V, H] calls of <= 64 rows take the
+  // tile kernel)
+  if (HV && a.B <= 64)
+    hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV, false, HV>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
+  else if (a.B <= kGemmBB - 64)
+    hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV, true, false>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
   else
-    hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV, false>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
+    hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV, false, false>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
   NVJSEL_CHECK_LAUNCH("lm_head_gemm_kernel");
   return NVJSEL_OK;
 }
@@ -1895,7 +1906,11 @@ static size_t lm_ws_small_bytes(int batch) {
 // 244 us sampled; B = 160 greedy 236 vs 183 us; B = 192 sampled 304 vs 339 us)
 static constexpr int kGemmMinBatch = 64, kGemmMinBatchTile = 128, kGemmMinBatchTileSample = 192;
 static constexpr int kGemm3MinBatch = 64, kGemm3MinBatchSample = 80;  // f32 activations (three-term GEMM)
-static constexpr int kGemmHvMinBatch = 8, kGemmHvMinBatchSample = 16, kGemm3HvMinBatch = 40, kGemm3HvMinBatchSample = 56;  // [H, V] weights
+// [H, V] weights: the GEMM above 8 rows for bf16 activations (V = 248k, up
+// to 64 rows in the narrow layout: ~94-98 us greedy, ~113-143 us sampled,
+// against 8-row streaming passes of ~88-100 us each) and above 24 for fp32
+// (~291 / ~325-355 us against three passes of ~97 / ~110 us)
+static constexpr int kGemmHvMinBatch = 8, kGemmHvMinBatchSample = 8, kGemm3HvMinBatch = 24, kGemm3HvMinBatchSample = 24;
 
 
 // Final-RMSNorm prologue request (norm_w == nullptr: hidden is already normed).
@@ -2022,10 +2037,8 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   const bool tile = !gemv && bf16_mfma && H == 1024 && (prenorm || (((uintptr_t)hidden) & 15) == 0);
   // blocked GEMM: 64 < B, bf16 activations, one pass over W per 256 rows (greedy, logits and Gumbel sampling)
   // (sample mode packs vocabulary ids into 25 bits of its queue entries).
-  // [H, V] weights (transposing LDS reads): from 9 rows greedy / logits, 17
-  // sampling -- the [H, V] streaming kernel takes 8 rows per pass over W
-  // (V = 248k: B = 16 two passes 188 / 224 us, the GEMM ~165 / ~255 us; B = 64
-  // 706 / 826 us against 164 / 255 us)
+  // [H, V] weights (transposing LDS reads): from 9 rows (bf16), 25 (fp32);
+  // the [H, V] streaming kernel takes 8 rows per pass over W
   const bool hv_gemm_ok = layout == NVJSEL_W_HV && weight_dtype == NVJSEL_BF16 && aligned && (V % 8) == 0;
   const bool gemm_ok = (bf16_mfma || hv_gemm_ok) && (H % (2 * kGemmKC)) == 0 &&
                        (prenorm || (((uintptr_t)hidden) & 15) == 0) && (mode != MODE_SAMPLE || V < (1 << 25));
@@ -2037,8 +2050,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   // per 256-row pass at V = 248k ~460 us (greedy) / ~550-620 us (sampling),
   // ~345-370 / ~475 us below 97 rows (padding waves idle); it beats the
   // 16-row tile passes (~85 / ~90 us each) from 65 rows greedy (B = 80 371 vs
-  // 419 us) and 81 sampling (B = 96 475 vs 528 us), and the 8-row [H, V]
-  // passes from 41 / 57
+  // 419 us) and 81 sampling (B = 96 475 vs 528 us)
   const bool gemm3 = gemm_ok && eff_dtype == NVJSEL_F32 &&
                      batch > (hv_gemm_ok ? (mode == MODE_SAMPLE ? kGemm3HvMinBatchSample : kGemm3HvMinBatch)
                                          : (mode == MODE_SAMPLE ? kGemm3MinBatchSample : kGemm3MinBatch));

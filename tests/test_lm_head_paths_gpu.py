@@ -304,7 +304,8 @@ def test_gemm_f32_activations_with_prenorm():
 
 
 @pytest.mark.parametrize("B,H,act", [(9, 1024, torch.bfloat16), (17, 1024, torch.bfloat16), (64, 512, torch.bfloat16),
-                                     (300, 1024, torch.bfloat16), (48, 1024, torch.float32)])
+                                     (65, 1024, torch.bfloat16), (300, 1024, torch.bfloat16), (48, 1024, torch.float32),
+                                     (25, 512, torch.float32)])
 def test_gemm_hv_weights(B, H, act):
     """[H, V] weights (vocabulary contiguous: the reference's materialised
     lm_head operand) above the 8-row streaming kernel: the blocked GEMM with
@@ -366,10 +367,12 @@ def test_gemm_hv_matches_vh_bitwise(B, act):
     assert torch.equal(ia, ib)
 
 
-@pytest.mark.parametrize("B,act", [(20, torch.bfloat16), (130, torch.bfloat16), (64, torch.float32)])
+@pytest.mark.parametrize("B,act", [(12, torch.bfloat16), (20, torch.bfloat16), (130, torch.bfloat16),
+                                   (30, torch.float32), (64, torch.float32)])
 def test_gemm_hv_sample(B, act):
-    """Fused Gumbel sampling through the [H, V] blocked GEMM (bf16 above 16
-    rows, fp32 activations above 56), greedy rows beside temperature rows.
+    """Fused Gumbel sampling through the [H, V] blocked GEMM (bf16 above 8
+    rows, fp32 activations above 24; the narrow layout up to 64 rows), greedy
+    rows beside temperature rows.
     Rows whose kernel id differs within the rounding-flip exemption are
     listed in the terminal summary."""
     rng = np.random.default_rng(9500 + B)
