@@ -1255,7 +1255,8 @@ static constexpr int kGemmQcap = 768;  // queue entries per wave (sample mode; L
 // beats the lane's running best (bo, bi) is the first element rounding to it
 // looked up.  Rounding is monotone, so max(round(x)) = round(max(x)), and ties
 // keep the lowest vocabulary row (rows ascend with e and with the tiles).
-// Rows past V repeat row V - 1 (clamped loads) and lose its ties.
+// Rows past V hold re-read data ([V, H]: row V - 1; [H, V]: the last 8-column
+// group) and are masked in the last tile.
 template <int MODE, int TV>
 __device__ __forceinline__ void gemm_epilogue(const LmArgs& a, const f32x16_t (&acc)[TV][2], int v0, int bj, int h,
                                               int c32, uint32_t (&bo)[2], uint32_t (&bi)[2]) {
