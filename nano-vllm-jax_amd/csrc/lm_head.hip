@@ -1353,14 +1353,19 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   constexpr int NBQ = NARROW ? 1 : 4;  // 64-row batch quarters
   constexpr int NT = VH * NBQ * 64;  // threads
   constexpr int KBR = NARROW ? 64 : kGemmBB;  // batch rows of the block's row reduction
-  constexpr int PA = Q * BV / NT, PB = Q * kGemmBB / NT;  // 8-element load pieces per thread (W, hidden)
+  // hidden rows staged per stage (NARROW with f32 hidden: only the 64 the
+  // waves multiply, loaded by the first Q * 64 threads -- whole waves; 291 ->
+  // ~180 us greedy at B = 40-64; with bf16 hidden it measured ~7 us slower)
+  constexpr int XB = (NARROW && NS == 3) ? 64 : kGemmBB;
+  constexpr int XT = Q * XB < NT ? Q * XB : NT;  // threads loading hidden pieces
+  constexpr int PA = Q * BV / NT, PB = Q * XB / XT;  // 8-element load pieces per loading thread (W, hidden)
   constexpr int HB = NS == 1 ? 1 : 2;  // 16-byte loads per hidden piece
-  static_assert(PA >= 1 && PA * NT == Q * BV && PB * NT == Q * kGemmBB, "whole load pieces per thread");
+  static_assert(PA >= 1 && PA * NT == Q * BV && PB * XT == Q * XB && XT % 64 == 0, "whole load pieces per thread");
   static_assert(NS == 1 || NS == 3, "bf16 or three-term f32 hidden");
   constexpr int ROWV = BV + 8;  // HV: LDS row length in elements (16-byte pad)
   constexpr int AW = HV ? KC * ROWV / 8 : Q * BV;  // 16-byte slots of a W stage
   __shared__ u32x4_t As[2][AW];
-  __shared__ u32x4_t Bs[2][NS][Q * kGemmBB];
+  __shared__ u32x4_t Bs[2][NS][Q * XB];
   __shared__ unsigned long long kred[VH][KBR];
   // sample mode: per-wave queue of entries that may be their row's maximum
   // (scaled logit, approximate score, vocab << 7 | tb << 6 | lane) and the
@@ -1401,9 +1406,9 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
   }
 #pragma unroll
   for (int i = 0; i < PB; ++i) {
-    const unsigned p = (unsigned)(tid + NT * i);
+    const unsigned p = (unsigned)(tid + XT * i);
     const int row = (int)(p / Q), q = (int)(p % Q);
-    bslot[i] = q * kGemmBB + (row ^ (q << 1));
+    bslot[i] = q * XB + (row ^ (q << 1));
     // rows >= B repeat row B - 1: a fixed count of loads in flight and no
     // select on the loaded data (which would make the compiler wait for it
     // early); their batch columns are never read
@@ -1442,6 +1447,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
     constexpr int e = decltype(set)::value;
     int v0, kc;
     stage_of(st, v0, kc);
+    if (XT < NT && tid >= XT) return;  // (wave-uniform)
 #pragma unroll
     for (int i = 0; i < PB; ++i)
 #pragma unroll
@@ -1451,6 +1457,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
     constexpr int e = decltype(set)::value, f = decltype(buf)::value;
 #pragma unroll
     for (int i = 0; i < PA; ++i) As[f][aslot[i]] = RA[e][i];
+    if (XT < NT && tid >= XT) return;  // (wave-uniform)
 #pragma unroll
     for (int i = 0; i < PB; ++i) {
       if constexpr (NS == 1) {
@@ -1491,7 +1498,7 @@ __global__ void __launch_bounds__(BV * 2, 256 / BV) lm_head_gemm_kernel(LmArgs a
 #pragma unroll
       for (int t = 0; t < NS; ++t)
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) bf[t][tb] = Bs[f][t][q * kGemmBB + ((bj * 64 + tb * 32 + c32) ^ sw)];
+        for (int tb = 0; tb < 2; ++tb) bf[t][tb] = Bs[f][t][q * XB + ((bj * 64 + tb * 32 + c32) ^ sw)];
 #pragma unroll
       for (int tv = 0; tv < TV; ++tv) {
         u32x4_t af;
@@ -1722,10 +1729,11 @@ static int launch_gemm(const LmArgs& a, hipStream_t stream) {
   int grid = kGemmBpc * device_cu_count();
   if (grid > ntiles) grid = ntiles;
   constexpr int KC = (NS == 3 && MODE == MODE_SAMPLE) ? kGemmKC / 2 : kGemmKC;
-  // (the narrow layout only for [H, V]: [V, H] calls of <= 64 rows take the
-  // tile kernel)
-  if (HV && a.B <= 64)
-    hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV, false, HV>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
+  // (the narrow layout for [H, V] and for f32 hidden: [V, H] bf16 calls of
+  // <= 64 rows take the tile kernel)
+  constexpr bool kNarrow = HV || NS == 3;
+  if (kNarrow && a.B <= 64)
+    hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV, false, kNarrow>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
   else if (a.B <= kGemmBB - 64)
     hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV, true, false>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
   else
@@ -1906,12 +1914,12 @@ static size_t lm_ws_small_bytes(int batch) {
 // its 64-row passes are faster (one box: B = 96 157 vs 168 us greedy, 192 vs
 // 244 us sampled; B = 160 greedy 236 vs 183 us; B = 192 sampled 304 vs 339 us)
 static constexpr int kGemmMinBatch = 64, kGemmMinBatchTile = 128, kGemmMinBatchTileSample = 192;
-static constexpr int kGemm3MinBatch = 64, kGemm3MinBatchSample = 80;  // f32 activations (three-term GEMM)
+static constexpr int kGemm3MinBatch = 32, kGemm3MinBatchSample = 56;  // f32 activations (three-term GEMM)
 // [H, V] weights: the GEMM above 8 rows for bf16 activations (V = 248k, up
 // to 64 rows in the narrow layout: ~94-98 us greedy, ~113-143 us sampled,
-// against 8-row streaming passes of ~88-100 us each) and above 24 for fp32
-// (~291 / ~325-355 us against three passes of ~97 / ~110 us)
-static constexpr int kGemmHvMinBatch = 8, kGemmHvMinBatchSample = 8, kGemm3HvMinBatch = 24, kGemm3HvMinBatchSample = 24;
+// against 8-row streaming passes of ~88-100 us each) and for fp32 above 8
+// greedy, 16 sampled (~180 / ~320 us against passes of ~90 / ~110 us)
+static constexpr int kGemmHvMinBatch = 8, kGemmHvMinBatchSample = 8, kGemm3HvMinBatch = 8, kGemm3HvMinBatchSample = 16;
 
 
 // Final-RMSNorm prologue request (norm_w == nullptr: hidden is already normed).
@@ -2049,12 +2057,15 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
                                         : (mode == MODE_SAMPLE ? kGemmMinBatchTileSample : kGemmMinBatchTile));
   // f32 activations: the same one-pass GEMM on three bf16 terms per value,
   // per 256-row pass at V = 248k ~460 us (greedy) / ~550-620 us (sampling),
-  // ~345-370 / ~475 us below 97 rows (padding waves idle); it beats the
-  // 16-row tile passes (~85 / ~90 us each) from 65 rows greedy (B = 80 371 vs
-  // 419 us) and 81 sampling (B = 96 475 vs 528 us)
+  // ~345-370 / ~475 us for 65-192 rows (padding waves idle), ~180 / ~320 us
+  // up to 64 rows (narrow layout); it beats the 16-row tile passes (~85 / ~90
+  // us each) from 33 rows greedy (B = 48 252 us in passes) and, sampling, at
+  // 57-64 rows (B = 64 333 vs 350 us) and above 80 (B = 80 480 us against 438
+  // in five passes; B = 96 477 against ~528)
   const bool gemm3 = gemm_ok && eff_dtype == NVJSEL_F32 &&
-                     batch > (hv_gemm_ok ? (mode == MODE_SAMPLE ? kGemm3HvMinBatchSample : kGemm3HvMinBatch)
-                                         : (mode == MODE_SAMPLE ? kGemm3MinBatchSample : kGemm3MinBatch));
+                     (hv_gemm_ok ? batch > (mode == MODE_SAMPLE ? kGemm3HvMinBatchSample : kGemm3HvMinBatch)
+                      : mode == MODE_SAMPLE ? (batch > kGemm3MinBatchSample && (batch <= 64 || batch > 80))
+                                            : batch > kGemm3MinBatch);
   const bool fused_prenorm = prenorm && !gemm && !gemm3 && (gemv || tile);
   if (prenorm && !fused_prenorm) {
     LmArgs p{};

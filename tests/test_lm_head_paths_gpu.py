@@ -247,12 +247,12 @@ def test_gemm_greedy_and_logits(B, H):
     assert torch.equal(ids, ids2)
 
 
-@pytest.mark.parametrize("B,H", [(65, 512), (200, 1024), (300, 1024), (64, 1024)])
+@pytest.mark.parametrize("B,H", [(33, 1024), (64, 1024), (65, 512), (200, 1024), (300, 1024), (32, 1024)])
 def test_gemm_f32_activations(B, H):
-    """fp32 activations (lm_head_decode_act_dtype fp32) above 64 rows: the
-    blocked GEMM on three bf16 terms per value -- one pass over W per 256
-    rows, greedy and logits -- against the float64 dot (fp32 logits); 64 rows
-    take four 16-row tile passes."""
+    """fp32 activations (lm_head_decode_act_dtype fp32) above 32 rows: the
+    blocked GEMM on three bf16 terms per value (the narrow layout up to 64
+    rows) -- one pass over W per 256 rows, greedy and logits -- against the
+    float64 dot (fp32 logits); 32 rows take two 16-row tile passes."""
     rng = np.random.default_rng(7700 + B + H)
     V = 9001
     W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
@@ -266,9 +266,10 @@ def test_gemm_f32_activations(B, H):
     _check_logits(logits, hf, wf, 0, f"gemm f32 logits B={B} H={H}")
 
 
-@pytest.mark.parametrize("B", [85, 300])
+@pytest.mark.parametrize("B", [60, 85, 300])
 def test_gemm_sample_f32_activations(B):
-    """Fused Gumbel sampling with fp32 activations above 80 rows: the blocked
+    """Fused Gumbel sampling with fp32 activations at 57-64 rows (narrow) and
+    above 80 rows: the blocked
     GEMM on three bf16 terms with 16-wide K stages (B = 300: two 256-row
     passes), greedy rows beside temperature rows, against the oracle's scores
     on the float64 logits (fp32 logits, no rounding)."""
