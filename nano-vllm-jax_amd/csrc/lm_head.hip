@@ -1330,8 +1330,9 @@ __device__ __forceinline__ void gemm_finish_rows(const LmArgs& a, unsigned long 
 // NS = 1: bf16 hidden.  NS = 3: f32 hidden, each value split exactly into
 // three bf16 terms as it is staged into LDS (split_terms), and three MFMAs
 // per fragment pair (fp32 products and sums, as the tile kernel's NS = 3).
-// KC: K per stage (32; 16 for f32 hidden in sample mode, whose three-term
-// stages and candidate queues would not fit the LDS at 32).
+// KC: K per stage (32; 16 for f32 hidden in sample mode above 64 rows, whose
+// three-term 256-row stages and candidate queues would not fit the LDS at 32;
+// the narrow layout's 64-row stages do, ~144 KB).
 // HV: weight stored [H, V] (vocabulary contiguous).  A W stage is then KC
 // k-rows of BV columns (512-byte rows, read whole), kept row-major in LDS
 // (rows padded by 16 bytes), and the A fragments -- 8 consecutive k of one
@@ -1730,10 +1731,11 @@ static int launch_gemm(const LmArgs& a, hipStream_t stream) {
   if (grid > ntiles) grid = ntiles;
   constexpr int KC = (NS == 3 && MODE == MODE_SAMPLE) ? kGemmKC / 2 : kGemmKC;
   // (the narrow layout for [H, V] and for f32 hidden: [V, H] bf16 calls of
-  // <= 64 rows take the tile kernel)
+  // <= 64 rows take the tile kernel; its 64-row f32 stages leave room for
+  // K stages of 32 in sample mode)
   constexpr bool kNarrow = HV || NS == 3;
   if (kNarrow && a.B <= 64)
-    hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV, false, kNarrow>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
+    hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, kGemmKC, HV, false, kNarrow>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
   else if (a.B <= kGemmBB - 64)
     hipLaunchKernelGGL((lm_head_gemm_kernel<MODE, kGemmBV, NS, KC, HV, true, false>), dim3(grid), dim3(kGemmBV * 2), 0, stream, a);
   else
@@ -1914,11 +1916,11 @@ static size_t lm_ws_small_bytes(int batch) {
 // its 64-row passes are faster (one box: B = 96 157 vs 168 us greedy, 192 vs
 // 244 us sampled; B = 160 greedy 236 vs 183 us; B = 192 sampled 304 vs 339 us)
 static constexpr int kGemmMinBatch = 64, kGemmMinBatchTile = 128, kGemmMinBatchTileSample = 192;
-static constexpr int kGemm3MinBatch = 32, kGemm3MinBatchSample = 56;  // f32 activations (three-term GEMM)
+static constexpr int kGemm3MinBatch = 32, kGemm3MinBatchSample = 32;  // f32 activations (three-term GEMM)
 // [H, V] weights: the GEMM above 8 rows for bf16 activations (V = 248k, up
 // to 64 rows in the narrow layout: ~94-98 us greedy, ~113-143 us sampled,
 // against 8-row streaming passes of ~88-100 us each) and for fp32 above 8
-// greedy, 16 sampled (~180 / ~320 us against passes of ~90 / ~110 us)
+// greedy, 16 sampled (~180 / ~190-218 us against passes of ~90 / ~110 us)
 static constexpr int kGemmHvMinBatch = 8, kGemmHvMinBatchSample = 8, kGemm3HvMinBatch = 8, kGemm3HvMinBatchSample = 16;
 
 
@@ -2057,11 +2059,11 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
                                         : (mode == MODE_SAMPLE ? kGemmMinBatchTileSample : kGemmMinBatchTile));
   // f32 activations: the same one-pass GEMM on three bf16 terms per value,
   // per 256-row pass at V = 248k ~460 us (greedy) / ~550-620 us (sampling),
-  // ~345-370 / ~475 us for 65-192 rows (padding waves idle), ~180 / ~320 us
+  // ~345-370 / ~475 us for 65-192 rows (padding waves idle), ~180 / ~215 us
   // up to 64 rows (narrow layout); it beats the 16-row tile passes (~85 / ~90
   // us each) from 33 rows greedy (B = 48 252 us in passes) and, sampling, at
-  // 57-64 rows (B = 64 333 vs 350 us) and above 80 (B = 80 480 us against 438
-  // in five passes; B = 96 477 against ~528)
+  // 33-64 rows (B = 40 215 vs 258 us; B = 32 197 vs 177) and above 80 (B = 80
+  // 480 us against 438 in five passes; B = 96 477 against ~528)
   const bool gemm3 = gemm_ok && eff_dtype == NVJSEL_F32 &&
                      (hv_gemm_ok ? batch > (mode == MODE_SAMPLE ? kGemm3HvMinBatchSample : kGemm3HvMinBatch)
                       : mode == MODE_SAMPLE ? (batch > kGemm3MinBatchSample && (batch <= 64 || batch > 80))

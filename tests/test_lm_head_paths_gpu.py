@@ -266,12 +266,12 @@ def test_gemm_f32_activations(B, H):
     _check_logits(logits, hf, wf, 0, f"gemm f32 logits B={B} H={H}")
 
 
-@pytest.mark.parametrize("B", [60, 85, 300])
+@pytest.mark.parametrize("B", [33, 60, 85, 300])
 def test_gemm_sample_f32_activations(B):
-    """Fused Gumbel sampling with fp32 activations at 57-64 rows (narrow) and
-    above 80 rows: the blocked
-    GEMM on three bf16 terms with 16-wide K stages (B = 300: two 256-row
-    passes), greedy rows beside temperature rows, against the oracle's scores
+    """Fused Gumbel sampling with fp32 activations at 33-64 rows (the narrow
+    layout, 32-wide K stages) and above 80 rows (the full layout, 16-wide K
+    stages; B = 300: two 256-row passes) -- the blocked GEMM on three bf16
+    terms -- greedy rows beside temperature rows, against the oracle's scores
     on the float64 logits (fp32 logits, no rounding)."""
     rng = np.random.default_rng(9300 + B)
     H, V = 1024, 12007
