@@ -1921,6 +1921,7 @@ static constexpr int kGemm3MinBatch = 32, kGemm3MinBatchSample = 32;  // f32 act
 // to 64 rows in the narrow layout: ~94-98 us greedy, ~113-143 us sampled,
 // against 8-row streaming passes of ~88-100 us each) and for fp32 above 8
 // greedy, 16 sampled (~180 / ~190-218 us against passes of ~90 / ~110 us)
+static constexpr int kMix3MaxBatch = 96, kMix3MaxBatchSample = 96;
 static constexpr int kGemmHvMinBatch = 8, kGemmHvMinBatchSample = 8, kGemm3HvMinBatch = 8, kGemm3HvMinBatchSample = 16;
 
 
@@ -2061,14 +2062,22 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   // per 256-row pass at V = 248k ~460 us (greedy) / ~550-620 us (sampling),
   // ~345-370 / ~475 us for 65-192 rows (padding waves idle), ~180 / ~215 us
   // up to 64 rows (narrow layout); it beats the 16-row tile passes (~85 / ~90
-  // us each) from 33 rows greedy (B = 48 252 us in passes) and, sampling, at
-  // 33-64 rows (B = 40 215 vs 258 us; B = 32 197 vs 177) and above 80 (B = 80
-  // 480 us against 438 in five passes; B = 96 477 against ~528)
-  const bool gemm3 = gemm_ok && eff_dtype == NVJSEL_F32 &&
+  // us each) from 33 rows greedy (B = 48 252 us in passes) and, sampling,
+  // from 33 rows (B = 40 215 vs 258 us; B = 32 197 vs 177); 65-96 rows mix the
+  // two (below)
+  // 65-96 rows, [V, H]: the narrow GEMM on the first 64 rows, then 16-row
+  // tile passes (or the streaming GEMV for a rest of <= 2 rows).  One box,
+  // V = 248k: greedy B = 72 / 80 / 96 267 / 261 / 345 us against 364-367 us
+  // for the 256-row kernel with idle padding waves; sampled B = 72 / 80 / 96
+  // 318 / 318 / 408 us against 434-436 us in tile passes and 474 us
+  // (from B = 104 the 256-row kernel is faster: 479 vs 495 us sampled)
+  const bool mix3 = gemm_ok && tile && !hv_gemm_ok && eff_dtype == NVJSEL_F32 && batch > 64 &&
+                    batch <= (mode == MODE_SAMPLE ? kMix3MaxBatchSample : kMix3MaxBatch);
+  const bool gemm3 = !mix3 && gemm_ok && eff_dtype == NVJSEL_F32 &&
                      (hv_gemm_ok ? batch > (mode == MODE_SAMPLE ? kGemm3HvMinBatchSample : kGemm3HvMinBatch)
-                      : mode == MODE_SAMPLE ? (batch > kGemm3MinBatchSample && (batch <= 64 || batch > 80))
+                      : mode == MODE_SAMPLE ? batch > kGemm3MinBatchSample
                                             : batch > kGemm3MinBatch);
-  const bool fused_prenorm = prenorm && !gemm && !gemm3 && (gemv || tile);
+  const bool fused_prenorm = prenorm && !gemm && !gemm3 && !mix3 && (gemv || tile);
   if (prenorm && !fused_prenorm) {
     LmArgs p{};
     p.hidden = hidden;
@@ -2093,9 +2102,12 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     if (mode == MODE_SAMPLE) return fn(std::integral_constant<int, MODE_SAMPLE>{});
     return fn(std::integral_constant<int, MODE_LOGITS>{});
   };
-  for (int b0 = 0; b0 < batch; b0 += (chunk > 0 ? chunk : batch)) {
+  for (int b0 = 0, nb = 0; b0 < batch; b0 += nb) {
     LmArgs a{};
-    const int nb = chunk > 0 ? (batch - b0 < chunk ? batch - b0 : chunk) : batch;
+    const bool g3 = gemm3 || (mix3 && b0 == 0);
+    const bool gv = gemv || (mix3 && b0 > 0 && batch - b0 <= 2);
+    const int step = mix3 ? (b0 == 0 ? 64 : chunk) : (chunk > 0 ? chunk : batch);
+    nb = batch - b0 < step ? batch - b0 : step;
     a.W = weight;
     a.hidden = (const char*)hidden + (size_t)b0 * H * dtype_size(hidden_dtype);
     a.hidden_dtype = hidden_dtype;
@@ -2124,11 +2136,11 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
       rc = by_mode([&](auto M) {
         return hv_gemm_ok ? launch_gemm<decltype(M)::value, 1, true>(a, s) : launch_gemm<decltype(M)::value, 1, false>(a, s);
       });
-    } else if (gemm3) {
+    } else if (g3) {
       rc = by_mode([&](auto M) {
         return hv_gemm_ok ? launch_gemm<decltype(M)::value, 3, true>(a, s) : launch_gemm<decltype(M)::value, 3, false>(a, s);
       });
-    } else if (gemv) {
+    } else if (gv) {
       rc = by_mode([&](auto M) { return dispatch_gemv<decltype(M)::value>(a, s); });
     } else if (hv) {
       rc = by_mode([&](auto M) { return dispatch_hv<decltype(M)::value>(a, s); });
