@@ -1921,7 +1921,7 @@ static constexpr int kGemm3MinBatch = 32, kGemm3MinBatchSample = 32;  // f32 act
 // to 64 rows in the narrow layout: ~94-98 us greedy, ~113-143 us sampled,
 // against 8-row streaming passes of ~88-100 us each) and for fp32 above 8
 // greedy, 16 sampled (~180 / ~190-218 us against passes of ~90 / ~110 us)
-static constexpr int kMix3MaxBatch = 96, kMix3MaxBatchSample = 96;
+static constexpr int kMix3MaxBatch = 128;  // f32 activations, [V, H]: 64-row narrow passes up to here
 static constexpr int kGemmHvMinBatch = 8, kGemmHvMinBatchSample = 8, kGemm3HvMinBatch = 8, kGemm3HvMinBatchSample = 16;
 
 
@@ -2063,16 +2063,17 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   // ~345-370 / ~475 us for 65-192 rows (padding waves idle), ~180 / ~215 us
   // up to 64 rows (narrow layout); it beats the 16-row tile passes (~85 / ~90
   // us each) from 33 rows greedy (B = 48 252 us in passes) and, sampling,
-  // from 33 rows (B = 40 215 vs 258 us; B = 32 197 vs 177); 65-96 rows mix the
-  // two (below)
-  // 65-96 rows, [V, H]: the narrow GEMM on the first 64 rows, then 16-row
-  // tile passes (or the streaming GEMV for a rest of <= 2 rows).  One box,
-  // V = 248k: greedy B = 72 / 80 / 96 267 / 261 / 345 us against 364-367 us
-  // for the 256-row kernel with idle padding waves; sampled B = 72 / 80 / 96
-  // 318 / 318 / 408 us against 434-436 us in tile passes and 474 us
-  // (from B = 104 the 256-row kernel is faster: 479 vs 495 us sampled)
-  const bool mix3 = gemm_ok && tile && !hv_gemm_ok && eff_dtype == NVJSEL_F32 && batch > 64 &&
-                    batch <= (mode == MODE_SAMPLE ? kMix3MaxBatchSample : kMix3MaxBatch);
+  // from 33 rows (B = 40 215 vs 258 us; B = 32 197 vs 177); 65-128 rows mix
+  // the two (below)
+  // 65-128 rows, [V, H]: passes of 64 rows through the narrow GEMM while
+  // more than 32 rows are left, then 16-row tile passes (or the streaming
+  // GEMV for a rest of <= 2 rows).  One box, V = 248k: greedy B = 72 / 80 /
+  // 96 / 97 267 / 261 / 345 / ~355 us against 364-367 us (B = 97: 407) for
+  // the 256-row kernel with idle padding waves, B = 104-128 the same ~364 us;
+  // sampled B = 72 / 80 / 96 / 104 / 128 318 / 318 / 408 / 443 / 449 us
+  // against 434-436 us in tile passes and 474-481 us; from B = 136 the
+  // 256-row kernel is faster (sampled 526 vs 543 us)
+  const bool mix3 = gemm_ok && tile && !hv_gemm_ok && eff_dtype == NVJSEL_F32 && batch > 64 && batch <= kMix3MaxBatch;
   const bool gemm3 = !mix3 && gemm_ok && eff_dtype == NVJSEL_F32 &&
                      (hv_gemm_ok ? batch > (mode == MODE_SAMPLE ? kGemm3HvMinBatchSample : kGemm3HvMinBatch)
                       : mode == MODE_SAMPLE ? batch > kGemm3MinBatchSample
@@ -2104,9 +2105,9 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   };
   for (int b0 = 0, nb = 0; b0 < batch; b0 += nb) {
     LmArgs a{};
-    const bool g3 = gemm3 || (mix3 && b0 == 0);
-    const bool gv = gemv || (mix3 && b0 > 0 && batch - b0 <= 2);
-    const int step = mix3 ? (b0 == 0 ? 64 : chunk) : (chunk > 0 ? chunk : batch);
+    const bool g3 = gemm3 || (mix3 && (b0 == 0 || batch - b0 > 32));
+    const bool gv = gemv || (mix3 && !g3 && batch - b0 <= 2);
+    const int step = mix3 ? (g3 ? 64 : chunk) : (chunk > 0 ? chunk : batch);
     nb = batch - b0 < step ? batch - b0 : step;
     a.W = weight;
     a.hidden = (const char*)hidden + (size_t)b0 * H * dtype_size(hidden_dtype);

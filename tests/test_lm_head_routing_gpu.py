@@ -5,9 +5,10 @@ The library picks among the streaming GEMV / [H, V] streaming kernel, the
 MFMA tile kernel (64-row passes for bf16, 16-row for three-term fp32
 activations), the blocked GEMM (the kernel that idles padding waves below
 193 rows, the full-batch kernel above, 256-row passes beyond 256) and the
-three-term blocked GEMM (for fp32 activations on [V, H] at 65-96 rows: its
-narrow layout on the first 64 rows, then 16-row tile passes and the GEMV for
-a rest of one or two rows), by layout, activation dtype, mode and batch.  Each
+three-term blocked GEMM (for fp32 activations on [V, H] at 65-128 rows:
+64-row passes of its narrow layout while more than 32 rows are left, then
+16-row tile passes and the GEMV for a rest of one or two rows), by layout,
+activation dtype, mode and batch.  Each
 case checks greedy ids (check_greedy: first index of the maximum of the
 rounded logits, rows within the fp32-summation flip accepted) or sampled ids
 (check_fused_sampled: the oracle's Gumbel-max scores) on a vocabulary that is
@@ -23,7 +24,7 @@ from tests.gpu_helpers import bf16_tensor, check_fused_sampled, check_greedy, en
 pytestmark = pytest.mark.gpu
 
 H, V = 1024, 4104
-BATCHES = [9, 17, 33, 57, 65, 66, 81, 96, 97, 129, 193, 257]
+BATCHES = [9, 17, 33, 57, 65, 66, 81, 96, 97, 128, 129, 193, 257]
 
 
 @pytest.fixture(scope="module")

@@ -35,7 +35,7 @@ def _inputs(rng, batch, H, V, hidden_dtype):
     (5, 1024, "bf16", "bf16"),   # tile kernel, fused
     (64, 1024, "f32", "bf16"),   # tile kernel, fused, f32 input
     (70, 1024, "bf16", "bf16"),  # blocked GEMM, prologue kernel
-    (82, 1024, "bf16", "f32"),   # fp32 operand, 65-96 rows: narrow GEMM + tile pass + GEMV, prologue kernel
+    (82, 1024, "bf16", "f32"),   # fp32 operand, 65-128 rows: narrow GEMM + tile pass + GEMV, prologue kernel
     (8, 1024, "bf16", "f32"),    # exact-split MFMA path, prologue kernel
     (4, 40, "f16", "f32"),       # generic path, prologue kernel
 ])
@@ -83,7 +83,7 @@ def test_prenorm_tile_unaligned_and_f16_hidden(batch, hidden_dtype, act_dtype):
 
 
 @pytest.mark.parametrize("batch,act_dtype", [(1, "bf16"), (2, "f32"), (16, "bf16"), (24, "bf16"), (64, "bf16"), (9, "f32"),
-                                             (90, "f32")])
+                                             (90, "f32"), (110, "f32")])
 def test_prenorm_fused_sample(batch, act_dtype):
     rng = np.random.default_rng(300 + batch)
     H, V = 1024, 8191
