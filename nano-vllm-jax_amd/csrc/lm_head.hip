@@ -2065,15 +2065,20 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   // us each) from 33 rows greedy (B = 48 252 us in passes) and, sampling,
   // from 33 rows (B = 40 215 vs 258 us; B = 32 197 vs 177); 65-128 rows mix
   // the two (below)
-  // 65-128 rows, [V, H]: passes of 64 rows through the narrow GEMM while
-  // more than 32 rows are left, then 16-row tile passes (or the streaming
-  // GEMV for a rest of <= 2 rows).  One box, V = 248k: greedy B = 72 / 80 /
+  // 65-128 rows: passes of 64 rows through the narrow GEMM while more rows
+  // are left than the GEMM's own threshold, then the passes of the
+  // layout's small-batch kernel ([H, V]: 8-row streaming passes; greedy B =
+  // 65 / 72 / 96-128 ~262 / ~278 / ~350 us, sampled ~302 / ~333 / ~409-434
+  // us, against ~376-396 / ~494-504 us in the 256-row kernel).  [V, H]:
+  // 16-row tile passes (or the streaming GEMV for a rest of <= 2 rows); one
+  // box, V = 248k: greedy B = 72 / 80 /
   // 96 / 97 267 / 261 / 345 / ~355 us against 364-367 us (B = 97: 407) for
   // the 256-row kernel with idle padding waves, B = 104-128 the same ~364 us;
   // sampled B = 72 / 80 / 96 / 104 / 128 318 / 318 / 408 / 443 / 449 us
   // against 434-436 us in tile passes and 474-481 us; from B = 136 the
   // 256-row kernel is faster (sampled 526 vs 543 us)
-  const bool mix3 = gemm_ok && tile && !hv_gemm_ok && eff_dtype == NVJSEL_F32 && batch > 64 && batch <= kMix3MaxBatch;
+  const bool mix3 = gemm_ok && (tile || hv_gemm_ok) && eff_dtype == NVJSEL_F32 && batch > 64 && batch <= kMix3MaxBatch;
+  const int mix_rest = hv_gemm_ok ? (mode == MODE_SAMPLE ? kGemm3HvMinBatchSample : kGemm3HvMinBatch) : kGemm3MinBatch;
   const bool gemm3 = !mix3 && gemm_ok && eff_dtype == NVJSEL_F32 &&
                      (hv_gemm_ok ? batch > (mode == MODE_SAMPLE ? kGemm3HvMinBatchSample : kGemm3HvMinBatch)
                       : mode == MODE_SAMPLE ? batch > kGemm3MinBatchSample
@@ -2105,8 +2110,8 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   };
   for (int b0 = 0, nb = 0; b0 < batch; b0 += nb) {
     LmArgs a{};
-    const bool g3 = gemm3 || (mix3 && (b0 == 0 || batch - b0 > 32));
-    const bool gv = gemv || (mix3 && !g3 && batch - b0 <= 2);
+    const bool g3 = gemm3 || (mix3 && (b0 == 0 || batch - b0 > mix_rest));
+    const bool gv = gemv || (mix3 && !g3 && !hv_gemm_ok && batch - b0 <= 2);
     const int step = mix3 ? (g3 ? 64 : chunk) : (chunk > 0 ? chunk : batch);
     nb = batch - b0 < step ? batch - b0 : step;
     a.W = weight;

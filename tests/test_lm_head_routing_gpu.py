@@ -5,10 +5,10 @@ The library picks among the streaming GEMV / [H, V] streaming kernel, the
 MFMA tile kernel (64-row passes for bf16, 16-row for three-term fp32
 activations), the blocked GEMM (the kernel that idles padding waves below
 193 rows, the full-batch kernel above, 256-row passes beyond 256) and the
-three-term blocked GEMM (for fp32 activations on [V, H] at 65-128 rows:
-64-row passes of its narrow layout while more than 32 rows are left, then
-16-row tile passes and the GEMV for a rest of one or two rows), by layout,
-activation dtype, mode and batch.  Each
+three-term blocked GEMM (for fp32 activations at 65-128 rows: 64-row passes
+of its narrow layout while more rows are left than its threshold, then
+[V, H] 16-row tile passes and the GEMV for a rest of one or two rows, [H, V]
+8-row streaming passes), by layout, activation dtype, mode and batch.  Each
 case checks greedy ids (check_greedy: first index of the maximum of the
 rounded logits, rows within the fp32-summation flip accepted) or sampled ids
 (check_fused_sampled: the oracle's Gumbel-max scores) on a vocabulary that is
