@@ -14,7 +14,9 @@ to exceed the 256 MB MALL (cold numbers, the headline); the warm numbers
 reuse one copy.  Each timed region is exactly ``--steps`` calls of the C ABI
 on torch's current stream, bracketed by device synchronisation; it is
 repeated ``--repeats`` times and the median and p90 per-step times are
-reported.
+reported.  Before its timed regions each config runs its ``--warmup`` steps
+and then ``--settle-ms`` of the same calls back to back, untimed, so that the
+timed regions see the device's sustained clock state.
 
 ``cpu_baseline`` times the numpy oracle on the host cores, on a bounded sample
 of each config's own inputs (kind "port": the build's restatement of the
@@ -48,6 +50,8 @@ def _parse():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--repeats", type=int, default=5, help="timed regions per config (median / p90)")
+    ap.add_argument("--settle-ms", type=float, default=30.0,
+                    help="untimed back-to-back calls per config after the warmup steps, in ms")
     ap.add_argument("--configs", default=ALL_CONFIGS)
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bounded CPU-baseline sample for C1")
     ap.add_argument("--cpu-seconds-other", type=float, default=3.0, help="... for each other config")
@@ -366,9 +370,21 @@ def time_region(torch, cfg, steps, ncopies):
     return start.elapsed_time(stop) / steps
 
 
-def time_config(torch, cfg, steps, warmup, repeats, ncopies):
+def time_config(torch, cfg, steps, warmup, repeats, ncopies, settle_s=0.0):
     for s in range(warmup):
         cfg.launch(s % ncopies)
+    # Then the same calls, untimed, until settle_s of back-to-back work has
+    # passed: the timed regions see the device's sustained clock state, not
+    # its ramp out of a lighter load (C4 on one box, windows of 50 calls:
+    # 125, 113, 105, 100, 98, then 93-96 us per call from ~25 ms on).
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    s = warmup
+    while time.perf_counter() - t0 < settle_s:
+        for _ in range(10):
+            cfg.launch(s % ncopies)
+            s += 1
+        torch.cuda.synchronize()
     ms = sorted(time_region(torch, cfg, steps, ncopies) for _ in range(repeats))
     med = ms[len(ms) // 2] if len(ms) % 2 else 0.5 * (ms[len(ms) // 2 - 1] + ms[len(ms) // 2])
     p90 = ms[min(len(ms) - 1, int(round(0.9 * (len(ms) - 1))))]
@@ -478,7 +494,8 @@ def main():
     cfgs = build_configs(torch, which, with_cpu=not args.no_cpu)
     per = {}
     for cfg in cfgs:
-        med, p90, all_ms = time_config(torch, cfg, args.steps, args.warmup, args.repeats, cfg.ncopies)
+        med, p90, all_ms = time_config(torch, cfg, args.steps, args.warmup, args.repeats, cfg.ncopies,
+                                       args.settle_ms * 1e-3)
         us = med * 1e3
         e = {
             "desc": cfg.desc,
@@ -492,7 +509,7 @@ def main():
             "dominant_kernel": cfg.kernel,
         }
         if not args.no_warm:
-            wmed, wp90, _ = time_config(torch, cfg, args.steps, args.warmup, args.repeats, 1)
+            wmed, wp90, _ = time_config(torch, cfg, args.steps, args.warmup, args.repeats, 1, args.settle_ms * 1e-3)
             e["us_per_step_warm"] = round(wmed * 1e3, 3)
             e["us_p90_warm"] = round(wp90 * 1e3, 3)
         per[cfg.name] = e
@@ -529,7 +546,9 @@ def main():
         "config": {"workload": "c1_greedy_lm_head_b1: greedy LM-head top-1, hidden [1,1024] bf16 x "
                                "W [248320,1024] bf16, fp32 accumulate, bf16-rounded logits",
                    "batch": 1, "vocab": V_FULL, "hidden": H_FULL, "repeats": args.repeats,
-                   "timing": "median over repeats of exactly `steps` calls; W alternates between 2 copies"},
+                   "timing": "median over repeats of exactly `steps` calls; W alternates between 2 copies; "
+                             "each config warmed by `warmup` steps plus `settle_ms` of untimed back-to-back calls",
+                   "settle_ms": args.settle_ms},
         "roofline": {"bound": "hbm", "kernel": "lm_head_gemv_kernel", "achieved": round(achieved / 1e9, 1),
                      "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
                      "traffic": committed_traffic()},
