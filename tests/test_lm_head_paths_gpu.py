@@ -247,12 +247,15 @@ def test_gemm_greedy_and_logits(B, H):
     assert torch.equal(ids, ids2)
 
 
-@pytest.mark.parametrize("B,H", [(33, 1024), (64, 1024), (65, 512), (200, 1024), (300, 1024), (32, 1024)])
+@pytest.mark.parametrize("B,H", [(33, 1024), (64, 1024), (65, 512), (81, 1024), (100, 1024), (200, 1024),
+                                 (300, 1024), (32, 1024)])
 def test_gemm_f32_activations(B, H):
     """fp32 activations (lm_head_decode_act_dtype fp32) above 32 rows: the
     blocked GEMM on three bf16 terms per value (the narrow layout up to 64
-    rows) -- one pass over W per 256 rows, greedy and logits -- against the
-    float64 dot (fp32 logits); 32 rows take two 16-row tile passes."""
+    rows; at H = 1024 and 65-128 rows 64-row narrow passes, then 16-row tile
+    passes and the GEMV for a last row: B = 81, 100) -- one pass over W per
+    256 rows, greedy and logits -- against the float64 dot (fp32 logits); 32
+    rows take two 16-row tile passes."""
     rng = np.random.default_rng(7700 + B + H)
     V = 9001
     W = bf16_tensor(rng.standard_normal((V, H)) * 0.05)
@@ -345,8 +348,8 @@ def test_gemm_hv_greedy_winner_in_last_columns():
 
 @pytest.mark.parametrize("B,act", [(130, torch.bfloat16), (100, torch.float32)])
 def test_gemm_hv_matches_vh_bitwise(B, act):
-    """Where both layouts run the blocked GEMM (bf16 above 64 rows, fp32
-    activations above 80 / 96), the [H, V] kernel multiplies the same products
+    """Where both layouts run the blocked GEMM (bf16 above 64 rows; fp32
+    activations at 100 rows: two narrow passes on either layout), the [H, V] kernel multiplies the same products
     in the same k order as the [V, H] one: logits bitwise equal, sampled ids
     equal."""
     rng = np.random.default_rng(9600 + B)
