@@ -167,3 +167,51 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2
     msg = json.loads(r.stdout.strip().splitlines()[-1])
     assert msg["n_gpus"] == 2 and "one GPU" in msg["error"]
+
+
+def test_bench_timed_regions_hold_exactly_steps_calls():
+    """bench.time_config: the warmup steps and the settle phase run untimed
+    before the timed regions, and each timed region holds exactly `steps`
+    calls between two device synchronisations (a stand-in device that only
+    records the call order)."""
+    import sys
+    import time
+
+    root = Path(__file__).resolve().parents[1]
+    sys.path.insert(0, str(root))
+    import bench
+
+    log = []
+
+    class Event:
+        def __init__(self, enable_timing=False):
+            self.t = None
+
+        def record(self):
+            log.append("event")
+            self.t = time.perf_counter()
+
+        def elapsed_time(self, other):
+            return (other.t - self.t) * 1e3
+
+    from types import SimpleNamespace
+
+    FakeTorch = SimpleNamespace(cuda=SimpleNamespace(Event=Event, synchronize=lambda: log.append("sync")))
+
+    class Cfg:
+        def launch(self, i):
+            log.append(("call", i))
+
+    med, p90, ms = bench.time_config(FakeTorch, Cfg(), steps=7, warmup=3, repeats=4, ncopies=2, settle_s=0.01)
+    assert len(ms) == 4 and med <= p90
+    first_event = log.index("event")
+    untimed = [e for e in log[:first_event] if e != "sync"]
+    assert len(untimed) >= 3 + 10  # the warmup steps, then at least one settle round of ten calls
+    assert [e[1] for e in untimed[:3]] == [0, 1, 0]
+    # the timed part: per region sync, event, exactly 7 calls, event, sync
+    timed = log[first_event - 1:]
+    for r in range(4):
+        region = timed[r * 11:(r + 1) * 11]
+        assert region[0] == "sync" and region[1] == "event" and region[9] == "event" and region[10] == "sync"
+        assert [e[1] for e in region[2:9]] == [s % 2 for s in range(7)]
+    assert len(timed) == 44
