@@ -437,7 +437,7 @@ lm_head_mfma_kernel(LmArgs a) {
 }
 
 // ------------------------------------------------------------------ streaming GEMV kernel
-// Small batch (B <= 2), weight [V,H] bf16 with H = KJ * 512.  Every load
+// Small batch (B <= 4), weight [V,H] bf16 with H = KJ * 512.  Every load
 // instruction of a wave reads 1 KB of W contiguous (64 lanes x 16 B), the
 // pattern that streams HBM at full rate: lane l holds k = 512 j + 8 l .. +7 of
 // each row.  A wave takes R consecutive rows per step (R * 2H bytes
@@ -1888,9 +1888,17 @@ static int dispatch_gemv(const LmArgs& a, hipStream_t s) {
     if (kj == 2) return launch_gemv<1, 2, MODE>(a, s);
     return launch_gemv<1, 4, MODE>(a, s);
   }
-  if (kj == 1) return launch_gemv<2, 1, MODE>(a, s);
-  if (kj == 2) return launch_gemv<2, 2, MODE>(a, s);
-  return launch_gemv<2, 4, MODE>(a, s);
+  if (MODE == MODE_SAMPLE || a.B <= 2) {
+    if (kj == 1) return launch_gemv<2, 1, MODE>(a, s);
+    if (kj == 2) return launch_gemv<2, 2, MODE>(a, s);
+    return launch_gemv<2, 4, MODE>(a, s);
+  }
+  if constexpr (MODE != MODE_SAMPLE) {  // 3-4 rows: greedy / logits only
+    if (kj == 1) return launch_gemv<4, 1, MODE>(a, s);
+    if (kj == 2) return launch_gemv<4, 2, MODE>(a, s);
+    return launch_gemv<4, 4, MODE>(a, s);
+  }
+  return NVJSEL_EINVAL;
 }
 
 template <int WT, int NSPLIT, int MODE>
@@ -2029,9 +2037,19 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   const bool f16_mfma = layout == NVJSEL_W_VH && weight_dtype == NVJSEL_F16 &&
                         eff_dtype == NVJSEL_F16 && (H % 32) == 0 && aligned;
   const int nsplit = (bf16_mfma && eff_dtype != NVJSEL_BF16) ? 3 : 1;
-  // streaming GEMV ([V, H] bf16): B <= 2, any activation (fp32 products on the VALU)
-  const bool gemv = layout == NVJSEL_W_VH && weight_dtype == NVJSEL_BF16 && aligned && batch <= 2 &&
-                    (H == 512 || H == 1024 || H == 2048);
+  // streaming GEMV ([V, H] bf16, any activation; fp32 products on the VALU):
+  // greedy / logits up to 2 rows, 4 for activations other than bf16 (fp32 B
+  // = 3 / 4 ~76 / ~78-80 us against ~84 in a tile pass; bf16 at 3-4 rows
+  // ~92-96 against ~77); sampling where the tile kernel cannot take the call,
+  // and for one row of non-bf16 activations (fp32 B = 1 ~82 vs ~84 us; bf16
+  // B = 1 / 2 77.5 / 77 us in a tile pass against 80 / 98.5 here, fp32 B = 2
+  // 83 vs 113)
+  const bool gemv_shape = layout == NVJSEL_W_VH && weight_dtype == NVJSEL_BF16 && aligned &&
+                          (H == 512 || H == 1024 || H == 2048);
+  const bool tile_shape = bf16_mfma && H == 1024 && (prenorm || (((uintptr_t)hidden) & 15) == 0);
+  const bool gemv = gemv_shape && (mode == MODE_SAMPLE
+                                       ? batch <= 2 && (!tile_shape || (batch == 1 && eff_dtype != NVJSEL_BF16))
+                                       : batch <= 2 || (batch <= 4 && eff_dtype != NVJSEL_BF16));
   // [H, V] bf16 streaming kernel, up to 8 rows per launch
   const bool hv = layout == NVJSEL_W_HV && weight_dtype == NVJSEL_BF16 && aligned && (V % 8) == 0 &&
                   hv_lds_bytes(batch < 8 ? batch : 8, H) + kStaticLdsSlack <= device_max_lds_per_block();
@@ -2046,7 +2064,7 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
     if (nsplit == 3 && tiles > 1) tiles = 1;
     chunk = tiles * 16;
   }
-  const bool tile = !gemv && bf16_mfma && H == 1024 && (prenorm || (((uintptr_t)hidden) & 15) == 0);
+  const bool tile = !gemv && tile_shape;
   // blocked GEMM: 64 < B, bf16 activations, one pass over W per 256 rows (greedy, logits and Gumbel sampling)
   // (sample mode packs vocabulary ids into 25 bits of its queue entries).
   // [H, V] weights (transposing LDS reads): from 9 rows (bf16), 25 (fp32);

@@ -1,7 +1,8 @@
 """GPU: every LM-head route at the batch sizes on both sides of its
 thresholds, against the oracle.
 
-The library picks among the streaming GEMV / [H, V] streaming kernel, the
+The library picks among the streaming GEMV (greedy / logits up to 2 rows, 4
+for fp32 activations; sampling one fp32 row), the [H, V] streaming kernel, the
 MFMA tile kernel (64-row passes for bf16, 16-row for three-term fp32
 activations), the blocked GEMM (the kernel that idles padding waves below
 193 rows, the full-batch kernel above, 256-row passes beyond 256) and the
@@ -24,7 +25,7 @@ from tests.gpu_helpers import bf16_tensor, check_fused_sampled, check_greedy, en
 pytestmark = pytest.mark.gpu
 
 H, V = 1024, 4104
-BATCHES = [9, 17, 33, 57, 65, 66, 81, 96, 97, 128, 129, 193, 257]
+BATCHES = [1, 2, 3, 4, 9, 17, 33, 57, 65, 66, 81, 96, 97, 128, 129, 193, 257]
 
 
 @pytest.fixture(scope="module")
