@@ -1928,9 +1928,10 @@ static constexpr int kGemm3MinBatch = 32, kGemm3MinBatchSample = 32;  // f32 act
 // [H, V] weights: the GEMM above 8 rows for bf16 activations (V = 248k, up
 // to 64 rows in the narrow layout: ~94-98 us greedy, ~113-143 us sampled,
 // against 8-row streaming passes of ~88-100 us each) and for fp32 above 8
-// greedy, 16 sampled (~180 / ~190-218 us against passes of ~90 / ~110 us)
-static constexpr int kMix3MaxBatch = 128;  // f32 activations, [V, H]: 64-row narrow passes up to here
-static constexpr int kGemmHvMinBatch = 8, kGemmHvMinBatchSample = 8, kGemm3HvMinBatch = 8, kGemm3HvMinBatchSample = 16;
+// (~168-180 / ~185-218 us against passes of ~97 / ~111 us: B = 12 sampled
+// 185 vs 206 us in two passes)
+static constexpr int kMix3MaxBatch = 128;  // f32 activations, 64-row narrow passes up to here
+static constexpr int kGemmHvMinBatch = 8, kGemmHvMinBatchSample = 8, kGemm3HvMinBatch = 8, kGemm3HvMinBatchSample = 8;
 
 
 // Final-RMSNorm prologue request (norm_w == nullptr: hidden is already normed).

@@ -372,10 +372,10 @@ def test_gemm_hv_matches_vh_bitwise(B, act):
 
 
 @pytest.mark.parametrize("B,act", [(12, torch.bfloat16), (20, torch.bfloat16), (130, torch.bfloat16),
-                                   (30, torch.float32), (64, torch.float32)])
+                                   (12, torch.float32), (30, torch.float32), (64, torch.float32)])
 def test_gemm_hv_sample(B, act):
-    """Fused Gumbel sampling through the [H, V] blocked GEMM (bf16 above 8
-    rows, fp32 activations above 24; the narrow layout up to 64 rows), greedy
+    """Fused Gumbel sampling through the [H, V] blocked GEMM (above 8 rows;
+    the narrow layout up to 64 rows), greedy
     rows beside temperature rows.
     Rows whose kernel id differs within the rounding-flip exemption are
     listed in the terminal summary."""
