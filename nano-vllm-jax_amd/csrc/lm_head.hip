@@ -1920,10 +1920,13 @@ static size_t lm_ws_small_bytes(int batch) {
   return batch <= 0 ? 0 : lm_ws_keys_bytes(batch) + 256;
 }
 // [V, H] bf16: the GEMM above 64 rows; where the tile kernel serves the shape
-// (H = 1024) above 128 rows (greedy / logits) and 192 (sampling) -- below,
-// its 64-row passes are faster (one box: B = 96 157 vs 168 us greedy, 192 vs
-// 244 us sampled; B = 160 greedy 236 vs 183 us; B = 192 sampled 304 vs 339 us)
+// (H = 1024) above 128 rows (greedy / logits) and, sampling, at 129-160 rows
+// and above 192 -- elsewhere its 64-row passes are faster (one box: B = 96
+// 157 vs 168 us greedy, 182 vs 245 us sampled; sampled B = 144 / 160 264 /
+// 270 us in the GEMM against 270-279 / 280-285 in three tile passes, B = 176
+// / 192 296-298 / 300 against 318 / 323)
 static constexpr int kGemmMinBatch = 64, kGemmMinBatchTile = 128, kGemmMinBatchTileSample = 192;
+static constexpr int kGemmBandSample = 160;  // sampling: the GEMM also at kGemmMinBatchTile < B <= this
 static constexpr int kGemm3MinBatch = 32, kGemm3MinBatchSample = 32;  // f32 activations (three-term GEMM)
 // [H, V] weights: the GEMM above 8 rows for bf16 activations (V = 248k, up
 // to 64 rows in the narrow layout: ~94-98 us greedy, ~113-143 us sampled,
@@ -2074,9 +2077,11 @@ static int lm_head_entry(int mode, const void* hidden, int hidden_dtype, const v
   const bool gemm_ok = (bf16_mfma || hv_gemm_ok) && (H % (2 * kGemmKC)) == 0 &&
                        (prenorm || (((uintptr_t)hidden) & 15) == 0) && (mode != MODE_SAMPLE || V < (1 << 25));
   const bool gemm = gemm_ok && eff_dtype == NVJSEL_BF16 &&
-                    batch > (hv_gemm_ok ? (mode == MODE_SAMPLE ? kGemmHvMinBatchSample : kGemmHvMinBatch)
-                             : !tile    ? kGemmMinBatch
-                                        : (mode == MODE_SAMPLE ? kGemmMinBatchTileSample : kGemmMinBatchTile));
+                    (batch > (hv_gemm_ok ? (mode == MODE_SAMPLE ? kGemmHvMinBatchSample : kGemmHvMinBatch)
+                              : !tile    ? kGemmMinBatch
+                                         : (mode == MODE_SAMPLE ? kGemmMinBatchTileSample : kGemmMinBatchTile)) ||
+                     (tile && !hv_gemm_ok && mode == MODE_SAMPLE && batch > kGemmMinBatchTile &&
+                      batch <= kGemmBandSample));
   // f32 activations: the same one-pass GEMM on three bf16 terms per value,
   // per 256-row pass at V = 248k ~460 us (greedy) / ~550-620 us (sampling),
   // ~345-370 / ~475 us for 65-192 rows (padding waves idle), ~180 / ~215 us

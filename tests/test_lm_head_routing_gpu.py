@@ -25,7 +25,7 @@ from tests.gpu_helpers import bf16_tensor, check_fused_sampled, check_greedy, en
 pytestmark = pytest.mark.gpu
 
 H, V = 1024, 4104
-BATCHES = [1, 2, 3, 4, 9, 17, 33, 57, 65, 66, 81, 96, 97, 128, 129, 193, 257]
+BATCHES = [1, 2, 3, 4, 9, 17, 33, 57, 65, 66, 81, 96, 97, 128, 129, 160, 161, 193, 257]
 
 
 @pytest.fixture(scope="module")
